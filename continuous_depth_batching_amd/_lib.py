@@ -1,0 +1,74 @@
+"""ctypes binding of ``libcdb_amd.so``, the C ABI declared in ``include/cdb_amd.h``.
+
+Loading fails loudly: there is no CPU or PyTorch fallback for any kernel. The
+library must have been built (``continuous_depth_batching_amd._build``) before
+the first call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int32, c_int64, c_void_p
+from functools import lru_cache
+
+from ._build import LIBRARY_PATH
+
+CDB_OK = 0
+CDB_ERRORS = {
+    -1: "a required pointer is null",
+    -2: "an extent or stride is out of range",
+    -3: "unsupported dtype/head_dim combination",
+    -4: "a HIP kernel launch failed",
+    -5: "a caller buffer is too small",
+}
+CDB_DTYPE_F32 = 0
+CDB_DTYPE_BF16 = 1
+
+_P = c_void_p
+_I32P = c_void_p
+
+# name -> (restype, argtypes); mirrors include/cdb_amd.h one to one.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "cdb_paged_decode_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "cdb_paged_decode_attention": (
+        c_int32,
+        [
+            _P, _P, _P, _P, _P,  # q, k_new, v_new, k_pool, v_pool
+            c_int64, c_int32, c_int64,  # layer_stride, num_cache_layers, pool_blocks
+            _I32P, c_int32,  # cache_layer, cache_layer0
+            _I32P, _I32P, c_int32,  # block_table, table_row, table_width
+            _I32P,  # seqlens
+            _P, _P, c_int32, c_int32,  # rope_cos, rope_sin, rope_style, max_positions
+            _P, _P,  # q_bias, k_bias
+            _P, _P, c_int64,  # out, workspace, workspace_bytes
+            c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
+            c_float, c_int32, _P,  # scale, dtype, stream
+        ],
+    ),
+}
+
+
+class CdbKernelError(RuntimeError):
+    """A C-ABI entry point returned an error code."""
+
+
+@lru_cache(maxsize=1)
+def lib() -> ctypes.CDLL:
+    """Load the kernel library once; raise ImportError when it has not been built."""
+
+    if not LIBRARY_PATH.exists():
+        raise ImportError(
+            f"{LIBRARY_PATH} is missing: build the HIP kernels first "
+            "(python -m continuous_depth_batching_amd._build)"
+        )
+    handle = ctypes.CDLL(str(LIBRARY_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
+
+
+def check(code: int, what: str) -> None:
+    if code != CDB_OK:
+        raise CdbKernelError(f"{what} failed with code {code}: {CDB_ERRORS.get(code, 'unknown error')}")

@@ -1,0 +1,162 @@
+// Device helpers shared by the CDB decode-step kernels (gfx950 / CDNA4).
+//
+// Storage types: activations and KV pages are either fp32 or bf16. bf16 is
+// carried as raw uint16_t bits; all arithmetic happens in fp32 and is rounded
+// back with round-to-nearest-even, which is what torch's bf16 ops do.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define CDB_DEVICE __device__ __forceinline__
+
+namespace cdb {
+
+constexpr int kWave = 64;
+
+struct bf16_t {
+  uint16_t bits;
+};
+
+CDB_DEVICE float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+CDB_DEVICE uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Round an fp32 value to the nearest bf16 and return it as fp32.
+CDB_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Element traits: load/store one scalar of the storage type as fp32.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static CDB_DEVICE float load(const float* p) { return *p; }
+  static CDB_DEVICE void store(float* p, float v) { *p = v; }
+  // Rounding applied after every elementwise op of a torch tensor of this dtype.
+  static CDB_DEVICE float round(float v) { return v; }
+};
+template <> struct Elem<bf16_t> {
+  static CDB_DEVICE float load(const bf16_t* p) { return bf16_to_f32(p->bits); }
+  static CDB_DEVICE void store(bf16_t* p, float v) { p->bits = f32_to_bf16(v); }
+  static CDB_DEVICE float round(float v) { return round_bf16(v); }
+};
+
+// Vector of N storage elements loaded with the widest aligned loads available.
+template <typename T, int N> struct Vec {
+  static constexpr int kBytes = N * (int)sizeof(T);
+  static_assert(kBytes % 4 == 0, "vector must be a whole number of dwords");
+  static constexpr int kWords = kBytes / 4;
+  uint32_t w[kWords];
+
+  CDB_DEVICE void load(const T* p) {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p);
+    if constexpr (kWords % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 4) {
+        uint4 v = *reinterpret_cast<const uint4*>(src + i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+      }
+    } else if constexpr (kWords % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 2) {
+        uint2 v = *reinterpret_cast<const uint2*>(src + i);
+        w[i] = v.x; w[i + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) w[i] = src[i];
+    }
+  }
+  CDB_DEVICE void store(T* p) const {
+    uint32_t* dst = reinterpret_cast<uint32_t*>(p);
+    if constexpr (kWords % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 4)
+        *reinterpret_cast<uint4*>(dst + i) = make_uint4(w[i], w[i + 1], w[i + 2], w[i + 3]);
+    } else if constexpr (kWords % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 2) *reinterpret_cast<uint2*>(dst + i) = make_uint2(w[i], w[i + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) dst[i] = w[i];
+    }
+  }
+  CDB_DEVICE float get(int i) const {
+    if constexpr (sizeof(T) == 4) {
+      return __uint_as_float(w[i]);
+    } else {
+      uint32_t word = w[i >> 1];
+      return (i & 1) ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16);
+    }
+  }
+  CDB_DEVICE void set(int i, float v) {
+    if constexpr (sizeof(T) == 4) {
+      w[i] = __float_as_uint(v);
+    } else {
+      uint32_t b = f32_to_bf16(v);
+      uint32_t& word = w[i >> 1];
+      word = (i & 1) ? ((word & 0x0000ffffu) | (b << 16)) : ((word & 0xffff0000u) | b);
+    }
+  }
+};
+
+// DPP row rotate by n within each 16-lane row. Used only for all-lane row reductions,
+// which give every lane of the row the same result whichever way the rotation runs.
+template <int kCtrl> CDB_DEVICE float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xf, 0xf, false));
+}
+constexpr int kRowRor1 = 0x121, kRowRor2 = 0x122, kRowRor4 = 0x124, kRowRor8 = 0x128;
+
+// Sum across the 16 lanes of a DPP row; every lane of the row receives the total.
+CDB_DEVICE float row16_sum(float v) {
+  v += dpp_f32<kRowRor8>(v);
+  v += dpp_f32<kRowRor4>(v);
+  v += dpp_f32<kRowRor2>(v);
+  v += dpp_f32<kRowRor1>(v);
+  return v;
+}
+CDB_DEVICE float row16_max(float v) {
+  v = fmaxf(v, dpp_f32<kRowRor8>(v));
+  v = fmaxf(v, dpp_f32<kRowRor4>(v));
+  v = fmaxf(v, dpp_f32<kRowRor2>(v));
+  v = fmaxf(v, dpp_f32<kRowRor1>(v));
+  return v;
+}
+
+CDB_DEVICE float shfl_xor_f32(float v, int mask) {
+  int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));
+}
+
+CDB_DEVICE float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor_f32(v, m);
+  return v;
+}
+CDB_DEVICE float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f32(v, m));
+  return v;
+}
+
+// Exact fp32 product and sum without contraction into an FMA, matching two
+// separately rounded torch elementwise ops.
+// The pragma clears the contract flag on these instructions, so the backend
+// cannot fuse a product into a following add after inlining.
+CDB_DEVICE float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+CDB_DEVICE float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+CDB_DEVICE float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a - b;
+}
+
+}  // namespace cdb

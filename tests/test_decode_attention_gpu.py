@@ -1,0 +1,126 @@
+"""HIP mixed-depth paged decode attention vs the oracle (through the C ABI).
+
+Tolerances (bf16 storage, fp32 accumulate): max |err| <= 2e-2 and mean |err|
+<= 2e-3 against the float64 oracle; fp32 storage: 2e-5 / 2e-6. The appended
+KV rows must be bit-identical to the oracle's (same rounding of the rotated
+key), and every other pool row must be untouched.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.paged_attention import paged_decode_attention as oracle_decode
+from tests.decode_cases import make_case
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": (2e-2, 2e-3), "f32": (2e-5, 2e-6)}
+TORCH_DTYPE = {"bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def run_hip(case, split_pages: int, use_table_row: bool = False):
+    from continuous_depth_batching_amd import ops
+
+    dev = torch.device("cuda")
+    dt = TORCH_DTYPE[case.dtype]
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    q, k, v = t(case.q).to(dt), t(case.k_new).to(dt), t(case.v_new).to(dt)
+    pool = t(case.kv_pool).to(dt).contiguous()
+    num_rows, num_heads, head_dim = case.q.shape
+    table = t(case.block_table)
+    table_row = None
+    if use_table_row:
+        # Reverse the table rows and index them through table_row.
+        table = torch.flip(table, dims=[0]).contiguous()
+        table_row = torch.arange(num_rows - 1, -1, -1, dtype=torch.int32, device=dev)
+    max_pos = int(case.seqlens.max()) + 1
+    ws = torch.empty(ops.decode_workspace_bytes(num_rows, num_heads, head_dim, max(max_pos, 1), case.block_size,
+                                                split_pages) // 4, dtype=torch.float32, device=dev)
+    cos = sin = None
+    if case.rope_style:
+        cos, sin = t(case.rope[0]), t(case.rope[1])
+    qb = t(case.q_bias).to(dt) if case.q_bias is not None else None
+    kb = t(case.k_bias).to(dt) if case.k_bias is not None else None
+    out = torch.ops.cdb.paged_decode_attention(
+        q, k, v, pool, t(case.cache_layer), 0, table, table_row, t(case.seqlens), cos, sin, case.rope_style,
+        qb, kb, ws, case.block_size, split_pages, case.scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), pool.float().cpu().numpy()
+
+
+def run_oracle(case):
+    pool = case.kv_pool.copy()
+    out = oracle_decode(case.q, case.k_new, case.v_new, pool, case.cache_layer, case.block_table, case.seqlens,
+                        case.block_size, case.scale, rope=case.rope, rope_style=case.rope_style,
+                        q_bias=case.q_bias, k_bias=case.k_bias, dtype=case.dtype)
+    return out, pool
+
+
+def check(case, split_pages: int, use_table_row: bool = False) -> None:
+    got, got_pool = run_hip(case, split_pages, use_table_row)
+    want, want_pool = run_oracle(case)
+    live = case.seqlens >= 0
+    err = np.abs(got[live] - want[live])
+    max_tol, mean_tol = TOL[case.dtype]
+    assert np.isfinite(got[live]).all()
+    assert err.max() <= max_tol, f"max err {err.max()}"
+    assert err.mean() <= mean_tol, f"mean err {err.mean()}"
+    assert np.all(got[~live] == 0.0)
+    np.testing.assert_array_equal(got_pool, want_pool)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("split_pages", [1, 4, 64])
+def test_ouro_shape_mixed_depth(dtype: str, split_pages: int) -> None:
+    case = make_case(seed=10, num_rows=24, num_heads=16, num_kv_heads=16, head_dim=128, max_context=700,
+                     rope_style=1, dtype=dtype, padding_rows=3)
+    check(case, split_pages)
+
+
+def test_table_row_indirection() -> None:
+    case = make_case(seed=11, num_rows=9, num_heads=16, num_kv_heads=16, head_dim=128, max_context=300,
+                     rope_style=1, dtype="bf16")
+    check(case, 2, use_table_row=True)
+
+
+@pytest.mark.parametrize("head_dim,rope_style,num_kv_heads", [(64, 1, 4), (96, 2, 5), (128, 0, 16)])
+def test_other_head_dims_and_rope_styles(head_dim: int, rope_style: int, num_kv_heads: int) -> None:
+    case = make_case(seed=12, num_rows=10, num_heads=num_kv_heads * (2 if head_dim == 64 else 1),
+                     num_kv_heads=num_kv_heads, head_dim=head_dim, max_context=400, rope_style=rope_style,
+                     dtype="bf16", qk_bias=rope_style == 2)
+    check(case, 4)
+
+
+def test_huginn_shape_55_heads() -> None:
+    case = make_case(seed=13, num_rows=5, num_heads=55, num_kv_heads=55, head_dim=96, max_context=200,
+                     rope_style=2, dtype="bf16", qk_bias=True)
+    check(case, 4)
+
+
+def test_single_token_rows_and_block_size_32() -> None:
+    case = make_case(seed=14, num_rows=7, num_heads=4, num_kv_heads=4, head_dim=64, max_context=1, rope_style=1,
+                     dtype="f32", block_size=32)
+    check(case, 1)
+
+
+def test_long_context_rows() -> None:
+    case = make_case(seed=15, num_rows=4, num_heads=16, num_kv_heads=16, head_dim=128, max_context=8192,
+                     min_context=6000, rope_style=1, dtype="bf16")
+    check(case, 16)
+
+
+def test_out_of_range_row_is_flagged_nan_and_writes_nothing() -> None:
+    case = make_case(seed=16, num_rows=3, num_heads=4, num_kv_heads=4, head_dim=64, max_context=40, rope_style=0,
+                     dtype="f32")
+    width = case.block_table.shape[1]
+    case.seqlens[1] = width * case.block_size  # one past the table
+    got, got_pool = run_hip(case, 1)
+    assert np.isnan(got[1]).all()
+    ok = np.array([True, False, True])
+    case.seqlens[1] = -1
+    want, want_pool = run_oracle(case)
+    np.testing.assert_allclose(got[ok], want[ok], atol=2e-5)
+    np.testing.assert_array_equal(got_pool, want_pool)

@@ -8,7 +8,7 @@ the first call.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int32, c_int64, c_void_p
+from ctypes import c_double, c_float, c_int32, c_int64, c_void_p
 from functools import lru_cache
 
 from ._build import LIBRARY_PATH
@@ -43,6 +43,43 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _P, _P, c_int64,  # out, workspace, workspace_bytes
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
             c_float, c_int32, _P,  # scale, dtype, stream
+        ],
+    ),
+    "cdb_rmsnorm_fused": (
+        c_int32, [_P, _P, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_float, c_float, c_int32, _P]),
+    "cdb_silu_mul": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
+    "cdb_copy_rows": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P]),
+    "cdb_argmax": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
+    "cdb_exit_gate": (
+        c_int32,
+        [
+            _P, _P, _P, _P, _P,  # hidden, prev, weight, bias, signal
+            _P, _P, _P, c_int64, _P,  # cdf, survival, pending, state_capacity, state_index
+            _P, _P, _P, c_int64,  # steps, synthetic_depth, exit_flags, rows
+            c_int32, c_int32, c_int32, c_int32, c_int32,  # width, kind, rule, delayed, round_hazard
+            c_int32, c_int32, c_double, c_int32, c_int32, _P,  # min/max steps, threshold, has_threshold, dtype, stream
+        ],
+    ),
+    "cdb_exit_gate_reset": (c_int32, [_P, _P, _P, c_int64, _P, c_int64, _P]),
+    "cdb_exit_kv_copy": (
+        c_int32, [_P, _P, c_int64, c_int64, c_int32, c_int32, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, _P]),
+    "cdb_rope_kv_write": (
+        c_int32,
+        [
+            _P, _P, _P, _P, _P, _P,  # q, k, v, q_out, k_pool, v_pool
+            c_int64, c_int32, _P, c_int64,  # layer_stride, layer, rows, pool_rows
+            _P, _P, _P, c_int32, c_int32,  # positions, rope_cos, rope_sin, rope_style, max_positions
+            _P, _P, c_int64,  # q_bias, k_bias, tokens
+            c_int32, c_int32, c_int32, c_int32, _P,  # H, Hkv, D, dtype, stream
+        ],
+    ),
+    "cdb_prefill_attention": (
+        c_int32,
+        [
+            _P, _P, _P, c_int64, c_int32, c_int32, c_int64,  # q, k_pool, v_pool, layer_stride, layer, layers, blocks
+            _P, _P, c_int32, _P, _P, c_int32,  # block_table, table_row, width, cu_q, past, num_seqs
+            _P, _P, c_int32, _P,  # tile_seq, tile_q0, num_tiles, out
+            c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P,  # H, Hkv, D, block_size, scale, dtype, stream
         ],
     ),
 }

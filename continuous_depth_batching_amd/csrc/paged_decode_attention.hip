@@ -42,7 +42,7 @@ struct DecodeParams {
   const int32_t* block_table;   // [num_table_rows, table_width]
   const int32_t* table_row;     // [B] or null (row b uses table row b)
   const int32_t* seqlens;       // [B]: position of the new token; < 0 marks a padding row
-  const int32_t* cache_layer;   // [B] or null (every row uses cache_layer0)
+  const int32_t* cache_layer;   // [B] per-row offset added to cache_layer0, or null
   const float* rope_cos;        // [max_positions, D/2] or null
   const float* rope_sin;
   const void* q_bias;           // [H, D] or null, added to q before rotation
@@ -75,7 +75,7 @@ CDB_DEVICE bool row_valid(const DecodeParams& P, int b, int p) {
   if (p < 0) return false;
   if ((int64_t)p >= ((int64_t)P.table_width << P.block_size_log2)) return false;
   if (P.rope_cos != nullptr && p >= P.max_positions) return false;
-  const int layer = P.cache_layer ? P.cache_layer[b] : P.cache_layer0;
+  const int layer = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
   return layer >= 0 && layer < P.num_cache_layers;
 }
 
@@ -218,7 +218,7 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
     const int nsplit = split_prefix[b + 1] - split_prefix[b];
     const int p = P.seqlens[b];
     const int kvh = h / kv_group;
-    const int layer = P.cache_layer ? P.cache_layer[b] : P.cache_layer0;
+    const int layer = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
     T* k_base = static_cast<T*>(P.k_pool) + (int64_t)layer * P.layer_stride;
     T* v_base = static_cast<T*>(P.v_pool) + (int64_t)layer * P.layer_stride;
     const int32_t* table = P.block_table + (int64_t)(P.table_row ? P.table_row[b] : b) * P.table_width;

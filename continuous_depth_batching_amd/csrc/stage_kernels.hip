@@ -260,6 +260,7 @@ struct GateParams {
   const int32_t* synthetic;     // [B] or null
   uint8_t* exit_flags;          // [B]
   int64_t rows;
+  int64_t state_capacity;
   int32_t width;
   int32_t kind;            // 0 hazard, 1 latent difference
   int32_t rule;            // 0 cumulative hazard, 1 direct threshold
@@ -312,7 +313,7 @@ __global__ void __launch_bounds__(kThreads) exit_gate_kernel(GateParams P) {
   }
   Elem<T>::store(static_cast<T*>(P.signal) + row, signal);
   const int64_t si = P.state_index[row];
-  if (si < 0) {
+  if (si < 0 || si >= P.state_capacity) {
     P.exit_flags[row] = 0;
     return;
   }
@@ -355,11 +356,11 @@ __global__ void __launch_bounds__(kThreads) exit_gate_kernel(GateParams P) {
 
 // Reset the policy state of fresh tokens (cdb/exit_policy.py:43-48).
 __global__ void gate_state_reset_kernel(double* cdf, double* survival, float* pending, const int64_t* index,
-                                        int64_t n) {
+                                        int64_t n, int64_t capacity) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t s = index[i];
-  if (s < 0) return;
+  if (s < 0 || s >= capacity) return;
   cdf[s] = 0.0;
   survival[s] = 1.0;
   pending[s] = __builtin_nanf("");
@@ -638,7 +639,7 @@ int cdb_exit_gate(const void* hidden, const void* prev, const void* weight, cons
       max_steps <= 0 || state_capacity <= 0)
     return CDB_ERR_SHAPE;
   GateParams P{hidden, prev, weight, bias, signal, cdf, survival, pending, state_index, steps, synthetic_depth,
-               exit_flags, rows, width, kind, rule, delayed, round_hazard, min_steps, max_steps, threshold,
+               exit_flags, rows, state_capacity, width, kind, rule, delayed, round_hazard, min_steps, max_steps, threshold,
                has_threshold};
   if (dtype == CDB_DTYPE_F32) {
     if (width % 4) return CDB_ERR_SHAPE;
@@ -652,13 +653,13 @@ int cdb_exit_gate(const void* hidden, const void* prev, const void* weight, cons
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 
-int cdb_exit_gate_reset(double* cdf, double* survival, float* pending, const int64_t* index, int64_t n,
-                        hipStream_t stream) {
+int cdb_exit_gate_reset(double* cdf, double* survival, float* pending, int64_t state_capacity,
+                        const int64_t* index, int64_t n, hipStream_t stream) {
   if (n == 0) return CDB_OK;
   if (!cdf || !survival || !pending || !index) return CDB_ERR_NULL;
   if (n < 0) return CDB_ERR_SHAPE;
   hipLaunchKernelGGL(gate_state_reset_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream, cdf, survival, pending,
-                     index, n);
+                     index, n, state_capacity);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 

@@ -218,3 +218,295 @@ def default_split_pages(num_rows: int, block_size: int) -> int:
 
 def softmax_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
+
+
+# ---------------------------------------------------------------------------
+# Row-wise stage kernels.
+# ---------------------------------------------------------------------------
+
+NORM_PLAIN, NORM_OURO_SANDWICH, NORM_HUGINN_SANDWICH = 0, 1, 2
+
+
+def rmsnorm_fused_raw(x: torch.Tensor, residual: torch.Tensor | None, w_a: torch.Tensor, w_b: torch.Tensor | None,
+                      out_h: torch.Tensor, out_y: torch.Tensor | None, mode: int, eps_a: float, eps_b: float) -> None:
+    """Launch ``cdb_rmsnorm_fused`` on 2-D contiguous row tensors (no allocation)."""
+
+    rows, width = x.shape[0], x.shape[-1]
+    for name, t in (("residual", residual), ("out_h", out_h), ("out_y", out_y)):
+        if t is not None and (t.shape != x.shape or t.dtype != x.dtype):
+            raise ValueError(f"{name} must match x")
+    for name, w in (("w_a", w_a), ("w_b", w_b)):
+        if w is not None and (w.shape != (width,) or w.dtype != x.dtype):
+            raise ValueError(f"{name} must be a [{width}] vector of x's dtype")
+    _require_cuda(x, residual, w_a, w_b, out_h, out_y)
+    _require_contiguous(x=x, residual=residual, w_a=w_a, w_b=w_b, out_h=out_h, out_y=out_y)
+    code = _lib.lib().cdb_rmsnorm_fused(
+        x.data_ptr(), _ptr(residual), w_a.data_ptr(), _ptr(w_b), out_h.data_ptr(), _ptr(out_y),
+        rows, width, mode, eps_a, eps_b, dtype_code(x.dtype), _stream())
+    _lib.check(code, "cdb_rmsnorm_fused")
+
+
+@torch.library.custom_op("cdb::rmsnorm", mutates_args=(), device_types="cuda")
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm as OuroRMSNorm / HuginnRMSNorm computes it, over the last dimension."""
+
+    x2 = x.reshape(-1, x.shape[-1])
+    out = torch.empty_like(x2)
+    rmsnorm_fused_raw(x2, None, weight, None, out, None, NORM_PLAIN, eps, eps)
+    return out.view_as(x)
+
+
+@rmsnorm.register_fake
+def _(x, weight, eps):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("cdb::residual_rmsnorm", mutates_args=(), device_types="cuda")
+def residual_rmsnorm(x: torch.Tensor, residual: torch.Tensor, w_a: torch.Tensor, w_b: torch.Tensor, eps_a: float,
+                     eps_b: float, mode: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Sandwich-norm residual step: returns (h, norm_b(h)); see ``cdb_rmsnorm_fused`` for ``mode``."""
+
+    x2 = x.reshape(-1, x.shape[-1])
+    r2 = residual.reshape(-1, x.shape[-1])
+    h = torch.empty_like(x2)
+    y = torch.empty_like(x2)
+    rmsnorm_fused_raw(x2, r2, w_a, w_b, h, y, mode, eps_a, eps_b)
+    return h.view_as(x), y.view_as(x)
+
+
+@residual_rmsnorm.register_fake
+def _(x, residual, w_a, w_b, eps_a, eps_b, mode):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
+def silu_mul_raw(gate_up: torch.Tensor, out: torch.Tensor) -> None:
+    rows, width = out.shape[0], out.shape[-1]
+    if gate_up.shape != (rows, 2 * width) or gate_up.dtype != out.dtype:
+        raise ValueError("gate_up must be [rows, 2 * width] of out's dtype")
+    _require_cuda(gate_up, out)
+    _require_contiguous(gate_up=gate_up, out=out)
+    _lib.check(_lib.lib().cdb_silu_mul(gate_up.data_ptr(), out.data_ptr(), rows, width, dtype_code(out.dtype),
+                                       _stream()), "cdb_silu_mul")
+
+
+@torch.library.custom_op("cdb::silu_mul", mutates_args=(), device_types="cuda")
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up for gate_up = [gate | up] along the last dimension."""
+
+    g2 = gate_up.reshape(-1, gate_up.shape[-1])
+    out = torch.empty((g2.shape[0], g2.shape[1] // 2), dtype=gate_up.dtype, device=gate_up.device)
+    silu_mul_raw(g2, out)
+    return out.view(*gate_up.shape[:-1], gate_up.shape[-1] // 2)
+
+
+@silu_mul.register_fake
+def _(gate_up):
+    return gate_up.new_empty((*gate_up.shape[:-1], gate_up.shape[-1] // 2))
+
+
+def copy_rows_raw(src: torch.Tensor, src_index: torch.Tensor | None, dst: torch.Tensor,
+                  dst_index: torch.Tensor | None, rows: int) -> None:
+    """dst[dst_index[i]] = src[src_index[i]] over whole rows of the first dimension (no allocation)."""
+
+    if src.dtype != dst.dtype or src.shape[1:] != dst.shape[1:]:
+        raise ValueError("src and dst rows must have the same shape and dtype")
+    for name, idx in (("src_index", src_index), ("dst_index", dst_index)):
+        if idx is not None and (idx.dtype != torch.int64 or idx.numel() < rows):
+            raise ValueError(f"{name} must be int64 with at least {rows} entries")
+    if src_index is None and src.shape[0] < rows or dst_index is None and dst.shape[0] < rows:
+        raise ValueError("identity index needs at least `rows` rows")
+    _require_cuda(src, dst, src_index, dst_index)
+    _require_contiguous(src=src, dst=dst, src_index=src_index, dst_index=dst_index)
+    row_bytes = src[0].numel() * src.element_size() if src.shape[0] else 0
+    _lib.check(_lib.lib().cdb_copy_rows(src.data_ptr(), _ptr(src_index), src.shape[0], dst.data_ptr(),
+                                        _ptr(dst_index), dst.shape[0], rows, row_bytes, _stream()),
+               "cdb_copy_rows")
+
+
+@torch.library.custom_op("cdb::gather_rows", mutates_args=(), device_types="cuda")
+def gather_rows(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """src[index] along dim 0; negative indices give zero rows."""
+
+    out = src.new_empty((index.numel(), *src.shape[1:]))
+    copy_rows_raw(src, index.contiguous(), out, None, index.numel())
+    return out
+
+
+@gather_rows.register_fake
+def _(src, index):
+    return src.new_empty((index.numel(), *src.shape[1:]))
+
+
+@torch.library.custom_op("cdb::scatter_rows_", mutates_args=("dst",), device_types="cuda")
+def scatter_rows_(dst: torch.Tensor, index: torch.Tensor, src: torch.Tensor) -> None:
+    """dst[index[i]] = src[i] along dim 0; negative indices skip the row."""
+
+    copy_rows_raw(src, None, dst, index.contiguous(), index.numel())
+
+
+def argmax_raw(logits: torch.Tensor, out: torch.Tensor) -> None:
+    rows, vocab = logits.shape
+    if out.dtype != torch.int64 or out.numel() < rows:
+        raise ValueError("out must be int64 with a slot per row")
+    _require_cuda(logits, out)
+    _require_contiguous(logits=logits, out=out)
+    _lib.check(_lib.lib().cdb_argmax(logits.data_ptr(), out.data_ptr(), rows, vocab, dtype_code(logits.dtype),
+                                     _stream()), "cdb_argmax")
+
+
+@torch.library.custom_op("cdb::argmax", mutates_args=(), device_types="cuda")
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy token per row of a [rows, vocab] logits matrix (first index of the max)."""
+
+    l2 = logits.reshape(-1, logits.shape[-1])
+    out = torch.empty((l2.shape[0],), dtype=torch.int64, device=logits.device)
+    argmax_raw(l2, out)
+    return out.view(logits.shape[:-1])
+
+
+@argmax.register_fake
+def _(logits):
+    return logits.new_empty(logits.shape[:-1], dtype=torch.int64)
+
+
+@dataclass
+class GateState:
+    """Device-resident exit-policy state, one entry per hidden-bank slot."""
+
+    cdf: torch.Tensor        # float64 [capacity]
+    survival: torch.Tensor   # float64 [capacity]
+    pending: torch.Tensor    # float32 [capacity], NaN = no pending signal
+
+    @classmethod
+    def allocate(cls, capacity: int, device: torch.device) -> "GateState":
+        return cls(
+            cdf=torch.zeros(capacity, dtype=torch.float64, device=device),
+            survival=torch.ones(capacity, dtype=torch.float64, device=device),
+            pending=torch.full((capacity,), float("nan"), dtype=torch.float32, device=device),
+        )
+
+    @property
+    def capacity(self) -> int:
+        return self.cdf.numel()
+
+    def reset(self, index: torch.Tensor, n: int | None = None) -> None:
+        n = index.numel() if n is None else n
+        _lib.check(_lib.lib().cdb_exit_gate_reset(self.cdf.data_ptr(), self.survival.data_ptr(),
+                                                  self.pending.data_ptr(), self.capacity, index.data_ptr(), n,
+                                                  _stream()), "cdb_exit_gate_reset")
+
+
+GATE_HAZARD, GATE_LATENT_DIFF = 0, 1
+RULE_CUMULATIVE_HAZARD, RULE_DIRECT_THRESHOLD = 0, 1
+
+
+def exit_gate_raw(hidden: torch.Tensor, prev: torch.Tensor | None, weight: torch.Tensor | None,
+                  bias: torch.Tensor | None, signal: torch.Tensor, state: GateState, state_index: torch.Tensor,
+                  steps: torch.Tensor, synthetic_depth: torch.Tensor | None, exit_flags: torch.Tensor, rows: int,
+                  *, kind: int, rule: int, delayed: bool, round_hazard: bool, min_steps: int, max_steps: int,
+                  threshold: float | None) -> None:
+    """Launch ``cdb_exit_gate`` for the first ``rows`` rows (no allocation)."""
+
+    width = hidden.shape[-1]
+    if hidden.dim() != 2 or hidden.shape[0] < rows:
+        raise ValueError("hidden must be [>= rows, width]")
+    if kind == GATE_HAZARD and (weight is None or weight.numel() != width):
+        raise ValueError("the hazard gate needs a [width] weight")
+    if kind == GATE_LATENT_DIFF and (prev is None or prev.shape != hidden.shape):
+        raise ValueError("the latent-difference gate needs prev shaped like hidden")
+    if state_index.dtype != torch.int64 or steps.dtype != torch.int32 or exit_flags.dtype != torch.uint8:
+        raise TypeError("state_index int64, steps int32, exit_flags uint8 expected")
+    if synthetic_depth is not None and synthetic_depth.dtype != torch.int32:
+        raise TypeError("synthetic_depth must be int32")
+    for t in (signal, state_index, steps, exit_flags, synthetic_depth):
+        if t is not None and t.numel() < rows:
+            raise ValueError("per-row buffers need at least `rows` entries")
+    _require_cuda(hidden, prev, weight, bias, signal, state_index, steps, synthetic_depth, exit_flags)
+    code = _lib.lib().cdb_exit_gate(
+        hidden.data_ptr(), _ptr(prev), _ptr(weight), _ptr(bias), signal.data_ptr(),
+        state.cdf.data_ptr(), state.survival.data_ptr(), state.pending.data_ptr(), state.capacity,
+        state_index.data_ptr(), steps.data_ptr(), _ptr(synthetic_depth), exit_flags.data_ptr(), rows,
+        width, kind, rule, int(delayed), int(round_hazard), min_steps, max_steps,
+        0.0 if threshold is None else float(threshold), int(threshold is not None), dtype_code(hidden.dtype),
+        _stream())
+    _lib.check(code, "cdb_exit_gate")
+
+
+def exit_kv_copy_raw(view: KVPoolView, rows: torch.Tensor, exit_slot: torch.Tensor, n: int, *, layer_base: int,
+                     core_layers: int, num_slots: int) -> None:
+    """Copy each exiting token's exit-slot KV into its deeper slots (copy-on-exit layout)."""
+
+    pool = view.pool
+    if rows.dtype != torch.int64 or exit_slot.dtype != torch.int32:
+        raise TypeError("rows int64 and exit_slot int32 expected")
+    if layer_base + num_slots * core_layers > view.num_cache_layers:
+        raise ValueError("slot layout exceeds the pool's cache layers")
+    _require_cuda(pool, rows, exit_slot)
+    code = _lib.lib().cdb_exit_kv_copy(view.k_ptr, view.v_ptr, view.layer_stride, view.pool_rows, pool.shape[3],
+                                       pool.shape[4], rows.data_ptr(), exit_slot.data_ptr(), n, layer_base,
+                                       core_layers, num_slots, dtype_code(pool.dtype), _stream())
+    _lib.check(code, "cdb_exit_kv_copy")
+
+
+def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor, view: KVPoolView,
+                      layer: int, rows: torch.Tensor, positions: torch.Tensor, rope_cos: torch.Tensor | None,
+                      rope_sin: torch.Tensor | None, rope_style: int, q_bias: torch.Tensor | None,
+                      k_bias: torch.Tensor | None) -> None:
+    """Rotate q/k of T tokens, write k/v to pool rows of cache layer ``layer`` (no allocation)."""
+
+    tokens, num_heads, head_dim = q.shape
+    num_kv_heads = k.shape[1]
+    if k.shape != (tokens, num_kv_heads, head_dim) or v.shape != k.shape or q_out.shape != q.shape:
+        raise ValueError("q/k/v/q_out shapes disagree")
+    if rows.dtype != torch.int64 or positions.dtype != torch.int32 or rows.numel() < tokens:
+        raise TypeError("rows int64 and positions int32 with a slot per token expected")
+    if not 0 <= layer < view.num_cache_layers:
+        raise ValueError("layer out of range")
+    _require_cuda(q, k, v, q_out, rows, positions, rope_cos, rope_sin)
+    _require_contiguous(q=q, k=k, v=v, q_out=q_out, rows=rows, positions=positions)
+    code = _lib.lib().cdb_rope_kv_write(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q_out.data_ptr(), view.k_ptr, view.v_ptr, view.layer_stride,
+        layer, rows.data_ptr(), view.pool_rows, positions.data_ptr(), _ptr(rope_cos), _ptr(rope_sin), rope_style,
+        0 if rope_cos is None else rope_cos.shape[0], _ptr(q_bias), _ptr(k_bias), tokens, num_heads,
+        num_kv_heads, head_dim, dtype_code(q.dtype), _stream())
+    _lib.check(code, "cdb_rope_kv_write")
+
+
+PREFILL_TILE = 64
+
+
+def prefill_tiles(query_lens: "list[int] | np.ndarray") -> tuple["np.ndarray", "np.ndarray"]:
+    """Tile -> (sequence, first query) arrays for cdb_prefill_attention (64 queries per tile)."""
+
+    import numpy as np
+
+    lens = np.asarray(query_lens, dtype=np.int64)
+    counts = (lens + PREFILL_TILE - 1) // PREFILL_TILE
+    seq = np.repeat(np.arange(lens.size, dtype=np.int32), counts)
+    starts = np.concatenate([[0], np.cumsum(counts)[:-1]]) if lens.size else np.zeros(0, np.int64)
+    q0 = (np.arange(int(counts.sum())) - np.repeat(starts, counts)) * PREFILL_TILE
+    return seq.astype(np.int32), q0.astype(np.int32)
+
+
+def prefill_attention_raw(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor,
+                          table_row: torch.Tensor, cu_q: torch.Tensor, past: torch.Tensor, tile_seq: torch.Tensor,
+                          tile_q0: torch.Tensor, out: torch.Tensor, scale: float) -> None:
+    """Launch ``cdb_prefill_attention`` (no allocation); all index tensors int32 on the GPU."""
+
+    tokens, num_heads, head_dim = q.shape
+    pool = view.pool
+    if out.shape != q.shape or out.dtype != q.dtype or pool.dtype != q.dtype:
+        raise ValueError("out/pool must match q")
+    num_seqs = past.numel()
+    if cu_q.numel() != num_seqs + 1 or table_row.numel() < num_seqs or tile_seq.numel() != tile_q0.numel():
+        raise ValueError("inconsistent prefill metadata")
+    _require_int32(block_table=block_table, table_row=table_row, cu_q=cu_q, past=past, tile_seq=tile_seq,
+                   tile_q0=tile_q0)
+    _require_cuda(q, pool, block_table, table_row, cu_q, past, tile_seq, tile_q0, out)
+    _require_contiguous(q=q, out=out, block_table=block_table)
+    code = _lib.lib().cdb_prefill_attention(
+        q.data_ptr(), view.k_ptr, view.v_ptr, view.layer_stride, layer, view.num_cache_layers, view.pool_blocks,
+        block_table.data_ptr(), table_row.data_ptr(), block_table.shape[1], cu_q.data_ptr(), past.data_ptr(),
+        num_seqs, tile_seq.data_ptr(), tile_q0.data_ptr(), tile_seq.numel(), out.data_ptr(), num_heads,
+        pool.shape[3], head_dim, view.block_size, scale, dtype_code(q.dtype), _stream())
+    _lib.check(code, "cdb_prefill_attention")

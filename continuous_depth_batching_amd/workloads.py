@@ -1,0 +1,141 @@
+"""Seeded synthetic workloads for the CDB decode step.
+
+* ``decode_attention_microbench``: the kernel-only mixed-depth paged decode
+  attention case -- bf16 q [B, H, D]; KV pages of 16 tokens in a pool holding
+  every row's pages in each of ``num_slots`` loop-slot cache layers; per-row
+  context lengths uniform in [ctx_min, ctx_max]; per-row loop step uniform in
+  {0..num_slots-1}; block tables drawn from a seeded random permutation of the
+  page pool; K/V values N(0, 1).
+* ``lognormal_requests`` / ``categorical_exit_trace`` / ``poisson_exit_trace``:
+  request length distributions and per-token replayed exit depths for the
+  end-to-end engine runs. Exit traces are 0-based recurrent steps, one per
+  staged decode token (``max_new_tokens - 1`` entries per request), the
+  format ``generate_batch(exit_depths=...)`` takes
+  (continuous_depth_batching/continuous_api.py:395-399).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass
+class DecodeAttentionCase:
+    q: torch.Tensor            # [B, H, D]
+    k_new: torch.Tensor        # [B, Hkv, D]
+    v_new: torch.Tensor
+    kv_pool: torch.Tensor      # [slots, 2, rows, Hkv, D]
+    slot_offset: torch.Tensor  # [B] int32 cache-layer offset (the row's loop slot)
+    block_table: torch.Tensor  # [B, W] int32
+    seqlens: torch.Tensor      # [B] int32 position of the new token
+    rope_cos: torch.Tensor     # [max_pos, D/2] float32
+    rope_sin: torch.Tensor
+    block_size: int
+    contexts: np.ndarray       # [B] tokens attended per row (position + 1)
+
+    def algorithmic_bytes(self) -> int:
+        """HBM bytes one launch must move: K/V of every attended token, q, out,
+        the appended K/V, block-table entries and positions."""
+
+        num_rows, num_heads, head_dim = self.q.shape
+        num_kv_heads = self.k_new.shape[1]
+        elem = self.q.element_size()
+        kv = int(self.contexts.sum()) * num_kv_heads * head_dim * elem * 2
+        q_out = 2 * num_rows * num_heads * head_dim * elem
+        appended = 2 * num_rows * num_kv_heads * head_dim * elem
+        tables = int(((self.contexts + self.block_size - 1) // self.block_size).sum()) * 4
+        return kv + q_out + appended + tables + 4 * num_rows
+
+
+def rope_tables_torch(head_dim: int, theta: float, max_positions: int, dtype: torch.dtype,
+                      device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """Split-half RoPE tables as the reference's rotary module builds them
+    (ouro/modeling_ouro.py:544-573): fp32 angles, cos/sin cast to the model dtype,
+    returned as fp32 [max_positions, D/2]."""
+
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).to(device=device,
+                                                                                  dtype=torch.float) / head_dim))
+    positions = torch.arange(max_positions, device=device, dtype=torch.float32)
+    freqs = positions[:, None] * inv_freq[None, :]
+    return freqs.cos().to(dtype).float().contiguous(), freqs.sin().to(dtype).float().contiguous()
+
+
+def decode_attention_microbench(
+    *,
+    num_rows: int = 1024,
+    num_heads: int = 16,
+    head_dim: int = 128,
+    ctx_min: int = 128,
+    ctx_max: int = 8192,
+    num_slots: int = 4,
+    block_size: int = 16,
+    seed: int = 0,
+    dtype: torch.dtype = torch.bfloat16,
+    device: torch.device | str = "cuda",
+) -> DecodeAttentionCase:
+    device = torch.device(device)
+    rng = np.random.default_rng(seed)
+    contexts = rng.integers(ctx_min, ctx_max + 1, size=num_rows).astype(np.int64)
+    slots = rng.integers(0, num_slots, size=num_rows).astype(np.int32)
+    pages = (contexts + block_size - 1) // block_size
+    total_pages = int(pages.sum())
+    perm = rng.permutation(total_pages).astype(np.int32)
+    width = int(pages.max())
+    table = np.full((num_rows, width), -1, dtype=np.int32)
+    offsets = np.concatenate([[0], np.cumsum(pages)])
+    for b in range(num_rows):
+        table[b, : pages[b]] = perm[offsets[b]: offsets[b + 1]]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    rows = total_pages * block_size
+    pool = torch.empty((num_slots, 2, rows, num_heads, head_dim), dtype=dtype, device=device)
+    for s in range(num_slots):
+        for kv in range(2):
+            pool[s, kv].normal_(generator=gen)
+    q = torch.randn((num_rows, num_heads, head_dim), generator=gen, device=device).to(dtype)
+    k_new = torch.randn((num_rows, num_heads, head_dim), generator=gen, device=device).to(dtype)
+    v_new = torch.randn((num_rows, num_heads, head_dim), generator=gen, device=device).to(dtype)
+    cos, sin = rope_tables_torch(head_dim, 10000.0, int(contexts.max()), dtype, device)
+    return DecodeAttentionCase(
+        q=q, k_new=k_new, v_new=v_new, kv_pool=pool,
+        slot_offset=torch.from_numpy(slots).to(device),
+        block_table=torch.from_numpy(table).to(device),
+        seqlens=torch.from_numpy((contexts - 1).astype(np.int32)).to(device),
+        rope_cos=cos, rope_sin=sin, block_size=block_size, contexts=contexts,
+    )
+
+
+def lognormal_lengths(rng: np.random.Generator, n: int, mu: float, sigma: float, lo: int, hi: int) -> np.ndarray:
+    return np.clip(np.rint(rng.lognormal(mu, sigma, size=n)), lo, hi).astype(np.int64)
+
+
+def lognormal_requests(*, num_requests: int, vocab_size: int, prompt_mu: float, prompt_sigma: float,
+                       prompt_range: tuple[int, int], output_mu: float, output_sigma: float,
+                       output_range: tuple[int, int], seed: int) -> tuple[list[list[int]], list[int]]:
+    """Prompts with uniform token ids and lognormal lengths, and lognormal output lengths."""
+
+    rng = np.random.default_rng(seed)
+    prompt_lens = lognormal_lengths(rng, num_requests, prompt_mu, prompt_sigma, *prompt_range)
+    output_lens = lognormal_lengths(rng, num_requests, output_mu, output_sigma, *output_range)
+    prompts = [rng.integers(0, vocab_size, size=int(n)).tolist() for n in prompt_lens]
+    return prompts, [int(n) for n in output_lens]
+
+
+def categorical_exit_trace(max_new_tokens: list[int], probabilities: tuple[float, ...], seed: int) -> list[list[int]]:
+    """0-based exit steps drawn from a categorical over depths 1..len(probabilities)."""
+
+    rng = np.random.default_rng(seed)
+    p = np.asarray(probabilities, dtype=np.float64)
+    p = p / p.sum()
+    return [rng.choice(len(p), size=max(0, n - 1), p=p).astype(int).tolist() for n in max_new_tokens]
+
+
+def poisson_exit_trace(max_new_tokens: list[int], mean: float, max_steps: int, seed: int) -> list[list[int]]:
+    """0-based exit steps from Poisson(mean) depths truncated to [1, max_steps]."""
+
+    rng = np.random.default_rng(seed)
+    return [(np.clip(rng.poisson(mean, size=max(0, n - 1)), 1, max_steps) - 1).astype(int).tolist()
+            for n in max_new_tokens]

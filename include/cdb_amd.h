@@ -50,8 +50,9 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
  *
  * q [B,H,D], k_new/v_new [B,Hkv,D] are the un-rotated projections of the
  * batch's new tokens. Row b appends its rotated key and its value at position
- * p = seqlens[b] (FA's cache_seqlens) in cache layer cache_layer[b] (or
- * cache_layer0 for every row when cache_layer is null) and attends over
+ * p = seqlens[b] (FA's cache_seqlens) in cache layer cache_layer0 + cache_layer[b]
+ * (cache_layer0 alone when cache_layer is null: a row's KV slot offset
+ * slot*num_layers goes in cache_layer, the physical layer in cache_layer0) and attends over
  * positions 0..p with softmax scale `scale`. seqlens[b] < 0 marks a padding
  * row (no KV write, zero output). Block table row for batch row b is
  * table_row[b] (or b when null). rope_cos/rope_sin are [max_positions, D/2]
@@ -69,6 +70,97 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
                                float scale, int32_t dtype, hipStream_t stream);
+
+/* Fused RMSNorm sandwich over rows of `width` elements.
+ *   norm_w(x) = R(w * R(x * rsqrt(mean(x^2) + eps)))  (R rounds to the storage dtype)
+ *   mode 0: out_h = norm_a(x)
+ *   mode 1: out_h = R(residual + norm_a(x)); out_y = norm_b(out_h)   (Ouro layer,
+ *           ouro/modeling_ouro.py:445-450 and :481-502)
+ *   mode 2: out_h = norm_a(R(residual + x)); out_y = norm_b(out_h)   (Huginn block,
+ *           huginn/modeling_huginn.py:141-146 and :335-338)
+ * out_y is written only when w_b is non-null. out_h may alias x or residual. */
+int cdb_rmsnorm_fused(const void* x, const void* residual, const void* w_a, const void* w_b, void* out_h,
+                      void* out_y, int64_t rows, int32_t width, int32_t mode, float eps_a, float eps_b,
+                      int32_t dtype, hipStream_t stream);
+
+/* out[r, :] = R(R(silu(g)) * u) for gate_up[r] = [g | u] of 2*width elements
+ * (ouro/modeling_ouro.py:167-169, huginn/modeling_huginn.py:314-316). */
+int cdb_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t width, int32_t dtype, hipStream_t stream);
+
+/* Row gather/scatter: dst[dst_index[i]] = src[src_index[i]] for i < rows, rows of
+ * row_bytes bytes (a multiple of 4). A null index means the identity; a negative
+ * (or out-of-range) src index writes zeros; a negative dst index skips the row.
+ * Replaces the hidden-bank index_select/index_copy_ of cdb/model_runner.py:685-693,
+ * :559 and :1101, the embedding lookup of cdb/adapters/ouro.py:199-212 and the
+ * device token gather of cdb/model_runner.py:439-457. */
+int cdb_copy_rows(const void* src, const int64_t* src_index, int64_t src_rows, void* dst, const int64_t* dst_index,
+                  int64_t dst_rows, int64_t rows, int64_t row_bytes, hipStream_t stream);
+
+/* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
+ * (torch.argmax semantics incl. NaN; cdb/model_runner.py:1062,1105). */
+int cdb_argmax(const void* logits, int64_t* out, int64_t rows, int32_t vocab, int32_t dtype, hipStream_t stream);
+
+/* Early-exit gate and decision for one recurrent launch.
+ * kind 0: signal[b] = R(hidden[b] . weight + bias) -- Ouro's Linear(E,1) gate
+ *         (cdb/adapters/ouro.py:286-291);
+ * kind 1: signal[b] = R(||hidden[b] - prev[b]|| / max(||hidden[b]||, 1e-9)) --
+ *         Huginn's latent difference (huginn/exit_gates.py:33-40).
+ * The token policy state (fp64 cdf/survival, pending signal) is kept in arrays
+ * of state_capacity entries indexed by state_index[b] (< 0: padding row). The
+ * decision follows cdb/exit_policy.py:150-169 and cdb/continuous_api.py:1671-1724:
+ * forced exit at step max_steps-1; a replayed synthetic_depth[b] >= 0 exits at
+ * step >= depth; otherwise, with has_threshold, rule 0 accumulates the sigmoid
+ * hazard (rounded to the storage dtype when round_hazard) into the cdf and exits
+ * when cdf >= threshold, rule 1 exits when signal < threshold, both only once
+ * step+1 >= min_steps. delayed=1 decides on the previous launch's signal
+ * (DecisionHorizon.OFFSET_ONE). exit_flags[b] is 1 for an exit. */
+int cdb_exit_gate(const void* hidden, const void* prev, const void* weight, const void* bias, void* signal,
+                  double* cdf, double* survival, float* pending, int64_t state_capacity, const int64_t* state_index,
+                  const int32_t* steps, const int32_t* synthetic_depth, uint8_t* exit_flags, int64_t rows,
+                  int32_t width, int32_t kind, int32_t rule, int32_t delayed, int32_t round_hazard,
+                  int32_t min_steps, int32_t max_steps, double threshold, int32_t has_threshold, int32_t dtype,
+                  hipStream_t stream);
+
+/* Reset the gate state of n fresh tokens: cdf 0, survival 1, no pending signal
+ * (TokenExitPolicyState(), cdb/exit_policy.py:43-48). */
+int cdb_exit_gate_reset(double* cdf, double* survival, float* pending, int64_t state_capacity,
+                        const int64_t* index, int64_t n, hipStream_t stream);
+
+/* Copy-on-exit KV propagation (kv_policy "last_exited"): for token i at pool row
+ * rows[i] that exited at KV slot exit_slot[i], copy its K and V rows from cache
+ * layer layer_base + exit_slot*core_layers + l to layer_base + s*core_layers + l
+ * for every core layer l and every deeper slot s < num_slots
+ * (cdb/continuous_api.py:1225-1245, kv_cache_policy.py:235-258, cdb/cache.py:105-113). */
+int cdb_exit_kv_copy(void* k_pool, void* v_pool, int64_t layer_stride, int64_t pool_rows, int32_t num_kv_heads,
+                     int32_t head_dim, const int64_t* rows, const int32_t* exit_slot, int64_t n, int32_t layer_base,
+                     int32_t core_layers, int32_t num_slots, int32_t dtype, hipStream_t stream);
+
+/* Prefill-side RoPE + paged KV write for T tokens: q_out = rotate(q [+ q_bias]);
+ * rotate(k [+ k_bias]) and v are written to cache layer `layer` at pool rows
+ * rows[t] (negative rows write nothing). Replaces the write half of
+ * PagedAttentionCache.update (continuous_batching/cache.py:284-318) and the
+ * RoPE before it. */
+int cdb_rope_kv_write(const void* q, const void* k, const void* v, void* q_out, void* k_pool, void* v_pool,
+                      int64_t layer_stride, int32_t layer, const int64_t* rows, int64_t pool_rows,
+                      const int32_t* positions, const float* rope_cos, const float* rope_sin, int32_t rope_style,
+                      int32_t max_positions, const void* q_bias, const void* k_bias, int64_t tokens,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype, hipStream_t stream);
+
+/* Varlen causal prefill attention over the paged pool on MFMA tiles.
+ * Replaces flash_attn_varlen_func as the reference's prefill calls it after
+ * the chunk's KV write (continuous_batching/prefill_graph.py:265-309,
+ * transformers integrations/flash_paged.py:62-86). Sequence s has query tokens
+ * cu_q[s] .. cu_q[s+1]-1 of q [T,H,D] (already rotated) at positions
+ * past[s] + i; each attends to positions 0..(its own) of cache layer `layer`
+ * through block-table row table_row[s]. The chunk's own K/V must already be in
+ * the pool. Work is split into tiles of 64 query tokens: tile n covers
+ * sequence tile_seq[n], queries tile_q0[n] .. +63. out is [T,H,D]. */
+int cdb_prefill_attention(const void* q, const void* k_pool, const void* v_pool, int64_t layer_stride, int32_t layer,
+                          int32_t num_cache_layers, int64_t pool_blocks, const int32_t* block_table,
+                          const int32_t* table_row, int32_t table_width, const int32_t* cu_q, const int32_t* past,
+                          int32_t num_seqs, const int32_t* tile_seq, const int32_t* tile_q0, int32_t num_tiles,
+                          void* out, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                          float scale, int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

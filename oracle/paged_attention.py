@@ -155,3 +155,37 @@ def paged_decode_attention(
             weights /= weights.sum()
             out[b, h] = (weights @ values[:, kvh, :]).astype(np.float32)
     return rnd(out)
+
+
+def prefill_attention(q: np.ndarray, kv_pool: np.ndarray, layer: int, block_table: np.ndarray,
+                      table_row: np.ndarray, cu_q: np.ndarray, past: np.ndarray, block_size: int, scale: float,
+                      dtype: str = "bf16") -> np.ndarray:
+    """Causal varlen attention over K/V already in the pool
+    (flash_attn_varlen_func after PagedAttentionCache.update, continuous_batching/cache.py:284-318
+    and prefill_graph.py:265-309). q: [T, H, D] rotated; returns [T, H, D]."""
+
+    rnd = rounder(dtype)
+    tokens, num_heads, head_dim = q.shape
+    num_kv_heads = kv_pool.shape[3]
+    group = num_heads // num_kv_heads
+    out = np.zeros_like(q, dtype=np.float32)
+    for s in range(len(past)):
+        begin, end = int(cu_q[s]), int(cu_q[s + 1])
+        n = end - begin
+        if n == 0:
+            continue
+        total = int(past[s]) + n
+        rows = read_rows(block_table[int(table_row[s])], total, block_size)
+        keys = kv_pool[layer, 0, rows].astype(np.float64)
+        values = kv_pool[layer, 1, rows].astype(np.float64)
+        qpos = int(past[s]) + np.arange(n)
+        mask = np.arange(total)[None, :] <= qpos[:, None]
+        for h in range(num_heads):
+            kvh = h // group
+            scores = q[begin:end, h].astype(np.float64) @ keys[:, kvh, :].T * scale
+            scores = np.where(mask, scores, -np.inf)
+            scores -= scores.max(axis=1, keepdims=True)
+            w = np.exp(scores)
+            w /= w.sum(axis=1, keepdims=True)
+            out[begin:end, h] = (w @ values[:, kvh, :]).astype(np.float32)
+    return rnd(out)

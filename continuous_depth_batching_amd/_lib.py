@@ -42,7 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _P, _P,  # q_bias, k_bias
             _P, _P, c_int64,  # out, workspace, workspace_bytes
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
-            c_float, c_int32, _P,  # scale, dtype, stream
+            c_float, c_int64, c_int64, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stream
         ],
     ),
     "cdb_rmsnorm_fused": (

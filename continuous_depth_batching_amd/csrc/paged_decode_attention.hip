@@ -34,9 +34,9 @@
 namespace cdb {
 
 struct DecodeParams {
-  const void* q;            // [B, H, D]
-  const void* k_new;        // [B, Hkv, D]
-  const void* v_new;        // [B, Hkv, D]
+  const void* q;            // [B, H, D], rows q_stride elements apart
+  const void* k_new;        // [B, Hkv, D], rows kv_stride elements apart
+  const void* v_new;        // [B, Hkv, D], rows kv_stride elements apart
   void* k_pool;             // cache layer l keys at k_pool + l * layer_stride, rows x [Hkv, D]
   void* v_pool;
   const int32_t* block_table;   // [num_table_rows, table_width]
@@ -50,6 +50,7 @@ struct DecodeParams {
   void* out;                    // [B, H, D]
   float* partial;               // [total_splits, H, D + 2] when a row has > 1 split
   int64_t layer_stride;         // elements between cache layers
+  int64_t q_stride, kv_stride;  // elements between consecutive rows of q and of k_new/v_new
   int32_t cache_layer0;
   int32_t num_rows, num_heads, num_kv_heads;
   int32_t table_width, block_size_log2, split_pages;
@@ -225,7 +226,7 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
 
     // Rotated query chunk, pre-scaled into the log2 domain.
     float q[C];
-    load_rotated<T, D>(P, q_all + ((int64_t)b * P.num_heads + h) * D,
+    load_rotated<T, D>(P, q_all + (int64_t)b * P.q_stride + (int64_t)h * D,
                        P.q_bias ? static_cast<const T*>(P.q_bias) + (int64_t)h * D : nullptr, p, chunk, q);
 #pragma unroll
     for (int i = 0; i < C; ++i) q[i] *= P.scale_log2;
@@ -290,9 +291,9 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
       // The new token: rotate and append its key/value, then attend to it from registers.
       float kr[C];
       const T* kbias = P.k_bias ? static_cast<const T*>(P.k_bias) + (int64_t)kvh * D : nullptr;
-      load_rotated<T, D>(P, k_new_all + ((int64_t)b * P.num_kv_heads + kvh) * D, kbias, p, chunk, kr);
+      load_rotated<T, D>(P, k_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D, kbias, p, chunk, kr);
       Vec<T, C> vn;
-      vn.load(v_new_all + ((int64_t)b * P.num_kv_heads + kvh) * D + chunk * C);
+      vn.load(v_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D + chunk * C);
       const int new_blk = table[p >> bs_log2];
       if (slot == 0 && h % kv_group == 0 && new_blk >= 0 && new_blk < P.pool_blocks) {
         const int blk = new_blk;
@@ -483,7 +484,8 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t rope_style, int32_t max_positions, const void* q_bias, const void* k_bias,
                                void* out, void* workspace, int64_t workspace_bytes, int32_t num_rows,
                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                               int32_t split_pages, float scale, int32_t dtype, hipStream_t stream) {
+                               int32_t split_pages, float scale, int64_t q_stride, int64_t kv_stride,
+                               int32_t dtype, hipStream_t stream) {
   if (num_rows == 0) return CDB_OK;
   if (!q || !k_new || !v_new || !k_pool || !v_pool || !block_table || !seqlens || !out) return CDB_ERR_NULL;
   if (num_rows < 0 || num_rows > kMaxRowsLds || num_heads <= 0 || num_kv_heads <= 0 ||
@@ -506,6 +508,9 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
   P.rope_cos = rope_style ? rope_cos : nullptr; P.rope_sin = rope_style ? rope_sin : nullptr;
   P.q_bias = q_bias; P.k_bias = k_bias; P.out = out; P.partial = static_cast<float*>(workspace);
   P.layer_stride = layer_stride; P.cache_layer0 = cache_layer0;
+  P.q_stride = q_stride > 0 ? q_stride : (int64_t)num_heads * head_dim;
+  P.kv_stride = kv_stride > 0 ? kv_stride : (int64_t)num_kv_heads * head_dim;
+  if (P.q_stride < (int64_t)num_heads * head_dim || P.kv_stride < (int64_t)num_kv_heads * head_dim) return CDB_ERR_SHAPE;
   P.num_rows = num_rows; P.num_heads = num_heads; P.num_kv_heads = num_kv_heads;
   P.table_width = table_width; P.block_size_log2 = bs_log2; P.split_pages = split_pages;
   P.rope_style = rope_style; P.max_positions = max_positions;

@@ -1,0 +1,722 @@
+"""ContinuousDepthBatchingEngine: the CDB decode loop on the MI355X kernels.
+
+Public API and scheduling semantics follow continuous_depth_batching/continuous_api.py:
+``from_model(model, cdb_config)`` / ``generate_batch(input_ids, max_new_tokens=...,
+eos_token_id=..., exit_depths=...)``. One scheduler tick launches one bucket:
+
+  * prefill -- a full-depth forward over admitted prompt chunks; on the async
+    path each prompt's first decode token enters its prelude straight from the
+    device tokens (eager entry) and queues at the tail;
+  * recurrent -- one block application over up to ``max_num_seqs`` work items
+    that may sit at different loop steps; exited items go to the coda queue,
+    survivors advance a step and return to the queue head in launch order;
+  * coda -- LM head + argmax for exited tokens; on the async path the
+    successor token's prelude is staged from the device tokens before the host
+    reads them (eager re-entry, queue head), with at most two codas in flight.
+
+The exit decision of every row comes from the ``cdb_exit_gate`` kernel (live
+gate, replayed synthetic depth, forced final step). On the synchronous horizon
+the host waits for a launch's decisions before routing it, as the reference
+does; on the delayed horizon a launch's routing uses the decisions of the
+item's previous launch, which have long landed.
+"""
+
+from __future__ import annotations
+
+import time
+from collections import Counter, deque
+from dataclasses import dataclass, field
+from typing import Any
+
+import torch
+
+from .cache import CacheFullError, PagedKVCache
+from .config import ContinuousDepthBatchingConfig
+from .exit_policy import ExitPolicy
+from .kv_cache_policy import LoopedKvLayout, copies_exit_kv, resolve_kv_slots_per_layer
+from .model_adapter import CDBModelAdapter, resolve_cdb_model_adapter
+from .model_runner import (
+    CODA_PIPELINE_DEPTH,
+    ModelRunner,
+    PendingCodaResult,
+    PendingFlags,
+    PendingPrefillResult,
+)
+from .requests import TMP_TOKEN_ID, DepthWorkItem, GenerationOutput, RequestState, RequestStatus
+from .scheduler import CDBScheduler, ScheduledCDBBatch
+
+
+@dataclass
+class ContinuousDepthBatchingStats:
+    """Runtime counters (continuous_api.py:114-228)."""
+
+    prefill_batches: int = 0
+    prefill_requests: int = 0
+    recurrent_batches: int = 0
+    coda_batches: int = 0
+    recurrent_steps: int = 0
+    coda_tokens: int = 0
+    generated_tokens: int = 0
+    prefill_recurrent_steps: int = 0
+    prefill_coda_tokens: int = 0
+    fixed_depth_recurrent_steps: int = 0
+    exit_depth_histogram: Counter = field(default_factory=Counter)
+    recurrent_step_histogram: Counter = field(default_factory=Counter)
+    mixed_recurrent_batches: int = 0
+    mixed_recurrent_depth_histogram: Counter = field(default_factory=Counter)
+    max_mixed_depths_per_batch: int = 0
+    scheduler_refills: int = 0
+    max_depth_queue_size: int = 0
+    recurrent_graph_hits: int = 0
+    recurrent_graph_captures: int = 0
+    max_in_flight_requests: int = 0
+    max_live_requests: int = 0
+    prelude_batches: Counter = field(default_factory=Counter)
+    prelude_tokens: Counter = field(default_factory=Counter)
+    prelude_gathered_tokens: Counter = field(default_factory=Counter)
+    cancelled_depth_items: int = 0
+    coda_suppressed_ticks: int = 0
+    max_pending_coda_results: int = 0
+    coda_pipeline_blocked_ticks: int = 0
+    scheduler_ticks: int = 0
+    exit_kv_copies: int = 0
+
+    @property
+    def skipped_recurrent_steps(self) -> int:
+        return max(0, self.fixed_depth_recurrent_steps - self.recurrent_steps)
+
+    @property
+    def mean_recurrent_batch_size(self) -> float:
+        return self.recurrent_steps / self.recurrent_batches if self.recurrent_batches else 0.0
+
+    @property
+    def mean_coda_batch_size(self) -> float:
+        return self.coda_tokens / self.coda_batches if self.coda_batches else 0.0
+
+
+@dataclass
+class LaunchRecord:
+    """One launch as the engine issued it (for schedule-parity checks)."""
+
+    kind: str
+    request_ids: list[str]
+    positions: list[int] = field(default_factory=list)
+    steps: list[int] = field(default_factory=list)
+    exits: list[bool] = field(default_factory=list)
+
+
+def resolve_num_blocks(num_blocks: int | None, mem_fraction: float | None, bytes_per_block: int,
+                       device: torch.device) -> int:
+    """Explicit num_blocks, or size the pool from free device memory (kv_cache_sizing.py:34-80)."""
+
+    if num_blocks is not None:
+        return num_blocks
+    free, total = torch.cuda.mem_get_info(device)
+    fraction = 0.8 if mem_fraction is None else mem_fraction
+    budget = int(free - (1.0 - fraction) * total)
+    blocks = budget // bytes_per_block - PagedKVCache.EXTRA_BLOCKS
+    if blocks <= 0:
+        raise CacheFullError("not enough free device memory for the paged KV cache")
+    return blocks
+
+
+@dataclass
+class ContinuousDepthBatchingEngine:
+    model: Any
+    cdb_config: ContinuousDepthBatchingConfig
+    cache: PagedKVCache
+    scheduler: CDBScheduler
+    runner: ModelRunner
+    model_adapter: CDBModelAdapter
+    exit_policy: ExitPolicy
+    exit_kv_layout: LoopedKvLayout | None = None
+    last_stats: ContinuousDepthBatchingStats = field(default_factory=ContinuousDepthBatchingStats)
+    pending_coda_results: deque = field(default_factory=deque)
+    pending_prefill_results: deque = field(default_factory=deque)
+    stalled_decoders: dict = field(default_factory=dict)
+    finished_outputs: dict = field(default_factory=dict)
+    record_launches: bool = False
+    launch_log: list = field(default_factory=list)
+    _exit_kv_backlog: list = field(default_factory=list)
+    _pending_flags: dict = field(default_factory=dict)
+
+    # -- construction (continuous_api.py:274-376) -------------------------------------------------------------
+    @classmethod
+    def from_model(cls, model: Any, cdb_config: ContinuousDepthBatchingConfig, *, dtype: torch.dtype | None = None,
+                   model_adapter: CDBModelAdapter | None = None) -> "ContinuousDepthBatchingEngine":
+        del dtype
+        cfg = cdb_config.get_resolved(model.config)
+        adapter = resolve_cdb_model_adapter(model, model_adapter)
+        assert cfg.max_recurrent_steps is not None
+        adapter.configure_recurrent_steps(cfg.max_recurrent_steps)
+        adapter.configure_exit_signal(cfg.exit_threshold is not None or cfg.synthetic_exit_replay)
+        exit_policy = ExitPolicy(spec=adapter.exit_policy_spec(), threshold=cfg.exit_threshold,
+                                 min_recurrent_steps=cfg.min_recurrent_steps,
+                                 max_recurrent_steps=cfg.max_recurrent_steps,
+                                 delay_gate_consumption=cfg.delay_gate_consumption,
+                                 use_async_batching=cfg.use_async_batching,
+                                 synthetic_exit_replay=cfg.synthetic_exit_replay)
+        adapter.configure_kv_policy(cfg.kv_policy, cfg.kv_slots_per_layer)
+        layout = adapter.kv_cache_layout()
+        num_kv_heads, head_dim = adapter.kv_geometry()
+        elem = torch.empty((), dtype=adapter.dtype).element_size()
+        bytes_per_block = 2 * layout.num_cache_layers * cfg.block_size * num_kv_heads * head_dim * elem
+        cfg.num_blocks = resolve_num_blocks(cfg.num_blocks, cfg.mem_fraction_static, bytes_per_block, adapter.device)
+        cfg.max_num_seqs = min(cfg.max_num_seqs, cfg.max_num_batched_tokens)
+        cache = PagedKVCache(layout=layout, num_blocks=cfg.num_blocks, block_size=cfg.block_size,
+                             num_kv_heads=num_kv_heads, head_dim=head_dim, max_model_len=cfg.max_model_len,
+                             max_num_batched_tokens=cfg.max_num_batched_tokens, max_requests=cfg.max_num_seqs,
+                             dtype=adapter.dtype, device=adapter.device)
+        runner = ModelRunner(engine_config=cfg, cache=cache, model_adapter=adapter, exit_policy=exit_policy)
+        scheduler = CDBScheduler(cache, cfg.max_recurrent_steps, safety_margin=cfg.safety_margin,
+                                 kv_pressure_mode=cfg.kv_pressure_mode, max_model_len=cfg.max_model_len,
+                                 max_num_seqs=cfg.max_num_seqs, min_free_slots=cfg.min_free_slots,
+                                 min_coda_batch_size=cfg.min_coda_batch_size)
+        exit_kv_layout = layout if copies_exit_kv(cfg.kv_policy) else None
+        return cls(model=model, cdb_config=cfg, cache=cache, scheduler=scheduler, runner=runner,
+                   model_adapter=adapter, exit_policy=exit_policy, exit_kv_layout=exit_kv_layout)
+
+    # -- public API (continuous_api.py:378-452) -----------------------------------------------------------------
+    @torch.no_grad()
+    def generate_batch(self, input_ids: list[list[int]], *, max_new_tokens: int | list[int],
+                       eos_token_id: int | list[int] | None = None, stop_sequences: list[list[int]] | None = None,
+                       warmup: bool = True, model_kwargs: dict | None = None,
+                       exit_depths: list[list[int]] | None = None, arrival_offsets_s: list[float] | None = None,
+                       record_token_times: bool = False, record_queue_samples: bool = False) -> list[GenerationOutput]:
+        del warmup, record_token_times, record_queue_samples
+        if arrival_offsets_s is not None:
+            raise NotImplementedError("open-loop arrivals are not served by this engine")
+        self._validate_generate_inputs(input_ids, max_new_tokens)
+        mnt = list(max_new_tokens) if isinstance(max_new_tokens, list) else [max_new_tokens] * len(input_ids)
+        mnt = self._cap_to_model_len(input_ids, mnt)
+        self._validate_model_kwargs(model_kwargs)
+        self.exit_policy.validate_serving_timing()
+        self._validate_exit_depths(input_ids, mnt, exit_depths)
+        self.reset()
+        states = [RequestState(request_id=f"request-{i}", initial_tokens=list(p), max_new_tokens=mnt[i],
+                               eos_token_id=eos_token_id,
+                               stop_sequences=[list(s) for s in stop_sequences] if stop_sequences else [],
+                               synthetic_exit_depths=list(exit_depths[i]) if exit_depths is not None else [],
+                               replay_eos_finishes=self.cdb_config.replay_eos_finishes)
+                  for i, p in enumerate(input_ids)]
+        for s in states:
+            self.scheduler.add_waiting_request(s)
+        try:
+            if self.cdb_config.refill:
+                self._run_scheduler_loop()
+            else:
+                self._run_no_refill_loop()
+        finally:
+            self.runner.synchronize()
+            self.scheduler.free_unfinished_requests()
+        outputs = [self.finished_outputs[s.request_id] for s in states]
+        self.last_stats.generated_tokens = sum(len(o.generated_tokens) for o in outputs)
+        return outputs
+
+    def reset(self) -> None:
+        self.scheduler.reset()
+        self.cache.free_all_requests()
+        self.cache.reset_peak_usage()
+        self.runner.reset_cdb_runtime_counters()
+        self.last_stats = ContinuousDepthBatchingStats()
+        self.pending_coda_results.clear()
+        self.pending_prefill_results.clear()
+        self.stalled_decoders.clear()
+        self.finished_outputs.clear()
+        self._exit_kv_backlog.clear()
+        self._pending_flags.clear()
+        self.launch_log.clear()
+
+    # -- refill loop (continuous_api.py:503-606) ----------------------------------------------------------------
+    def _run_scheduler_loop(self) -> None:
+        sched = self.scheduler
+        cfg = self.cdb_config
+        while sched.has_pending_work() or self.pending_coda_results or self.pending_prefill_results:
+            self._consume_ready_prefill_results(block=not sched.has_pending_work())
+            self._consume_ready_coda_results(block=not sched.has_pending_work())
+            if not sched.has_pending_work():
+                continue
+            resumed = self._restage_stalled_decoders()
+            self._prelude_and_enqueue_depth(resumed, site="resumed", front=True)
+            stats = self.last_stats
+            stats.scheduler_ticks += 1
+            pending_codas = len(self.pending_coda_results)
+            if pending_codas:
+                stats.coda_suppressed_ticks += 1
+            scheduled = sched.schedule_next(token_budget=self.cache.max_num_batched_tokens,
+                                            cache_budget=self.cache.num_pages,
+                                            allow_coda=pending_codas < CODA_PIPELINE_DEPTH)
+            if (pending_codas >= CODA_PIPELINE_DEPTH and sched.coda_queue
+                    and (scheduled is None or len(sched.coda_queue) >= sched.min_coda_batch_size)):
+                stats.coda_pipeline_blocked_ticks += 1
+            if scheduled is None:
+                if self.pending_prefill_results:
+                    self._consume_ready_prefill_results(block=True)
+                    continue
+                if self.pending_coda_results:
+                    self._consume_ready_coda_results(block=True)
+                    continue
+                if self.stalled_decoders:
+                    raise CacheFullError("KV cache full: stalled decoders cannot allocate and preemption "
+                                         f"(kv_pressure_mode={cfg.kv_pressure_mode!r}) is not served by this engine")
+                self._raise_scheduler_stall()
+            if scheduled.kind == "prefill":
+                self._run_prefill_batch(scheduled)
+            elif scheduled.kind == "coda":
+                self._stage_coda_batch(scheduled.depth_items or [])
+            else:
+                self._run_mixed_recurrent_batch(scheduled.depth_items or [])
+        self._consume_ready_prefill_results(block=True)
+        self._consume_ready_coda_results(block=True)
+        self._finish_stats()
+
+    def _finish_stats(self) -> None:
+        s = self.last_stats
+        s.scheduler_refills = self.scheduler.refill_events
+        s.max_depth_queue_size = self.scheduler.max_depth_queue_size
+        s.recurrent_graph_hits = self.runner.recurrent_graph_hits
+        s.recurrent_graph_captures = self.runner.recurrent_graph_captures
+        s.max_in_flight_requests = self.scheduler.max_in_flight_requests
+        s.max_live_requests = self.scheduler.max_live_requests
+        assert self.cdb_config.max_recurrent_steps is not None
+        s.fixed_depth_recurrent_steps = s.coda_tokens * self.cdb_config.max_recurrent_steps
+
+    # -- prefill (continuous_api.py:995-1088) -------------------------------------------------------------------
+    def _run_prefill_batch(self, scheduled: ScheduledCDBBatch) -> None:
+        requests = scheduled.requests or []
+        if not requests:
+            raise RuntimeError("Prefill scheduler tick has no requests")
+        stats = self.last_stats
+        stats.prefill_batches += 1
+        stats.prefill_requests += len(requests)
+        stats.prefill_recurrent_steps += scheduled.num_q_tokens * (self.cdb_config.max_recurrent_steps or 0)
+        pending = self.runner.stage_prefill_batch(requests, allow_async=self.cdb_config.use_async_batching)
+        if self.record_launches:
+            self.launch_log.append(LaunchRecord("prefill", [f.state.request_id for f in requests],
+                                                [f.state.position_offset for f in requests]))
+        eager_flags: list[bool] = []
+        eager_items: list[DepthWorkItem] = []
+        eager_rows: list[int] = []
+        for future in requests:
+            state = future.state
+            if not future.has_new_token:
+                self.scheduler.release_in_flight_request(state.request_id)
+                continue
+            stats.prefill_coda_tokens += 1
+            eager = False
+            if (self.cdb_config.use_async_batching and not state.will_finish_on_pending_token()
+                    and self._try_allocate_one_decode_token(state)):
+                eager = True
+                eager_rows.append(len(eager_flags))
+                eager_items.append(self._build_decode_item(state, token_id=TMP_TOKEN_ID))
+            eager_flags.append(eager)
+        pending.eager_entries = eager_flags
+        if eager_items:
+            self._record_prelude("after_prefill_eager", len(eager_items), gathered=len(eager_items))
+            self.runner.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
+            self._enqueue_prelude_items(eager_items, front=False)
+        self.pending_prefill_results.append(pending)
+
+    def _consume_ready_prefill_results(self, *, block: bool) -> None:
+        while self.pending_prefill_results:
+            pending = self.pending_prefill_results[0]
+            if not block and not pending.is_ready():
+                return
+            self.pending_prefill_results.popleft()
+            self._consume_prefill_result(pending)
+
+    def _consume_prefill_result(self, pending: PendingPrefillResult) -> None:
+        tokens = self.runner.consume_prefill_result(pending)
+        eager = pending.eager_entries or [False] * len(tokens)
+        new_items: list[DepthWorkItem] = []
+        k = 0
+        for future in pending.futures:
+            if not future.has_new_token:
+                continue
+            state = future.state
+            token, was_eager = tokens[k], eager[k]
+            k += 1
+            if state.status == RequestStatus.FINISHED:
+                continue
+            if was_eager:
+                if state.update_and_check_completion(token):
+                    self._retire_request(state)
+                continue
+            if self._advance_after_prefill(state, token):
+                continue
+            item = self._stage_decode_token(state)
+            if item is not None:
+                new_items.append(item)
+        self._prelude_and_enqueue_depth(new_items, site="after_prefill")
+
+    # -- recurrent (continuous_api.py:1090-1280) ----------------------------------------------------------------
+    def _run_mixed_recurrent_batch(self, items: list[DepthWorkItem]) -> None:
+        items = self._drop_cancelled_items(items)
+        if not items:
+            return
+        stats = self.last_stats
+        stats.mixed_recurrent_batches += 1
+        depth_counts = Counter(item.recurrent_step for item in items)
+        stats.max_mixed_depths_per_batch = max(stats.max_mixed_depths_per_batch, len(depth_counts))
+        for step, count in depth_counts.items():
+            stats.mixed_recurrent_depth_histogram[step] += count
+        launch_steps = [item.recurrent_step for item in items]
+        flags = self.runner.compute_recurrent_batch(items)
+        stats.recurrent_batches += 1
+        stats.recurrent_steps += len(items)
+        max_steps = self.cdb_config.max_recurrent_steps
+        delayed = self.exit_policy.delayed()
+        refills: list[DepthWorkItem] = []
+        exits: list[bool] = []
+        for idx, item in enumerate(items):
+            step = item.recurrent_step
+            stats.recurrent_step_histogram[step] += 1
+            if delayed:
+                previous = self._pending_flags.pop(id(item), None)
+                should_exit = step == max_steps - 1 or (
+                    item.apply_exit_gate and previous is not None and previous[0].get(previous[1]))
+                if not should_exit:
+                    self._pending_flags[id(item)] = (flags, idx)
+            elif not item.apply_exit_gate:
+                should_exit = step == max_steps - 1
+            else:
+                should_exit = flags.get(idx)
+            exits.append(should_exit)
+            if should_exit:
+                self._record_exit(item, step)
+                self.scheduler.enqueue_coda(item)
+            else:
+                item.recurrent_step = step + 1
+                refills.append(item)
+        if refills:
+            self.scheduler.enqueue_depth_front(refills)
+        self._flush_exit_kv_copies()
+        if self.record_launches:
+            self.launch_log.append(LaunchRecord("recurrent", [i.state.request_id for i in items],
+                                                [i.token_position for i in items], launch_steps, exits))
+
+    def _record_exit(self, item: DepthWorkItem, step: int) -> None:
+        if item.apply_exit_gate:
+            item.state.current_token_exit_depth = step
+            item.state.exit_depths.append(step)
+            self.last_stats.exit_depth_histogram[step] += 1
+        self._pending_flags.pop(id(item), None)
+        max_steps = self.cdb_config.max_recurrent_steps or 0
+        if self.exit_kv_layout is not None and step < max_steps - 1:
+            self._exit_kv_backlog.append((item, step))
+
+    def _flush_exit_kv_copies(self) -> None:
+        """Copy each exited token's exit-step KV into its deeper slots before any deeper read."""
+
+        if not self._exit_kv_backlog:
+            return
+        backlog, self._exit_kv_backlog = self._exit_kv_backlog, []
+        rows = [self.cache.token_row(item.state.request_id, item.token_position) for item, _ in backlog]
+        steps = [step for _, step in backlog]
+        self.runner.copy_exit_kv(rows, steps)
+        self.last_stats.exit_kv_copies += len(rows)
+
+    # -- coda (continuous_api.py:1282-1406) ---------------------------------------------------------------------
+    def _stage_coda_batch(self, items: list[DepthWorkItem]) -> None:
+        items = self._drop_cancelled_items(items)
+        if not items:
+            return
+        pending = self.runner.stage_coda_batch(items, allow_async=self.cdb_config.use_async_batching)
+        if self.record_launches:
+            self.launch_log.append(LaunchRecord("coda", [i.state.request_id for i in items],
+                                                [i.token_position for i in items]))
+        if self.cdb_config.use_async_batching:
+            eager_items, eager_rows = self._select_eager_reentries(pending)
+            if eager_items:
+                self._record_prelude("after_coda_eager", len(eager_items), gathered=len(eager_items))
+                self.runner.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
+            self._enqueue_prelude_items(eager_items, front=True)
+        self.pending_coda_results.append(pending)
+        self.last_stats.max_pending_coda_results = max(self.last_stats.max_pending_coda_results,
+                                                       len(self.pending_coda_results))
+
+    def _select_eager_reentries(self, pending: PendingCodaResult) -> tuple[list[DepthWorkItem], list[int]]:
+        flags = [False] * len(pending.items)
+        items: list[DepthWorkItem] = []
+        rows: list[int] = []
+        for idx, item in enumerate(pending.items):
+            state = item.state
+            if state.will_finish_on_pending_token():
+                continue
+            state.position_offset += 1
+            if not self._try_allocate_one_decode_token(state):
+                state.position_offset -= 1
+                continue
+            flags[idx] = True
+            items.append(self._build_decode_item(state, token_id=TMP_TOKEN_ID))
+            rows.append(idx)
+        pending.eager_reentries = flags
+        return items, rows
+
+    def _consume_ready_coda_results(self, *, block: bool) -> None:
+        while self.pending_coda_results:
+            pending = self.pending_coda_results[0]
+            if not block and not pending.is_ready():
+                return
+            self.pending_coda_results.popleft()
+            self._consume_coda_result(pending)
+
+    def _consume_coda_result(self, pending: PendingCodaResult) -> None:
+        tokens = self.runner.consume_coda_result(pending)
+        self.last_stats.coda_batches += 1
+        self.last_stats.coda_tokens += len(pending.items)
+        eager = pending.eager_reentries or [False] * len(pending.items)
+        new_items: list[DepthWorkItem] = []
+        for item, token, was_eager in zip(pending.items, tokens, eager):
+            state = item.state
+            if state.status == RequestStatus.FINISHED:
+                continue
+            if was_eager:
+                if state.update_and_check_completion(token):
+                    self._retire_request(state)
+                continue
+            if self._advance_after_coda(item, token):
+                continue
+            new = self._stage_decode_token(state)
+            if new is not None:
+                new_items.append(new)
+        self._prelude_and_enqueue_depth(new_items, site="after_coda_staged", front=True)
+
+    def _advance_after_coda(self, item: DepthWorkItem, token: int) -> bool:
+        state = item.state
+        state.position_offset += 1
+        finished = state.update_and_check_completion(token)
+        if finished:
+            self._retire_request(state)
+        return finished
+
+    def _advance_after_prefill(self, state: RequestState, token: int) -> bool:
+        finished = state.update_and_check_completion(token)
+        if finished:
+            self._retire_request(state)
+        return finished
+
+    def _retire_request(self, state: RequestState) -> None:
+        self.scheduler.record_completion(state)
+        self.scheduler.finish_request(state.request_id)
+        self.stalled_decoders.pop(state.request_id, None)
+        self.finished_outputs[state.request_id] = state.to_generation_output()
+        self.scheduler.block_new_requests = False
+
+    def _drop_cancelled_items(self, items: list[DepthWorkItem]) -> list[DepthWorkItem]:
+        live = [i for i in items if i.state.status != RequestStatus.FINISHED]
+        if len(live) != len(items):
+            dead = [i for i in items if i.state.status == RequestStatus.FINISHED]
+            self.runner.release_hidden_slots(dead)
+            for i in dead:
+                self._pending_flags.pop(id(i), None)
+            self.last_stats.cancelled_depth_items += len(dead)
+        return live
+
+    # -- decode-token staging (continuous_api.py:1530-1669) -----------------------------------------------------
+    def _record_prelude(self, site: str, count: int, *, gathered: int = 0) -> None:
+        self.last_stats.prelude_batches[site] += 1
+        self.last_stats.prelude_tokens[site] += count
+        if gathered:
+            self.last_stats.prelude_gathered_tokens[site] += gathered
+
+    def _prelude_and_enqueue_depth(self, items: list[DepthWorkItem], *, site: str, front: bool = False) -> None:
+        if items:
+            self._record_prelude(site, len(items))
+            self.runner.compute_prelude_batch(items)
+        self._enqueue_prelude_items(items, front=front)
+
+    def _enqueue_prelude_items(self, items: list[DepthWorkItem], *, front: bool) -> None:
+        if front:
+            self.scheduler.enqueue_depth_front(items)
+        else:
+            for item in items:
+                self.scheduler.enqueue_depth(item)
+
+    def _build_decode_item(self, state: RequestState, *, token_id: int | None = None) -> DepthWorkItem:
+        state.reset_depth_state_for_next_token()
+        return DepthWorkItem(state=state, token_id=state.tokens_to_process[0] if token_id is None else token_id,
+                             token_position=state.position_offset, recurrent_step=0,
+                             synthetic_exit_depth=state.next_synthetic_exit_depth())
+
+    def _stage_decode_token(self, state: RequestState) -> DepthWorkItem | None:
+        if not state.tokens_to_process or state.tokens_to_process[0] < 0:
+            raise RuntimeError(f"Request {state.request_id} has no sampled token ready for CDB decode")
+        if self._try_allocate_one_decode_token(state):
+            self.stalled_decoders.pop(state.request_id, None)
+            return self._build_decode_item(state)
+        if self.cdb_config.kv_pressure_mode in ("none", "reserve"):
+            raise CacheFullError(f"KV cache full staging a decode block for request {state.request_id} "
+                                 f"(kv_pressure_mode={self.cdb_config.kv_pressure_mode!r})")
+        self.stalled_decoders[state.request_id] = state
+        return None
+
+    def _restage_stalled_decoders(self) -> list[DepthWorkItem]:
+        items: list[DepthWorkItem] = []
+        for state in list(self.stalled_decoders.values()):
+            item = self._stage_decode_token(state)
+            if item is None:
+                break
+            items.append(item)
+        return items
+
+    def _try_allocate_one_decode_token(self, state: RequestState) -> bool:
+        current = state.current_len()
+        if state.allocated_blocks * self.cache.block_size - current >= 1 and state.allocated_blocks > 0:
+            return True
+        needed = -(-(current + 1) // self.cache.block_size) - state.allocated_blocks
+        got = self.cache.allocate_blocks(needed, state.request_id, state.allocated_blocks)
+        if got is None:
+            return False
+        state.allocated_blocks += got
+        return True
+
+    def _raise_scheduler_stall(self) -> None:
+        candidates = self.scheduler.get_prefill_bucket()
+        if not candidates:
+            raise CacheFullError("The CDB scheduler could place no work and has nothing in flight")
+        state = candidates[0]
+        n = min(len(state.remaining_prefill_tokens), self.cache.max_num_batched_tokens)
+        needed = -(-(state.current_len() + n) // self.cache.block_size) - state.allocated_blocks
+        if not self.cache.will_allocation_be_successful(needed, state.allocated_blocks):
+            raise CacheFullError(f"KV cache full: request {state.request_id} needs {needed} blocks for its next "
+                                 f"prefill chunk, {self.cache.get_num_free_blocks()} are free")
+        raise RuntimeError(f"No request could be scheduled: request {state.request_id} reads "
+                           f"{state.current_len()} KV tokens, exceeding the cache budget of {self.cache.num_pages}")
+
+    # -- no-refill baseline (continuous_api.py:608-944, synchronous wave form) ----------------------------------
+    def _run_no_refill_loop(self) -> None:
+        sched = self.scheduler
+        max_steps = self.cdb_config.max_recurrent_steps or 0
+        while sched.has_pending_work():
+            sched.record_resident_sample()
+            did_prefill = False
+            while sched.admit_prefill(sched.has_decode_work()):
+                scheduled = sched.schedule_prefill_batch(token_budget=self.cache.max_num_batched_tokens,
+                                                         cache_budget=self.cache.num_pages)
+                if scheduled is None or not scheduled.requests:
+                    break
+                self._run_no_refill_prefill(scheduled)
+                did_prefill = True
+            cohort = [s for s in sched.active_requests.values()
+                      if s.status == RequestStatus.DECODING and s.tokens_to_process and s.tokens_to_process[0] >= 0]
+            cohort = cohort[: self.cdb_config.max_num_seqs]
+            items = [item for s in cohort if (item := self._stage_decode_token(s)) is not None]
+            if not items:
+                if not did_prefill and sched.has_pending_work():
+                    raise CacheFullError("No-refill loop stalled with pending work")
+                continue
+            self._record_prelude("wave_cohort", len(items))
+            self.runner.compute_prelude_batch(items)
+            survivors = items
+            exited: list[DepthWorkItem] = []
+            for step in range(max_steps):
+                for item in survivors:
+                    item.recurrent_step = step
+                flags = self.runner.compute_recurrent_batch(survivors)
+                self.last_stats.recurrent_batches += 1
+                self.last_stats.recurrent_steps += len(survivors)
+                self.last_stats.recurrent_step_histogram[step] += len(survivors)
+                continuing = []
+                for idx, item in enumerate(survivors):
+                    if step == max_steps - 1 or (item.apply_exit_gate and flags.get(idx)):
+                        self._record_exit(item, step)
+                        exited.append(item)
+                    else:
+                        continuing.append(item)
+                self._flush_exit_kv_copies()
+                survivors = continuing
+                if not survivors:
+                    break
+            pending = self.runner.stage_coda_batch(exited, allow_async=False)
+            tokens = self.runner.consume_coda_result(pending)
+            self.last_stats.coda_batches += 1
+            self.last_stats.coda_tokens += len(exited)
+            for item, token in zip(exited, tokens):
+                if item.state.status != RequestStatus.FINISHED:
+                    self._advance_after_coda(item, token)
+        self._finish_stats()
+
+    def _run_no_refill_prefill(self, scheduled: ScheduledCDBBatch) -> None:
+        requests = scheduled.requests or []
+        stats = self.last_stats
+        stats.prefill_batches += 1
+        stats.prefill_requests += len(requests)
+        stats.prefill_recurrent_steps += scheduled.num_q_tokens * (self.cdb_config.max_recurrent_steps or 0)
+        pending = self.runner.stage_prefill_batch(requests, allow_async=False)
+        tokens = self.runner.consume_prefill_result(pending)
+        k = 0
+        for future in requests:
+            self.scheduler.release_in_flight_request(future.state.request_id)
+            if not future.has_new_token:
+                continue
+            stats.prefill_coda_tokens += 1
+            token = tokens[k]
+            k += 1
+            self._advance_after_prefill(future.state, token)
+
+    # -- validation (continuous_api.py:1746-1833) ---------------------------------------------------------------
+    @staticmethod
+    def _validate_generate_inputs(input_ids: list[list[int]], max_new_tokens: int | list[int]) -> None:
+        if not input_ids:
+            raise ValueError("input_ids must contain at least one prompt")
+        if isinstance(max_new_tokens, list):
+            if len(max_new_tokens) != len(input_ids):
+                raise ValueError(f"max_new_tokens has {len(max_new_tokens)} entries but there are "
+                                 f"{len(input_ids)} prompts")
+            bad = [i for i, v in enumerate(max_new_tokens) if v < 1]
+            if bad:
+                raise ValueError(f"max_new_tokens must be >= 1 for every request, but got <1 at indices {bad}")
+        elif max_new_tokens <= 0:
+            raise ValueError(f"max_new_tokens must be positive, but got {max_new_tokens}")
+        empty = [i for i, p in enumerate(input_ids) if not p]
+        if empty:
+            raise ValueError(f"input_ids contains empty prompts at indices {empty}")
+
+    def _cap_to_model_len(self, input_ids: list[list[int]], mnt: list[int]) -> list[int]:
+        limit = self.cdb_config.max_model_len
+        too_long = [i for i, p in enumerate(input_ids) if len(p) >= limit]
+        if too_long:
+            raise ValueError(f"{len(too_long)} prompt(s) have length >= max_model_len ({limit}) and leave no room "
+                             f"for a generated token: requests {too_long[:5]}")
+        return [min(m, limit - len(p)) for m, p in zip(mnt, input_ids)]
+
+    def _validate_model_kwargs(self, model_kwargs: dict | None) -> None:
+        if (self.cdb_config.exit_threshold is not None and model_kwargs is not None
+                and model_kwargs.get("use_early_exit_gate") is False):
+            raise ValueError("exit_threshold CDB requires use_early_exit_gate to stay enabled")
+
+    def _validate_exit_depths(self, input_ids: list[list[int]], mnt: list[int],
+                              exit_depths: list[list[int]] | None) -> None:
+        if exit_depths is None:
+            return
+        cfg = self.cdb_config
+        if not cfg.synthetic_exit_replay:
+            raise ValueError("exit_depths requires cdb_config.synthetic_exit_replay=True")
+        if cfg.exit_threshold is not None:
+            raise ValueError("exit_depths cannot be combined with exit_threshold")
+        if len(exit_depths) != len(input_ids):
+            raise ValueError(f"exit_depths has {len(exit_depths)} entries but there are {len(input_ids)} requests")
+        max_steps = cfg.max_recurrent_steps or 0
+        for i, depths in enumerate(exit_depths):
+            if len(depths) != mnt[i] - 1:
+                raise ValueError(f"exit_depths[{i}] has {len(depths)} entries but the request stages "
+                                 f"{mnt[i] - 1} decode tokens (max_new_tokens - 1)")
+            for d in depths:
+                if not 0 <= d < max_steps:
+                    raise ValueError(f"exit_depths[{i}] value {d} is out of range [0, {max_steps}); values are "
+                                     "0-based recurrent steps")
+        if copies_exit_kv(cfg.kv_policy):
+            return
+        slots = resolve_kv_slots_per_layer(cfg.kv_policy, total_recurrent_steps=max_steps,
+                                           requested_slots=cfg.kv_slots_per_layer)
+        extra = int(cfg.delay_gate_consumption and cfg.use_async_batching)
+        for depths in exit_depths:
+            for d in depths:
+                if d + 1 + extra < slots:
+                    raise ValueError("Every replay exit depth must write all static KV slots before exit: "
+                                     f"kv_slots_per_layer={slots}, exit step {d + 1 + extra}")
+
+
+__all__ = ["ContinuousDepthBatchingEngine", "ContinuousDepthBatchingStats", "CacheFullError", "LaunchRecord",
+           "PendingFlags", "time"]

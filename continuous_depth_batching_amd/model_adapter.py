@@ -1,0 +1,150 @@
+"""Model adapter boundary between the CDB engine and a looped model.
+
+Counterpart of the reference's CDBModelAdapter (continuous_depth_batching/model_adapter.py:14-122):
+a model exposes a prelude (token embedding, plus prelude layers where the
+model has them), one recurrent block application, and a coda (LM head).
+Here each stage is a sequence of HIP kernel launches over static device
+buffers owned by the runner, so a whole recurrent stage can be captured into
+one HIP graph per batch bucket.
+"""
+
+from __future__ import annotations
+
+from abc import ABC, abstractmethod
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import ops
+from .cache import PagedKVCache
+from .exit_policy import DecisionHorizon, ExitDecisionRule, ExitPolicySpec
+from .kv_cache_policy import LoopedKvLayout
+
+
+@dataclass
+class GateLaunch:
+    """Static per-bucket buffers of the exit gate (see ``cdb_exit_gate``)."""
+
+    state: ops.GateState
+    steps: torch.Tensor          # [Bp] int32
+    synthetic: torch.Tensor      # [Bp] int32 (-1 = no replayed depth)
+    flags: torch.Tensor          # [Bp] uint8
+    signal: torch.Tensor         # [Bp] model dtype
+    rule: int
+    round_hazard: bool
+    min_steps: int
+    max_steps: int
+    threshold: float | None
+    enabled: bool = True
+
+
+@dataclass
+class RecurrentLaunch:
+    """Static device inputs of one recurrent-stage bucket (rows = bucket size)."""
+
+    rows: int
+    bank: torch.Tensor           # [capacity, width] hidden-state bank
+    bank_slots: torch.Tensor     # [rows] int64, -1 = padding
+    positions: torch.Tensor      # [rows] int32 position of the token, -1 = padding
+    table_rows: torch.Tensor     # [rows] int32 block-table row of the token's request
+    slot_offset: torch.Tensor    # [rows] int32 cache layer of core layer 0 at the row's step (prelude + slot * C)
+    cache: PagedKVCache
+    workspace: torch.Tensor      # decode-attention split workspace (fp32)
+    split_pages: int
+    gate: GateLaunch
+
+
+@dataclass
+class PrefillLaunch:
+    """Device inputs of one full-depth prefill forward over T prompt tokens."""
+
+    tokens: torch.Tensor         # [T] int64
+    positions: torch.Tensor      # [T] int32
+    write_rows: torch.Tensor     # [T] int64 pool rows of each token
+    cu_q: torch.Tensor           # [S+1] int32
+    past: torch.Tensor           # [S] int32
+    table_rows: torch.Tensor     # [S] int32
+    tile_seq: torch.Tensor       # [tiles] int32
+    tile_q0: torch.Tensor        # [tiles] int32
+    last_index: torch.Tensor     # [N] int64 token index whose logits sample the next token
+    cache: PagedKVCache
+
+
+class CDBModelAdapter(ABC):
+    """Model-specific stage kernels used by the CDB runner."""
+
+    stages_use_attention: bool = False
+
+    @property
+    @abstractmethod
+    def hidden_width(self) -> int:
+        """Width of one hidden-bank row (the recurrent state carried between steps)."""
+
+    @property
+    @abstractmethod
+    def dtype(self) -> torch.dtype: ...
+
+    @property
+    @abstractmethod
+    def device(self) -> torch.device: ...
+
+    @abstractmethod
+    def configure_recurrent_steps(self, max_recurrent_steps: int) -> None: ...
+
+    @abstractmethod
+    def configure_kv_policy(self, kv_policy: str, kv_slots_per_layer: int | None) -> None: ...
+
+    @abstractmethod
+    def kv_cache_layout(self) -> LoopedKvLayout: ...
+
+    @abstractmethod
+    def kv_geometry(self) -> tuple[int, int]:
+        """(num_key_value_heads, head_dim) of the paged cache."""
+
+    def exit_policy_spec(self) -> ExitPolicySpec:
+        return ExitPolicySpec(ExitDecisionRule.CUMULATIVE_HAZARD, DecisionHorizon.SAME_STEP)
+
+    def configure_exit_signal(self, enabled: bool) -> None:
+        del enabled
+
+    def decides_exit_before_loop(self) -> bool:
+        return self.exit_policy_spec().rule is ExitDecisionRule.PRELOOP_DISTRIBUTION
+
+    @abstractmethod
+    def prelude(self, tokens: torch.Tensor, bank: torch.Tensor, slots: torch.Tensor, n: int) -> None:
+        """Write the prelude state of tokens[:n] into bank rows slots[:n]."""
+
+    @abstractmethod
+    def recurrent_step(self, launch: RecurrentLaunch) -> None:
+        """One block application over the bucket: bank rows in, bank rows + gate decisions out."""
+
+    @abstractmethod
+    def prefill(self, launch: PrefillLaunch) -> torch.Tensor:
+        """Full-depth prefill forward; returns the sampled next tokens [N] int64 of launch.last_index."""
+
+    @abstractmethod
+    def coda(self, bank: torch.Tensor, slots: torch.Tensor, n: int) -> torch.Tensor:
+        """Greedy next tokens [n] int64 for the hidden states in bank rows slots[:n]."""
+
+
+def resolve_cdb_model_adapter(model: Any, adapter: CDBModelAdapter | None = None) -> CDBModelAdapter:
+    """Explicit adapter, or one inferred from the model type (model_adapter.py:105-122)."""
+
+    if adapter is not None:
+        if not isinstance(adapter, CDBModelAdapter):
+            raise TypeError(f"model_adapter must inherit CDBModelAdapter, got {type(adapter)!r}")
+        return adapter
+    model_type = getattr(getattr(model, "config", None), "model_type", None)
+    if model_type == "ouro":
+        from .ouro import OuroCDBAdapter
+
+        if OuroCDBAdapter.supports(model):
+            return OuroCDBAdapter(model)
+    if model_type == "huginn_raven":
+        from .huginn import HuginnCDBAdapter
+
+        if HuginnCDBAdapter.supports(model):
+            return HuginnCDBAdapter(model)
+    raise TypeError(f"Continuous depth batching requires an explicit model adapter or a supported looped model; "
+                    f"got {type(model)!r}")

@@ -1,0 +1,439 @@
+"""CDB stage runner: device buffers, hidden-state bank, HIP graphs, readbacks.
+
+Counterpart of continuous_depth_batching/model_runner.py. Differences that
+follow from the MI355X design:
+  * the hidden-state bank and the exit-gate state are fixed-capacity device
+    arrays indexed by hidden slot; slots are handed out LIFO from a free list,
+    then by monotonic growth, exactly like the reference (:1193-1203), so slot
+    assignment is reproducible;
+  * a recurrent launch uploads one packed int32 and one int64 metadata buffer
+    (bank slots, positions, block-table rows, cache-layer offsets, steps,
+    replayed depths); block tables stay resident on the device;
+  * the whole recurrent stage -- bank gather, every layer, bank scatter and
+    the exit decision -- is one HIP graph per batch bucket (captured on first
+    use of the bucket); padding rows carry slot -1 / position -1 and are no-ops
+    in every kernel;
+  * exit decisions come back as one byte per row.
+"""
+
+from __future__ import annotations
+
+import gc
+from contextlib import contextmanager
+from dataclasses import dataclass, field
+from typing import Any, Iterator, Sequence
+
+import numpy as np
+import torch
+
+from . import ops
+from .cache import PagedKVCache
+from .config import ContinuousDepthBatchingConfig
+from .exit_policy import ExitDecisionRule, ExitPolicy
+from .model_adapter import CDBModelAdapter, GateLaunch, PrefillLaunch, RecurrentLaunch
+from .requests import TMP_TOKEN_ID, DepthWorkItem, FutureRequestState
+
+CODA_PIPELINE_DEPTH = 2
+
+
+def decode_graph_buckets(max_num_seqs: int) -> list[int]:
+    """Batch buckets of the decode graphs (continuous_batching/utils.py:65-76)."""
+
+    buckets = {1, 2, 4, 8, 12}
+    buckets.update(range(16, min(256, max_num_seqs) + 1, 8))
+    if max_num_seqs > 256:
+        buckets.update(range(272, min(512, max_num_seqs) + 1, 16))
+    if max_num_seqs > 512:
+        buckets.update(range(544, max_num_seqs + 1, 32))
+    buckets.add(max_num_seqs)
+    return sorted(b for b in buckets if b <= max_num_seqs)
+
+
+def pad_to_bucket(n: int, buckets: Sequence[int]) -> int:
+    for b in buckets:
+        if b >= n:
+            return b
+    raise ValueError(f"batch of {n} exceeds the largest bucket {buckets[-1]}")
+
+
+@contextmanager
+def gc_paused() -> Iterator[None]:
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if enabled:
+            gc.enable()
+
+
+@dataclass
+class PendingCodaResult:
+    items: list[DepthWorkItem]
+    host_tokens: torch.Tensor
+    device_tokens: torch.Tensor | None = None
+    ready_event: Any | None = None
+    eager_reentries: list[bool] | None = None
+
+    def is_ready(self) -> bool:
+        return self.ready_event is None or self.ready_event.query()
+
+
+@dataclass
+class PendingPrefillResult:
+    futures: list[FutureRequestState]
+    host_tokens: torch.Tensor
+    device_tokens: torch.Tensor | None = None
+    ready_event: Any | None = None
+    eager_entries: list[bool] | None = None
+
+    def is_ready(self) -> bool:
+        return self.ready_event is None or self.ready_event.query()
+
+
+@dataclass
+class PendingFlags:
+    """Exit decisions of one launch, on their way to the host."""
+
+    host: torch.Tensor
+    event: Any | None
+
+    def get(self, index: int) -> bool:
+        if self.event is not None:
+            self.event.synchronize()
+            self.event = None
+        return bool(self.host[index])
+
+
+@dataclass
+class _RecurrentBucket:
+    rows: int
+    host_i64: torch.Tensor
+    host_i32: torch.Tensor
+    dev_i64: torch.Tensor
+    dev_i32: torch.Tensor
+    launch: RecurrentLaunch
+    staged: Any | None = None
+    graph: torch.cuda.CUDAGraph | None = None
+    turn: int = 0
+    host_flags: list[torch.Tensor] = field(default_factory=list)
+    flag_events: list[Any] = field(default_factory=list)
+
+
+class ModelRunner:
+    META_POSITIONS, META_TABLE_ROWS, META_LAYER_OFFSET, META_STEPS, META_SYNTHETIC = range(5)
+    FLAG_TURNS = 4
+
+    def __init__(self, *, engine_config: ContinuousDepthBatchingConfig, cache: PagedKVCache,
+                 model_adapter: CDBModelAdapter, exit_policy: ExitPolicy) -> None:
+        self.engine_config = engine_config
+        self.cache = cache
+        self.adapter = model_adapter
+        self.exit_policy = exit_policy
+        self.device = cache.device
+        self.dtype = model_adapter.dtype
+        self.max_num_seqs = engine_config.max_num_seqs
+        self.decode_graph_buckets = decode_graph_buckets(self.max_num_seqs)
+        self.use_graphs = bool(engine_config.use_cuda_graph)
+        self.layout = cache.layout
+        self.stream = torch.cuda.Stream(device=self.device)
+        self.bank_capacity = 4 * self.max_num_seqs + 64
+        self.bank = torch.zeros((self.bank_capacity, model_adapter.hidden_width), dtype=self.dtype,
+                                device=self.device)
+        self.gate_state = ops.GateState.allocate(self.bank_capacity, self.device)
+        self.free_hidden_slots: list[int] = []
+        self.next_hidden_slot = 0
+        max_bucket = self.decode_graph_buckets[-1]
+        num_kv_heads, head_dim = model_adapter.kv_geometry()
+        self.split_pages = {b: ops.default_split_pages(b, cache.block_size) for b in self.decode_graph_buckets}
+        ws_bytes = max(ops.decode_workspace_bytes(b, max(model_adapter_num_heads(model_adapter), 1), head_dim,
+                                                  engine_config.max_model_len, cache.block_size, sp)
+                       for b, sp in self.split_pages.items() if b == max_bucket or b <= max_bucket)
+        self.workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=self.device)
+        self._buckets: dict[int, _RecurrentBucket] = {}
+        self.graph_pool = torch.cuda.graph_pool_handle() if self.use_graphs else None
+        spec = model_adapter.exit_policy_spec()
+        self.gate_rule = ops.RULE_DIRECT_THRESHOLD if spec.rule is ExitDecisionRule.DIRECT_THRESHOLD \
+            else ops.RULE_CUMULATIVE_HAZARD
+        self.delayed = exit_policy.delayed()
+        self.recurrent_graph_hits = 0
+        self.recurrent_graph_captures = 0
+        self.stage_graph_hits = 0
+        self.stage_graph_captures = 0
+
+    # -- hidden slots (cdb/model_runner.py:1193-1203, 1359-1363) ------------------------------------------------
+    def reset_cdb_runtime_counters(self) -> None:
+        self.recurrent_graph_hits = self.recurrent_graph_captures = 0
+        self.stage_graph_hits = self.stage_graph_captures = 0
+        self.free_hidden_slots = []
+        self.next_hidden_slot = 0
+
+    def allocate_hidden_slots(self, count: int) -> list[int]:
+        slots = []
+        while self.free_hidden_slots and len(slots) < count:
+            slots.append(self.free_hidden_slots.pop())
+        while len(slots) < count:
+            if self.next_hidden_slot >= self.bank_capacity:
+                raise RuntimeError(f"hidden-state bank exhausted ({self.bank_capacity} slots)")
+            slots.append(self.next_hidden_slot)
+            self.next_hidden_slot += 1
+        return slots
+
+    def release_hidden_slots(self, items: list[DepthWorkItem]) -> None:
+        for item in items:
+            if item.hidden_slot is not None:
+                self.free_hidden_slots.append(item.hidden_slot)
+                item.hidden_slot = None
+
+    # -- helpers --------------------------------------------------------------------------------------------------
+    def _pinned(self, shape: tuple[int, ...] | int, dtype: torch.dtype) -> torch.Tensor:
+        return torch.empty(shape, dtype=dtype, pin_memory=True)
+
+    def _to_device(self, array: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+        host = self._pinned(array.shape, dtype)
+        host.numpy()[...] = array
+        return host.to(self.device, non_blocking=True)
+
+    # -- prelude ---------------------------------------------------------------------------------------------------
+    def compute_prelude_batch(self, items: list[DepthWorkItem],
+                              device_groups: Sequence[tuple[Any, list[int]]] = ()) -> None:
+        """Embed the items' tokens into fresh bank slots; the first ``sum(len(rows))`` items take their
+        token from the staged results' device tokens (cdb/model_runner.py:395-463)."""
+
+        if not items:
+            return
+        n = len(items)
+        num_device = sum(len(rows) for _, rows in device_groups)
+        if any(item.token_id != TMP_TOKEN_ID for item in items[:num_device]):
+            raise AssertionError("device_groups must cover a prefix of items")
+        slots = self.allocate_hidden_slots(n)
+        with torch.cuda.stream(self.stream):
+            tokens = torch.empty((n, 1), dtype=torch.int64, device=self.device)
+            offset = 0
+            for result, rows in device_groups:
+                if result.device_tokens is None:
+                    raise RuntimeError("Cannot gather prelude tokens from a staged result that carries none")
+                idx = self._to_device(np.asarray(rows, dtype=np.int64), torch.int64)
+                src = result.device_tokens.view(-1, 1)
+                ops.copy_rows_raw(src, idx, tokens[offset:offset + len(rows)], None, len(rows))
+                offset += len(rows)
+            if n > num_device:
+                host_ids = np.fromiter((item.token_id for item in items[num_device:]), dtype=np.int64,
+                                       count=n - num_device)
+                tokens[num_device:].copy_(self._to_device(host_ids.reshape(-1, 1), torch.int64))
+            slot_dev = self._to_device(np.asarray(slots, dtype=np.int64), torch.int64)
+            self.adapter.prelude(tokens.view(-1), self.bank, slot_dev, n)
+            self.gate_state.reset(slot_dev, n)
+        for item, slot in zip(items, slots):
+            item.hidden_slot = slot
+
+    # -- recurrent stage -------------------------------------------------------------------------------------
+    def _bucket(self, rows: int) -> _RecurrentBucket:
+        b = self._buckets.get(rows)
+        if b is not None:
+            return b
+        host_i64 = self._pinned((rows,), torch.int64)
+        host_i32 = self._pinned((5, rows), torch.int32)
+        dev_i64 = torch.full((rows,), -1, dtype=torch.int64, device=self.device)
+        dev_i32 = torch.zeros((5, rows), dtype=torch.int32, device=self.device)
+        dev_i32[self.META_POSITIONS].fill_(-1)
+        dev_i32[self.META_SYNTHETIC].fill_(-1)
+        policy = self.exit_policy
+        gate = GateLaunch(
+            state=self.gate_state,
+            steps=dev_i32[self.META_STEPS],
+            synthetic=dev_i32[self.META_SYNTHETIC],
+            flags=torch.zeros(rows, dtype=torch.uint8, device=self.device),
+            signal=torch.zeros(rows, dtype=self.dtype, device=self.device),
+            rule=self.gate_rule,
+            # The synchronous path reads the model-dtype hazard; the delayed path the fp32 one
+            # (cdb/model_runner.py:807-813 vs continuous_api.py:1693-1697).
+            round_hazard=not self.delayed,
+            min_steps=policy.min_recurrent_steps,
+            max_steps=policy.max_recurrent_steps,
+            threshold=policy.threshold,
+        )
+        launch = RecurrentLaunch(
+            rows=rows, bank=self.bank, bank_slots=dev_i64, positions=dev_i32[self.META_POSITIONS],
+            table_rows=dev_i32[self.META_TABLE_ROWS], slot_offset=dev_i32[self.META_LAYER_OFFSET],
+            cache=self.cache, workspace=self.workspace, split_pages=self.split_pages.get(rows, 8), gate=gate)
+        b = _RecurrentBucket(rows=rows, host_i64=host_i64, host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32,
+                             launch=launch)
+        b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]
+        b.flag_events = [None] * self.FLAG_TURNS
+        self._buckets[rows] = b
+        return b
+
+    def compute_recurrent_batch(self, items: list[DepthWorkItem]) -> PendingFlags:
+        """One recurrent step over ``items``; returns their exit decisions (host-visible later)."""
+
+        if not items:
+            raise ValueError("items must not be empty")
+        n = len(items)
+        rows = pad_to_bucket(n, self.decode_graph_buckets)
+        b = self._bucket(rows)
+        if b.staged is not None:
+            b.staged.synchronize()  # the previous upload from these pinned buffers has completed
+        base = self.layout.core_base
+        core = self.layout.num_core_layers
+        slot_for = self.layout.slot_for_step
+        i64 = b.host_i64.numpy()
+        i32 = b.host_i32.numpy()
+        i64[:n] = [item.hidden_slot for item in items]
+        i32[self.META_POSITIONS, :n] = [item.token_position for item in items]
+        row_of = self.cache.table_row_of
+        i32[self.META_TABLE_ROWS, :n] = [row_of[item.state.request_id] for item in items]
+        steps = [item.recurrent_step for item in items]
+        i32[self.META_STEPS, :n] = steps
+        i32[self.META_LAYER_OFFSET, :n] = [base + slot_for(s) * core for s in steps]
+        i32[self.META_SYNTHETIC, :n] = [-1 if (d := item.synthetic_exit_depth) is None or not item.apply_exit_gate
+                                        else d for item in items]
+        if rows > n:
+            i64[n:] = -1
+            i32[self.META_POSITIONS, n:] = -1
+            i32[self.META_TABLE_ROWS, n:] = 0
+            i32[self.META_LAYER_OFFSET, n:] = base
+            i32[self.META_STEPS, n:] = 0
+            i32[self.META_SYNTHETIC, n:] = -1
+        turn = b.turn
+        b.turn = (turn + 1) % self.FLAG_TURNS
+        if b.flag_events[turn] is not None:
+            b.flag_events[turn].synchronize()
+        with torch.cuda.stream(self.stream):
+            self.cache.flush_table_updates()
+            b.dev_i64.copy_(b.host_i64, non_blocking=True)
+            b.dev_i32.copy_(b.host_i32, non_blocking=True)
+            if b.staged is None:
+                b.staged = torch.cuda.Event()
+            b.staged.record()
+            self._run_recurrent(b)
+            host_flags = b.host_flags[turn]
+            host_flags[:n].copy_(b.launch.gate.flags[:n], non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+            b.flag_events[turn] = event
+        return PendingFlags(host=host_flags, event=event)
+
+    def _run_recurrent(self, b: _RecurrentBucket) -> None:
+        if not self.use_graphs:
+            self.adapter.recurrent_step(b.launch)
+            return
+        if b.graph is not None:
+            self.recurrent_graph_hits += 1
+            b.graph.replay()
+            return
+        # First use of this bucket: run it eagerly (this launch's real work), then capture.
+        with gc_paused():
+            self.adapter.recurrent_step(b.launch)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=self.stream, pool=self.graph_pool, capture_error_mode="thread_local"):
+                self.adapter.recurrent_step(b.launch)
+        b.graph = graph
+        self.recurrent_graph_captures += 1
+
+    # -- coda --------------------------------------------------------------------------------------------------
+    def stage_coda_batch(self, items: list[DepthWorkItem], *, allow_async: bool = True) -> PendingCodaResult:
+        if not items:
+            return PendingCodaResult(items=[], host_tokens=torch.empty(0, dtype=torch.int64))
+        for item in items:
+            item.state.tokens_in_flight += 1
+        n = len(items)
+        with torch.cuda.stream(self.stream):
+            slots = self._to_device(np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n),
+                                    torch.int64)
+            tokens = self.adapter.coda(self.bank, slots, n)
+            host = self._pinned((n,), torch.int64)
+            host.copy_(tokens, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+        if not allow_async:
+            event.synchronize()
+        return PendingCodaResult(items=items, host_tokens=host, device_tokens=tokens, ready_event=event)
+
+    def consume_coda_result(self, pending: PendingCodaResult) -> list[int]:
+        if pending.ready_event is not None:
+            pending.ready_event.synchronize()
+        tokens = pending.host_tokens.tolist()
+        self.release_hidden_slots(pending.items)
+        return tokens
+
+    # -- prefill -----------------------------------------------------------------------------------------------
+    def stage_prefill_batch(self, requests: list[FutureRequestState], *, allow_async: bool = True) -> PendingPrefillResult:
+        """Full-depth prefill of the scheduled prompt chunks (cb/input_outputs.py:269-379 bookkeeping)."""
+
+        cache = self.cache
+        tokens: list[int] = []
+        positions: list[np.ndarray] = []
+        rows: list[np.ndarray] = []
+        cu_q = [0]
+        past: list[int] = []
+        table_rows: list[int] = []
+        lens: list[int] = []
+        last_index: list[int] = []
+        for future in requests:
+            state = future.state
+            qlen = future.query_length
+            p0 = state.position_offset
+            tokens.extend(state.tokens_to_process)
+            positions.append(np.arange(p0, p0 + qlen, dtype=np.int32))
+            rows.append(cache.write_rows(state.request_id, p0, qlen))
+            state.position_offset += qlen
+            cu_q.append(cu_q[-1] + qlen)
+            past.append(p0)
+            table_rows.append(cache.table_row_of[state.request_id])
+            lens.append(qlen)
+            if future.has_new_token:
+                last_index.append(cu_q[-1] - 1)
+                state.tokens_to_process = [TMP_TOKEN_ID]
+                state.tokens_in_flight += 1
+        tile_seq, tile_q0 = ops.prefill_tiles(lens)
+        with torch.cuda.stream(self.stream):
+            cache.flush_table_updates()
+            launch = PrefillLaunch(
+                tokens=self._to_device(np.asarray(tokens, dtype=np.int64), torch.int64),
+                positions=self._to_device(np.concatenate(positions), torch.int32),
+                write_rows=self._to_device(np.concatenate(rows), torch.int64),
+                cu_q=self._to_device(np.asarray(cu_q, dtype=np.int32), torch.int32),
+                past=self._to_device(np.asarray(past, dtype=np.int32), torch.int32),
+                table_rows=self._to_device(np.asarray(table_rows, dtype=np.int32), torch.int32),
+                tile_seq=self._to_device(tile_seq, torch.int32),
+                tile_q0=self._to_device(tile_q0, torch.int32),
+                last_index=self._to_device(np.asarray(last_index, dtype=np.int64), torch.int64),
+                cache=cache,
+            )
+            if last_index:
+                device_tokens = self.adapter.prefill(launch)
+            else:
+                self.adapter.prefill(launch)
+                device_tokens = torch.empty(0, dtype=torch.int64, device=self.device)
+            host = self._pinned((len(last_index),), torch.int64)
+            host.copy_(device_tokens, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+        if not allow_async:
+            event.synchronize()
+        return PendingPrefillResult(futures=list(requests), host_tokens=host, device_tokens=device_tokens,
+                                    ready_event=event)
+
+    def consume_prefill_result(self, pending: PendingPrefillResult) -> list[int]:
+        if pending.ready_event is not None:
+            pending.ready_event.synchronize()
+        return pending.host_tokens.tolist()
+
+    # -- exit-KV propagation ------------------------------------------------------------------------------------
+    def copy_exit_kv(self, rows: list[int], exit_steps: list[int]) -> None:
+        if not rows:
+            return
+        slots = [self.layout.slot_for_step(s) for s in exit_steps]
+        with torch.cuda.stream(self.stream):
+            ops.exit_kv_copy_raw(self.cache.view, self._to_device(np.asarray(rows, dtype=np.int64), torch.int64),
+                                 self._to_device(np.asarray(slots, dtype=np.int32), torch.int32), len(rows),
+                                 layer_base=self.layout.core_base, core_layers=self.layout.num_core_layers,
+                                 num_slots=self.layout.slots_per_layer)
+
+    def synchronize(self) -> None:
+        self.stream.synchronize()
+
+
+def model_adapter_num_heads(adapter: CDBModelAdapter) -> int:
+    return int(getattr(adapter, "num_heads", 1))

@@ -144,8 +144,13 @@ def paged_decode_attention_raw(
     if workspace.dtype != torch.float32:
         raise TypeError("workspace must be float32")
     _require_cuda(q, k_new, v_new, cache_layer, block_table, table_row, seqlens, rope_cos, rope_sin, out, workspace)
-    _require_contiguous(q=q, k_new=k_new, v_new=v_new, block_table=block_table, seqlens=seqlens, out=out,
-                        rope_cos=rope_cos, rope_sin=rope_sin, q_bias=q_bias, k_bias=k_bias)
+    for name, t in (("q", q), ("k_new", k_new), ("v_new", v_new)):
+        if t.stride(2) != 1 or t.stride(1) != head_dim:
+            raise ValueError(f"{name} must have contiguous heads and head dimension (row stride may differ)")
+    if k_new.stride(0) != v_new.stride(0):
+        raise ValueError("k_new and v_new must share a row stride")
+    _require_contiguous(block_table=block_table, seqlens=seqlens, out=out, rope_cos=rope_cos, rope_sin=rope_sin,
+                        q_bias=q_bias, k_bias=k_bias)
     _require_int32(cache_layer=cache_layer, block_table=block_table, table_row=table_row, seqlens=seqlens)
     code = _lib.lib().cdb_paged_decode_attention(
         q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_pool_ptr, v_pool_ptr,
@@ -157,7 +162,7 @@ def paged_decode_attention_raw(
         _ptr(q_bias), _ptr(k_bias),
         out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4,
         num_rows, num_heads, num_kv_heads, head_dim, block_size, split_pages,
-        scale, dtype_code(q.dtype), _stream(),
+        scale, q.stride(0), k_new.stride(0), dtype_code(q.dtype), _stream(),
     )
     _lib.check(code, "cdb_paged_decode_attention")
     return out

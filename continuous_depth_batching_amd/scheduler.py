@@ -1,0 +1,334 @@
+"""CDB scheduler: prompt admission, the mixed-depth ready queue and the coda queue.
+
+One tick schedules one homogeneous bucket, in priority order coda (once
+``min_coda_batch_size`` tokens wait) > prefill (when admission allows) >
+recurrent > an undersized coda flush (continuous_depth_batching/scheduler.py:101-140).
+Recurrent work is a FIFO deque; a stepped batch's survivors and freshly
+sampled successors return to its head in launch order, which keeps a bounded
+working set advancing (:142-180). Under multi-slot KV layouts a recurrent
+batch holds only items writing the same slot (:322-346). Admission, token
+budgets and block allocation follow scheduler_base.py:171-545.
+"""
+
+from __future__ import annotations
+
+from collections import deque
+from dataclasses import dataclass
+from itertools import islice
+from typing import Literal
+
+from .cache import PagedKVCache
+from .config import resolve_min_free_slots
+from .requests import DepthWorkItem, FutureRequestState, RequestState, RequestStatus, logger
+
+ScheduledKind = Literal["prefill", "coda", "recurrent"]
+
+
+def reserved_peak_blocks(initial_len: int, max_new_tokens: int | None, max_model_len: int, block_size: int) -> int:
+    """Worst-case blocks a request can hold (utils.py:107-129)."""
+
+    total = max_model_len if max_new_tokens is None else min(initial_len + max_new_tokens, max_model_len)
+    return -(-total // block_size)
+
+
+@dataclass
+class ScheduledCDBBatch:
+    kind: ScheduledKind
+    requests: list[FutureRequestState] | None = None
+    depth_items: list[DepthWorkItem] | None = None
+    num_q_tokens: int = 0
+    max_kv_read: int = 0
+
+
+class CDBScheduler:
+    def __init__(self, cache: PagedKVCache, max_recurrent_steps: int, *, safety_margin: float = 0.2,
+                 kv_pressure_mode: str = "recompute", max_model_len: int | None = None, max_num_seqs: int = 256,
+                 min_free_slots: int | None = None, min_coda_batch_size: int = 1) -> None:
+        if max_recurrent_steps <= 0:
+            raise ValueError(f"max_recurrent_steps must be positive, got {max_recurrent_steps}")
+        if min_coda_batch_size <= 0:
+            raise ValueError(f"min_coda_batch_size must be positive, got {min_coda_batch_size}")
+        if max_num_seqs <= 0:
+            raise ValueError(f"max_num_seqs must be positive, got {max_num_seqs}")
+        self.cache = cache
+        self.max_num_seqs = min(max_num_seqs, cache.max_num_batched_tokens)
+        self.safety_margin = 0.0 if kv_pressure_mode == "reserve" else safety_margin
+        self.kv_pressure_mode = kv_pressure_mode
+        self.max_model_len = max_model_len
+        self.max_decode_fast_path_length = cache.max_blocks_per_request * cache.block_size
+        self.min_free_slots = resolve_min_free_slots(min_free_slots, self.max_num_seqs)
+        self.max_recurrent_steps = max_recurrent_steps
+        self.min_coda_batch_size = min(min_coda_batch_size, self.max_num_seqs)
+        if kv_pressure_mode == "reserve":
+            if max_model_len is None:
+                raise ValueError("kv_pressure_mode='reserve' requires max_model_len")
+            peak = reserved_peak_blocks(0, max_model_len, max_model_len, cache.block_size)
+            if peak > cache.num_blocks:
+                raise ValueError(f"kv_pressure_mode='reserve' cannot serve a max-length request: needs {peak} "
+                                 f"blocks but the cache has {cache.num_blocks}")
+        self.reset()
+
+    def reset(self) -> None:
+        self.active_requests: dict[str, RequestState] = {}
+        self.waiting_requests: dict[str, RequestState] = {}
+        self.waiting_requests_order: deque[str] = deque()
+        self.block_new_requests = False
+        self.ready_queue: deque[DepthWorkItem] = deque()
+        self.coda_queue: deque[DepthWorkItem] = deque()
+        self.mixed_batches_scheduled = 0
+        self.refill_events = 0
+        self.max_depth_queue_size = 0
+        self.in_flight_request_ids: set[str] = set()
+        self.max_in_flight_requests = 0
+        self.max_live_requests = 0
+        self.max_resident_requests = 0
+        self.resident_samples = 0
+        self.resident_sum = 0
+        self.completed_requests = 0
+        self.completed_generated_tokens = 0
+
+    # -- bookkeeping -------------------------------------------------------------------------------------------
+    def add_waiting_request(self, state: RequestState) -> None:
+        self.waiting_requests[state.request_id] = state
+        self.waiting_requests_order.append(state.request_id)
+
+    def has_pending_work(self) -> bool:
+        return bool(self.coda_queue or self.ready_queue or self.active_requests or self.waiting_requests)
+
+    def has_decode_work(self) -> bool:
+        return any(s.status == RequestStatus.DECODING for s in self.active_requests.values())
+
+    def record_resident_sample(self) -> None:
+        resident = len(self.active_requests)
+        self.max_resident_requests = max(self.max_resident_requests, resident)
+        self.resident_samples += 1
+        self.resident_sum += resident
+
+    def record_completion(self, state: RequestState) -> None:
+        self.completed_requests += 1
+        self.completed_generated_tokens += state.total_generated_len()
+
+    def finish_request(self, request_id: str) -> None:
+        self.cache.free_blocks(request_id)
+        self.active_requests.pop(request_id, None)
+        self.in_flight_request_ids.discard(request_id)
+        if self.waiting_requests.pop(request_id, None) is not None:
+            self.waiting_requests_order.remove(request_id)
+
+    def free_unfinished_requests(self) -> None:
+        for request_id in list(self.active_requests):
+            self.finish_request(request_id)
+        for request_id in list(self.waiting_requests):
+            self.finish_request(request_id)
+
+    def release_in_flight_request(self, request_id: str) -> None:
+        self.in_flight_request_ids.discard(request_id)
+
+    def _mark_request_in_flight(self, request_id: str) -> None:
+        self.in_flight_request_ids.add(request_id)
+        self.max_in_flight_requests = max(self.max_in_flight_requests, len(self.in_flight_request_ids))
+        self.max_live_requests = max(self.max_live_requests, len(self.active_requests) + len(self.waiting_requests))
+
+    # -- admission (scheduler_base.py:171-201, 416-531) --------------------------------------------------------
+    def has_prefill_headroom(self) -> bool:
+        return self.cache.get_num_free_blocks() > self.safety_margin * self.cache.num_blocks
+
+    def admit_prefill(self, has_decode_work: bool) -> bool:
+        return not has_decode_work or self.has_prefill_headroom()
+
+    def free_residency_slots(self) -> int:
+        return max(0, self.max_num_seqs - len(self.active_requests))
+
+    def admit_prefill_batch(self, candidates: list[RequestState]) -> bool:
+        if not candidates:
+            return False
+        if any(s.status == RequestStatus.PREFILLING for s in candidates):
+            return True
+        return self.free_residency_slots() >= self.min_free_slots
+
+    def _prefill_admits(self, state: RequestState) -> bool:
+        return state.request_id not in self.in_flight_request_ids
+
+    def _get_waiting_candidates(self, limit: int | None = None) -> list[RequestState]:
+        fresh = (self.waiting_requests[r] for r in self.waiting_requests_order
+                 if not self.waiting_requests[r].is_cpu_offloaded)
+        return list(islice(fresh, limit))
+
+    def get_prefill_bucket(self) -> list[RequestState]:
+        prefilling = [s for s in self.active_requests.values()
+                      if s.status == RequestStatus.PREFILLING and self._prefill_admits(s)]
+        if self.block_new_requests:
+            return prefilling
+        admissible = self._get_waiting_candidates(limit=self.free_residency_slots())
+        if self.kv_pressure_mode == "reserve":
+            committed = sum(reserved_peak_blocks(len(s.initial_tokens), s.max_new_tokens, self.max_model_len,
+                                                 self.cache.block_size) for s in self.active_requests.values())
+            fitting = []
+            for s in admissible:
+                need = reserved_peak_blocks(len(s.initial_tokens), s.max_new_tokens, self.max_model_len,
+                                            self.cache.block_size)
+                if committed + need > self.cache.num_blocks:
+                    break
+                committed += need
+                fitting.append(s)
+            admissible = fitting
+        return prefilling + admissible
+
+    def get_prefill_candidates(self) -> list[RequestState]:
+        candidates = self.get_prefill_bucket()
+        return candidates if self.admit_prefill_batch(candidates) else []
+
+    def _cleanup_waiting_queue(self, ids: set[str]) -> None:
+        remaining = set(ids)
+        order = self.waiting_requests_order
+        while remaining and order and order[0] in remaining:
+            remaining.discard(order.popleft())
+        if remaining:
+            self.waiting_requests_order = deque(r for r in order if r not in remaining)
+
+    def _allocate_blocks_if_needed(self, state: RequestState, len_next_tokens: int) -> bool:
+        current = state.current_len()
+        if state.allocated_blocks * self.cache.block_size - current < len_next_tokens:
+            needed = -(-(current + len_next_tokens) // self.cache.block_size) - state.allocated_blocks
+            got = self.cache.allocate_blocks(needed, state.request_id, state.allocated_blocks)
+            if got is None:
+                return False
+            state.allocated_blocks += got
+        return True
+
+    # -- bucket selection (continuous_depth_batching/scheduler.py:101-349) ------------------------------------
+    def schedule_next(self, token_budget: int, cache_budget: int, *, allow_coda: bool = True) -> ScheduledCDBBatch | None:
+        self.record_resident_sample()
+        if allow_coda and len(self.coda_queue) >= self.min_coda_batch_size:
+            batch = self._schedule_coda_batch()
+            if batch:
+                return ScheduledCDBBatch(kind="coda", depth_items=batch)
+        if self.admit_prefill(self.has_decode_work()):
+            prefill = self.schedule_prefill_batch(token_budget=token_budget, cache_budget=cache_budget)
+            if prefill is not None:
+                return prefill
+        recurrent = self._schedule_recurrent_batch()
+        if recurrent:
+            return ScheduledCDBBatch(kind="recurrent", depth_items=recurrent)
+        if allow_coda:
+            batch = self._schedule_coda_batch()
+            if batch:
+                return ScheduledCDBBatch(kind="coda", depth_items=batch)
+        return None
+
+    def enqueue_depth(self, item: DepthWorkItem, *, front: bool = False) -> None:
+        if not 0 <= item.recurrent_step < self.max_recurrent_steps:
+            raise ValueError(f"recurrent_step must be in [0, {self.max_recurrent_steps}), got {item.recurrent_step}")
+        self._mark_request_in_flight(item.state.request_id)
+        if item.recurrent_step == 0 and self.ready_queue:
+            self.refill_events += 1
+        if front:
+            self.ready_queue.appendleft(item)
+        else:
+            self.ready_queue.append(item)
+        self.max_depth_queue_size = max(self.max_depth_queue_size, len(self.ready_queue))
+
+    def enqueue_depth_front(self, items: list[DepthWorkItem]) -> None:
+        """Return items to the queue head preserving their order."""
+
+        for item in reversed(items):
+            self.enqueue_depth(item, front=True)
+
+    def enqueue_coda(self, item: DepthWorkItem) -> None:
+        self._mark_request_in_flight(item.state.request_id)
+        self.coda_queue.append(item)
+
+    def schedule_prefill_batch(self, token_budget: int, cache_budget: int) -> ScheduledCDBBatch | None:
+        candidates = self.get_prefill_candidates()
+        if not candidates:
+            return None
+        to_remove: set[str] = set()
+        scheduled, num_q_tokens, max_kv_read = self._process_prefill_candidates(candidates, token_budget,
+                                                                                cache_budget, to_remove)
+        self._cleanup_waiting_queue(to_remove)
+        if not scheduled:
+            return None
+        return ScheduledCDBBatch(kind="prefill", requests=scheduled, num_q_tokens=num_q_tokens,
+                                 max_kv_read=max_kv_read)
+
+    def _process_prefill_candidates(self, candidates: list[RequestState], token_budget: int, cache_budget: int,
+                                    to_remove: set[str]) -> tuple[list[FutureRequestState], int, int]:
+        scheduled: list[FutureRequestState] = []
+        decode_fast_path = True
+        margin_blocks = self.safety_margin * self.cache.num_blocks
+        original_tokens, original_cache = token_budget, cache_budget
+        for state in candidates:
+            free = self.cache.get_num_free_blocks()
+            if free < margin_blocks and scheduled:
+                break
+            tokens = state.remaining_prefill_tokens
+            request_len = min(len(tokens), token_budget)
+            if request_len == 0:
+                continue
+            eligible = request_len == 1 and state.position_offset < self.max_decode_fast_path_length
+            read_needed = state.current_len()
+            if not (decode_fast_path and eligible) and cache_budget < read_needed:
+                continue
+            if not self._allocate_blocks_if_needed(state, request_len):
+                if free == 0 and state.request_id in self.waiting_requests:
+                    break
+                continue
+            self._schedule_prefill_request(state, tokens, request_len, to_remove)
+            self._mark_request_in_flight(state.request_id)
+            request_len = len(state.tokens_to_process)
+            decode_fast_path &= request_len == 1 and state.position_offset < self.max_decode_fast_path_length
+            token_budget -= request_len
+            cache_budget -= read_needed
+            scheduled.append(FutureRequestState(state, not state.remaining_prefill_tokens, request_len))
+            if self.waiting_requests.pop(state.request_id, None) is not None:
+                to_remove.add(state.request_id)
+            if token_budget == 0 or (cache_budget <= 0 and not decode_fast_path):
+                break
+        return scheduled, original_tokens - token_budget, original_cache - cache_budget
+
+    def _schedule_prefill_request(self, state: RequestState, tokens: list[int], request_len: int,
+                                  to_remove: set[str]) -> None:
+        if len(tokens) <= request_len:
+            if state.status == RequestStatus.PENDING:
+                self.active_requests[state.request_id] = state
+                to_remove.add(state.request_id)
+            if state.status <= RequestStatus.PREFILLING:
+                state.tokens_to_process = state.remaining_prefill_tokens
+                state.remaining_prefill_tokens = []
+                state.status = RequestStatus.DECODING
+            return
+        if state.status == RequestStatus.PENDING:
+            self.active_requests[state.request_id] = state
+            state.status = RequestStatus.PREFILLING
+            to_remove.add(state.request_id)
+        state.remaining_prefill_tokens = tokens[request_len:]
+        state.tokens_to_process = tokens[:request_len]
+
+    def _schedule_recurrent_batch(self) -> list[DepthWorkItem]:
+        size = min(self.max_num_seqs, len(self.ready_queue))
+        if size == 0:
+            return []
+        first = self.ready_queue.popleft()
+        batch = [first]
+        if self.cache.requires_slot_homogeneous_recurrent_batches:
+            target = self.cache.kv_slot_for_recurrent_step(first.recurrent_step)
+            deferred: deque[DepthWorkItem] = deque()
+            while self.ready_queue and len(batch) < size:
+                item = self.ready_queue.popleft()
+                if self.cache.kv_slot_for_recurrent_step(item.recurrent_step) == target:
+                    batch.append(item)
+                else:
+                    deferred.append(item)
+            deferred.extend(self.ready_queue)
+            self.ready_queue = deferred
+        else:
+            while self.ready_queue and len(batch) < size:
+                batch.append(self.ready_queue.popleft())
+        self.mixed_batches_scheduled += 1
+        return batch
+
+    def _schedule_coda_batch(self) -> list[DepthWorkItem]:
+        return [self.coda_queue.popleft() for _ in range(min(self.max_num_seqs, len(self.coda_queue)))]
+
+
+__all__ = ["CDBScheduler", "ScheduledCDBBatch", "reserved_peak_blocks", "logger"]

@@ -60,7 +60,10 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
  * (rounded to the model dtype for Ouro); rope_style 0 applies no rotation.
  * q_bias [H,D] / k_bias [Hkv,D] are optional pre-rotation biases (Huginn's
  * qk_bias). Rows whose position or cache layer is out of range get a NaN
- * output and no KV write. workspace: cdb_paged_decode_workspace_bytes(...). */
+ * output and no KV write. workspace: cdb_paged_decode_workspace_bytes(...).
+ * q_stride / kv_stride: elements between consecutive rows of q and of
+ * k_new/v_new (0 = dense), so q, k and v may be column slices of one fused
+ * QKV projection output. */
 int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
                                int64_t layer_stride, int32_t num_cache_layers, int64_t pool_blocks,
                                const int32_t* cache_layer, int32_t cache_layer0, const int32_t* block_table,
@@ -69,7 +72,7 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t max_positions, const void* q_bias, const void* k_bias, void* out,
                                void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
-                               float scale, int32_t dtype, hipStream_t stream);
+                               float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
 
 /* Fused RMSNorm sandwich over rows of `width` elements.
  *   norm_w(x) = R(w * R(x * rsqrt(mean(x^2) + eps)))  (R rounds to the storage dtype)

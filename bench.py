@@ -1,0 +1,263 @@
+"""Benchmark: Ouro-1.4B-shape CDB decode on one MI355X.
+
+Workload (one "step" = one ``generate_batch`` over the whole batch): a random-init
+bf16 Ouro with the 1.4B shape (hidden 2048, 24 layers looped 4 steps, 16 MHA heads
+x 128, SwiGLU 5632, vocab 49152, weights N(0, 0.02) seed 1); 256 concurrent
+sequences with prompt lengths lognormal(5.5, 1.0) clipped to [8, 2048] and output
+lengths lognormal(5.0, 0.8) clipped to [16, 1024], uniform token ids; per-token
+exit depths replayed from a seeded categorical over {1, 2, 3, 4} with
+probabilities (0.15, 0.25, 0.30, 0.30); CDB with refill, paged KV block 16,
+``kv_policy="single"``, synchronous exit horizon. Inputs are synthetic.
+
+The JSON line carries:
+  * ``value``: generated tokens / wall time of the timed generate_batch calls;
+  * ``roofline``: the mixed-depth decode-attention kernel (the hot kernel of a
+    recurrent step) timed with HIP events on its stream, at the recurrent
+    shape of this workload (256 rows, every sequence at its mid-generation
+    context), against MI355X's 8 TB/s HBM peak;
+  * ``decode_attention_microbench``: the same kernel on the 1024-row,
+    contexts-in-[128, 8192], 4-loop-slot microbench;
+  * ``cpu_baseline``: the numpy oracle's decode of a bounded sample of the same
+    workload on the host cores (a port of the reference algorithm, not the
+    GPU path).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBPS = 8000.0
+EXIT_PROBS = (0.15, 0.25, 0.30, 0.30)
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=1)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--num-seqs", type=int, default=256)
+    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention"), default="ouro-cdb",
+                   help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-microbench", action="store_true")
+    p.add_argument("--cpu-sample-tokens", type=int, default=6)
+    p.add_argument("--attention-iters", type=int, default=20)
+    return p.parse_args()
+
+
+def c2_workload(num_seqs: int, vocab: int):
+    from continuous_depth_batching_amd.workloads import categorical_exit_trace, lognormal_requests
+
+    prompts, outputs = lognormal_requests(num_requests=num_seqs, vocab_size=vocab, prompt_mu=5.5, prompt_sigma=1.0,
+                                          prompt_range=(8, 2048), output_mu=5.0, output_sigma=0.8,
+                                          output_range=(16, 1024), seed=1)
+    depths = categorical_exit_trace(outputs, EXIT_PROBS, seed=2)
+    return prompts, outputs, depths
+
+
+def ouro_1p4b_config():
+    from continuous_depth_batching_amd.ouro import OuroConfig
+
+    return OuroConfig(vocab_size=49152, hidden_size=2048, intermediate_size=5632, num_hidden_layers=24,
+                      num_attention_heads=16, num_key_value_heads=16, head_dim=128, total_ut_steps=4,
+                      max_position_embeddings=16384)
+
+
+def time_decode_attention(case, split_pages: int, iters: int) -> dict:
+    """Average duration of the decode-attention launch (kernel + split combine) on its stream."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+
+    view = ops.KVPoolView(case.kv_pool, case.block_size)
+    rows, heads, dim = case.q.shape
+    ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(case.contexts.max()), case.block_size,
+                                                split_pages) // 4, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(case.q)
+    stream = torch.cuda.Stream()
+
+    def launch():
+        ops.paged_decode_attention_raw(case.q, case.k_new, case.v_new, view.k_ptr, view.v_ptr, view.layer_stride,
+                                       view.num_cache_layers, view.pool_blocks, case.slot_offset, 0,
+                                       case.block_table, None, case.seqlens, case.rope_cos, case.rope_sin, 1,
+                                       None, None, out, ws, case.block_size, split_pages, dim ** -0.5)
+
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            launch()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            launch()
+        end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / iters
+    nbytes = case.algorithmic_bytes()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": ms, "bytes": nbytes, "gbps": gbps, "rows": rows, "split_pages": split_pages,
+            "mean_context": float(case.contexts.mean())}
+
+
+def decode_attention_c2_case(prompts, outputs, device):
+    """The 256-row recurrent shape of the workload: each sequence mid-way through its output."""
+
+    import torch
+
+    from continuous_depth_batching_amd.workloads import DecodeAttentionCase, rope_tables_torch
+
+    rng = np.random.default_rng(5)
+    contexts = np.asarray([len(p) + max(1, o // 2) for p, o in zip(prompts, outputs)], dtype=np.int64)
+    rows = len(contexts)
+    bs = 16
+    pages = (contexts + bs - 1) // bs
+    perm = rng.permutation(int(pages.sum())).astype(np.int32)
+    table = np.full((rows, int(pages.max())), -1, np.int32)
+    off = np.concatenate([[0], np.cumsum(pages)])
+    for b in range(rows):
+        table[b, :pages[b]] = perm[off[b]:off[b + 1]]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(7)
+    pool = torch.empty((1, 2, int(pages.sum()) * bs, 16, 128), dtype=torch.bfloat16, device=device)
+    pool.normal_(generator=gen)
+    mk = lambda: torch.randn((rows, 16, 128), generator=gen, device=device).bfloat16()
+    cos, sin = rope_tables_torch(128, 10000.0, int(contexts.max()), torch.bfloat16, device)
+    return DecodeAttentionCase(q=mk(), k_new=mk(), v_new=mk(), kv_pool=pool,
+                               slot_offset=torch.zeros(rows, dtype=torch.int32, device=device),
+                               block_table=torch.from_numpy(table).to(device),
+                               seqlens=torch.from_numpy((contexts - 1).astype(np.int32)).to(device),
+                               rope_cos=cos, rope_sin=sin, block_size=bs, contexts=contexts)
+
+
+def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
+    """Numpy oracle decoding a bounded sample of the workload on the host cores."""
+
+    import torch
+
+    from oracle.ouro_model import OuroOracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    weights = {k: v.detach().float().cpu().numpy() for k, v in model.state_dict().items()}
+    cfg = model.config
+    oracle = OuroOracle(weights, num_layers=cfg.num_hidden_layers, num_heads=cfg.num_attention_heads,
+                        num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rope_theta=cfg.rope_theta,
+                        eps=cfg.rms_norm_eps, dtype="bf16", max_positions=4096)
+    # The shortest prompt of the workload keeps the full-depth prefill inside the time budget.
+    idx = int(np.argmin([len(p) for p in prompts]))
+    n = min(sample_tokens, outputs[idx])
+    t0 = time.perf_counter()
+    out = oracle.generate(prompts[idx], n, max_steps=cfg.total_ut_steps, kv_policy="single",
+                          exit_depths=depths[idx][: n - 1])
+    dt = time.perf_counter() - t0
+    return {"value": len(out.tokens) / dt, "unit": "output tok/s", "cores": threads, "kind": "port",
+            "sample": f"request {idx} of the workload (prompt {len(prompts[idx])} tokens): full-depth prefill "
+                      f"+ {len(out.tokens)} generated tokens with its replayed exit depths, one request at a time "
+                      f"in numpy (bf16-rounded fp32), {dt:.1f} s"}
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU; the CDB decode step has no "
+                                   "multi-GPU path in this build (see DESIGN.md for how it would shard)"}))
+        return 2
+    import torch
+
+    from continuous_depth_batching_amd import workloads
+    from continuous_depth_batching_amd.config import ContinuousDepthBatchingConfig
+    from continuous_depth_batching_amd.engine import ContinuousDepthBatchingEngine
+    from continuous_depth_batching_amd.ouro import build_ouro
+
+    device = torch.device("cuda")
+    cfg = ouro_1p4b_config()
+    prompts, outputs, depths = c2_workload(args.num_seqs, cfg.vocab_size)
+    result: dict = {}
+
+    attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device),
+                                      split_pages=8, iters=args.attention_iters)
+    torch.cuda.empty_cache()
+    roofline = {"bound": "hbm", "achieved": round(attention["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_combine_kernel",
+                "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
+                "shape": f"{attention['rows']} rows x 16 heads x 128, mean context {attention['mean_context']:.0f}"}
+    micro = None
+    if not args.no_microbench:
+        case = workloads.decode_attention_microbench(num_rows=1024, ctx_min=128, ctx_max=8192, num_slots=4)
+        m = time_decode_attention(case, split_pages=32, iters=max(5, args.attention_iters // 2))
+        micro = {"ms": round(m["ms"], 4), "GBps": round(m["gbps"], 1), "frac": round(m["gbps"] / HBM_PEAK_GBPS, 4),
+                 "bytes": m["bytes"], "shape": "1024 rows x 16 heads x 128, ctx U[128,8192], 4 loop slots"}
+        del case
+        torch.cuda.empty_cache()
+
+    if args.workload == "decode-attention":
+        print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
+                          "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro}))
+        return 0
+
+    model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
+    blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs)) * 1.05) + 64
+    engine_cfg = ContinuousDepthBatchingConfig(
+        max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False, kv_policy="single",
+        refill=True, block_size=16, max_num_seqs=256, num_blocks=blocks, max_model_len=4096,
+        kv_pressure_mode="none")
+    engine = ContinuousDepthBatchingEngine.from_model(model, engine_cfg)
+    engine.runner.capture_all_buckets()
+    for _ in range(args.warmup):
+        k = min(32, len(prompts))
+        engine.generate_batch(prompts[:k], max_new_tokens=[min(o, 24) for o in outputs[:k]], eos_token_id=None,
+                              exit_depths=[d[: min(o, 24) - 1] for d, o in zip(depths[:k], outputs[:k])])
+    torch.cuda.synchronize()
+    generated = 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+        generated += sum(len(o.generated_tokens) for o in outs)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stats = engine.last_stats
+    value = generated / elapsed
+    result.update({
+        "metric": "output tok/s, Ouro-1.4B-shape CDB decode bs=256; decode-attn HBM GB/s % of peak",
+        "value": round(value, 1),
+        "unit": "output tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(elapsed / args.steps * 1e3, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform token ids, seeded lognormal lengths and exit trace)",
+        "config": {"workload": "Ouro-1.4B-shape CDB decode: 256 seqs, prompts lognormal(5.5,1.0)[8,2048], "
+                               "outputs lognormal(5.0,0.8)[16,1024], exit depths {1:.15,2:.25,3:.30,4:.30}, "
+                               "refill, block 16, kv single",
+                   "global_batch": args.num_seqs, "parallelism": "none"},
+        "roofline": roofline,
+        "decode_attention_microbench": micro,
+        "engine": {"generated_tokens": generated, "recurrent_batches": stats.recurrent_batches,
+                   "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),
+                   "coda_batches": stats.coda_batches, "prefill_batches": stats.prefill_batches,
+                   "recurrent_steps": stats.recurrent_steps, "skipped_recurrent_steps": stats.skipped_recurrent_steps,
+                   "graph_captures_in_timed_run": stats.recurrent_graph_captures},
+    })
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(model, prompts, outputs, depths, args.cpu_sample_tokens)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

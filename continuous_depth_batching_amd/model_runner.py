@@ -146,9 +146,10 @@ class ModelRunner:
         max_bucket = self.decode_graph_buckets[-1]
         num_kv_heads, head_dim = model_adapter.kv_geometry()
         self.split_pages = {b: ops.default_split_pages(b, cache.block_size) for b in self.decode_graph_buckets}
-        ws_bytes = max(ops.decode_workspace_bytes(b, max(model_adapter_num_heads(model_adapter), 1), head_dim,
-                                                  engine_config.max_model_len, cache.block_size, sp)
-                       for b, sp in self.split_pages.items() if b == max_bucket or b <= max_bucket)
+        num_heads = max(model_adapter_num_heads(model_adapter), 1)
+        ws_bytes = max(ops.decode_workspace_bytes(b, num_heads, head_dim, engine_config.max_model_len,
+                                                  cache.block_size, sp) for b, sp in self.split_pages.items())
+        del max_bucket, num_kv_heads
         self.workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=self.device)
         self._buckets: dict[int, _RecurrentBucket] = {}
         self.graph_pool = torch.cuda.graph_pool_handle() if self.use_graphs else None
@@ -313,6 +314,41 @@ class ModelRunner:
             event.record()
             b.flag_events[turn] = event
         return PendingFlags(host=host_flags, event=event)
+
+    def capture_all_buckets(self, buckets: Sequence[int] | None = None) -> int:
+        """Capture the recurrent-stage graph of every bucket ahead of time.
+
+        Each capture's eager pass runs an all-padding launch (bank slot -1, position
+        -1, no gate state), which every kernel treats as a no-op, so warming up
+        changes neither the KV pool, the bank nor the gate state."""
+
+        if not self.use_graphs:
+            return 0
+        captured = 0
+        for rows in buckets or self.decode_graph_buckets:
+            b = self._bucket(rows)
+            if b.graph is not None:
+                continue
+            if b.staged is not None:
+                b.staged.synchronize()
+            i32 = b.host_i32.numpy()
+            b.host_i64.numpy()[:] = -1
+            i32[self.META_POSITIONS] = -1
+            i32[self.META_TABLE_ROWS] = 0
+            i32[self.META_LAYER_OFFSET] = self.layout.core_base
+            i32[self.META_STEPS] = 0
+            i32[self.META_SYNTHETIC] = -1
+            with torch.cuda.stream(self.stream):
+                b.dev_i64.copy_(b.host_i64, non_blocking=True)
+                b.dev_i32.copy_(b.host_i32, non_blocking=True)
+                if b.staged is None:
+                    b.staged = torch.cuda.Event()
+                b.staged.record()
+                self._run_recurrent(b)
+            captured += 1
+        self.stream.synchronize()
+        self.recurrent_graph_captures = 0
+        return captured
 
     def _run_recurrent(self, b: _RecurrentBucket) -> None:
         if not self.use_graphs:

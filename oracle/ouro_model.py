@@ -57,7 +57,8 @@ class OuroOracle:
         return self.w[name]
 
     def _mm(self, x: np.ndarray, weight: np.ndarray) -> np.ndarray:
-        return self.rnd((x.astype(np.float64) @ weight.astype(np.float64).T).astype(np.float32))
+        # fp32 accumulation, like the GPU GEMMs; the result is rounded to the model dtype.
+        return self.rnd(np.asarray(x, np.float32) @ weight.T)
 
     def _layer_stack(self, h: np.ndarray, attend) -> np.ndarray:
         """One loop step over all layers; h is the step input (= residual). Returns final-normed hidden."""

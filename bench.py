@@ -50,7 +50,7 @@ def parse_args() -> argparse.Namespace:
                    help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-microbench", action="store_true")
-    p.add_argument("--cpu-sample-tokens", type=int, default=6)
+    p.add_argument("--cpu-sample-tokens", type=int, default=64)
     p.add_argument("--attention-iters", type=int, default=20)
     return p.parse_args()
 
@@ -74,7 +74,7 @@ def ouro_1p4b_config():
 
 
 def time_decode_attention(case, split_pages: int, iters: int) -> dict:
-    """Average duration of the decode-attention launch (kernel + split combine) on its stream."""
+    """Average duration of one decode-attention call (decode kernel + split merge) on its stream."""
 
     import torch
 
@@ -82,8 +82,9 @@ def time_decode_attention(case, split_pages: int, iters: int) -> dict:
 
     view = ops.KVPoolView(case.kv_pool, case.block_size)
     rows, heads, dim = case.q.shape
-    ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(case.contexts.max()), case.block_size,
-                                                split_pages) // 4, dtype=torch.float32, device="cuda")
+    ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(case.contexts.max()) + 1, case.block_size,
+                                                split_pages or ops.MIN_SPLIT_PAGES) // 4,
+                     dtype=torch.float32, device="cuda")
     out = torch.empty_like(case.q)
     stream = torch.cuda.Stream()
 
@@ -153,8 +154,10 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     oracle = OuroOracle(weights, num_layers=cfg.num_hidden_layers, num_heads=cfg.num_attention_heads,
                         num_kv_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim, rope_theta=cfg.rope_theta,
                         eps=cfg.rms_norm_eps, dtype="bf16", max_positions=4096)
-    # The shortest prompt of the workload keeps the full-depth prefill inside the time budget.
-    idx = int(np.argmin([len(p) for p in prompts]))
+    # The shortest prompt among requests generating at least sample_tokens keeps the full-depth
+    # prefill small, so most of the sample is decode.
+    eligible = [i for i, o in enumerate(outputs) if o >= sample_tokens] or [int(np.argmax(outputs))]
+    idx = min(eligible, key=lambda i: len(prompts[i]))
     n = min(sample_tokens, outputs[idx])
     t0 = time.perf_counter()
     out = oracle.generate(prompts[idx], n, max_steps=cfg.total_ut_steps, kv_policy="single",
@@ -169,8 +172,8 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this benchmark runs on exactly one GPU; the CDB decode step has no "
-                                   "multi-GPU path in this build (see DESIGN.md for how it would shard)"}))
+        print(json.dumps({"error": "this benchmark runs on exactly one GPU: the CDB decode step is built "
+                                   "for one GPU's share and has no multi-GPU path"}))
         return 2
     import torch
 
@@ -185,17 +188,17 @@ def main() -> int:
     result: dict = {}
 
     attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device),
-                                      split_pages=8, iters=args.attention_iters)
+                                      split_pages=0, iters=args.attention_iters)
     torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(attention["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_combine_kernel",
+                "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_merge_kernel",
                 "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
                 "shape": f"{attention['rows']} rows x 16 heads x 128, mean context {attention['mean_context']:.0f}"}
     micro = None
     if not args.no_microbench:
         case = workloads.decode_attention_microbench(num_rows=1024, ctx_min=128, ctx_max=8192, num_slots=4)
-        m = time_decode_attention(case, split_pages=32, iters=max(5, args.attention_iters // 2))
+        m = time_decode_attention(case, split_pages=0, iters=max(5, args.attention_iters // 2))
         micro = {"ms": round(m["ms"], 4), "GBps": round(m["gbps"], 1), "frac": round(m["gbps"] / HBM_PEAK_GBPS, 4),
                  "bytes": m["bytes"], "shape": "1024 rows x 16 heads x 128, ctx U[128,8192], 4 loop slots"}
         del case

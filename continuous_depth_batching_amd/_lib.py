@@ -14,6 +14,7 @@ from functools import lru_cache
 from ._build import LIBRARY_PATH
 
 CDB_OK = 0
+CDB_ERR_NULL, CDB_ERR_SHAPE, CDB_ERR_UNSUPPORTED, CDB_ERR_HIP, CDB_ERR_CAPACITY = -1, -2, -3, -4, -5
 CDB_ERRORS = {
     -1: "a required pointer is null",
     -2: "an extent or stride is out of range",
@@ -42,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _P, _P,  # q_bias, k_bias
             _P, _P, c_int64,  # out, workspace, workspace_bytes
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
+            c_int32, c_int32,  # min/max split pages (split_pages <= 0)
             c_float, c_int64, c_int64, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stream
         ],
     ),

@@ -13,20 +13,35 @@
 // folded in.
 //
 // Work decomposition (split-KV / flash-decoding):
-//   * a row's context is cut into splits of `split_pages` pages;
+//   * a row's context is cut into splits of `split_pages` pages; with
+//     split_pages <= 0 every workgroup derives the same split size from the
+//     launch's total page count: the smallest power of two in [min_split_pages,
+//     max_split_pages] for which the items do not outnumber the persistent
+//     workgroups (coarsened further if the workspace is too small). Longer
+//     splits mean fewer partials to merge and fewer per-item latency chains;
+//     shorter ones keep narrow batches from leaving workgroups idle;
 //   * a work item is (row, split, group of 4 query heads); one workgroup of
 //     4 waves takes an item, wave w owning query head 4*g + w;
 //   * workgroups are persistent: workgroup i processes items i, i+G, ...,
 //     so the grid does not depend on the context lengths (graph-capturable);
-//   * each workgroup rebuilds the per-row split prefix sum in LDS and maps an
-//     item to its row by binary search.
+//   * each workgroup builds the per-row split prefix sum in LDS and maps an
+//     item to its row by binary search; workgroup 0 also stores it in the
+//     workspace header for the merge kernel.
 // Inside a wave, lane = 16 * slot + chunk: the 16 lanes of a DPP row split the
 // head dimension into 16 chunks and the 4 rows ("slots") take interleaved
 // tokens. q.k is reduced across a row with four DPP rotate-adds; each slot keeps
-// its own online-softmax state, merged across slots at the end.
+// its own online-softmax state, merged across slots at the end. K/V loads run
+// one 16-token step ahead of the softmax update (two register buffers).
 // A row with one split writes its normalized output directly; otherwise the
-// split's (unnormalized acc, max, sum) goes to the workspace and
-// cdb_decode_combine merges the splits.
+// split's (unnormalized acc, max, sum) goes to the workspace and a second
+// kernel merges the splits. The merge is a separate launch on purpose: merging
+// in the last-arriving workgroup needs a device-scope release/acquire per item,
+// which on a multi-XCD part writes back and invalidates the XCD's L2 and costs
+// far more than the launch.
+//
+// Workspace: int32 header [split_tokens (-1: partial space too small),
+// split_prefix[0..B]] padded to 256 bytes, then fp32 partials
+// [total_splits, H, D + 2].
 
 #include "cdb_common.h"
 #include "../../include/cdb_amd.h"
@@ -48,6 +63,7 @@ struct DecodeParams {
   const void* q_bias;           // [H, D] or null, added to q before rotation
   const void* k_bias;           // [Hkv, D] or null
   void* out;                    // [B, H, D]
+  int32_t* header;              // [B + 2]: split_tokens (or -1), then the split prefix over rows
   float* partial;               // [total_splits, H, D + 2] when a row has > 1 split
   int64_t layer_stride;         // elements between cache layers
   int64_t q_stride, kv_stride;  // elements between consecutive rows of q and of k_new/v_new
@@ -59,6 +75,7 @@ struct DecodeParams {
   int32_t num_cache_layers;     // valid cache_layer values are [0, num_cache_layers)
   int64_t pool_blocks;          // valid block ids are [0, pool_blocks)
   int64_t partial_capacity;     // splits the workspace holds
+  int32_t min_split_pages, max_split_pages;  // range of the adaptive split size (split_pages <= 0)
   float scale_log2;             // softmax scale * log2(e)
 };
 
@@ -71,19 +88,13 @@ template <int D> struct Layout {
 
 // A row is served when its new-token position fits the block table and the
 // RoPE table and its cache layer exists. Rows failing this get no work and a
-// NaN output (the combine kernel writes it); padding rows (p < 0) get zeros.
+// NaN output; padding rows (p < 0) get zeros.
 CDB_DEVICE bool row_valid(const DecodeParams& P, int b, int p) {
   if (p < 0) return false;
   if ((int64_t)p >= ((int64_t)P.table_width << P.block_size_log2)) return false;
   if (P.rope_cos != nullptr && p >= P.max_positions) return false;
   const int layer = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
   return layer >= 0 && layer < P.num_cache_layers;
-}
-
-// Number of splits of row b (0 for padding and invalid rows).
-CDB_DEVICE int row_splits(const DecodeParams& P, int b, int split_tokens) {
-  const int p = P.seqlens[b];
-  return row_valid(P, b, p) ? (p + split_tokens) / split_tokens : 0;
 }
 
 // Rotate this lane's chunk of a head vector. `own`/`partner` are the lane's
@@ -155,10 +166,107 @@ CDB_DEVICE void load_rotated(const DecodeParams& P, const T* base, const T* bias
   rope_chunk<T, D>(P, pos, chunk, own, partner, out);
 }
 
+// The block ids of 64 consecutive pages starting at `base`, one per lane
+// (-1 past the table's width). Loaded once per 64 pages so that K/V addresses
+// never wait on a block-table load inside the streaming loop.
+CDB_DEVICE int load_page_window(const int32_t* table, int base, int table_width, int lane) {
+  const int page = base + lane;
+  return page < table_width ? table[page] : -1;
+}
+
+// Block id of `page` from the window (`page - base` must be in [0, 64)).
+CDB_DEVICE int window_block(int window, int base, int page) {
+  return __builtin_amdgcn_ds_bpermute((page - base) << 2, window);
+}
+
+// Load one wave step (16 tokens: 4 per slot) of K and V for this lane's chunk.
+// t0 is a multiple of 16 and the step's pages lie in the window. Tokens at or
+// past t_end, or with an out-of-range block id, are masked and their registers
+// zeroed so a zero softmax weight never multiplies garbage.
+template <typename T, int D>
+CDB_DEVICE void load_step(const DecodeParams& P, int window, int win_base, const T* k_base, const T* v_base,
+                          int t0, int t_end, int slot, int chunk, int kvh, int bs_log2, int64_t row_elems,
+                          Vec<T, D / 16> (&kv)[4], Vec<T, D / 16> (&vv)[4], bool (&valid)[4]) {
+  constexpr int C = D / 16;
+  // With pages of >= 16 tokens the whole step sits in one page: one wave-uniform lookup.
+  const int step_blk = bs_log2 >= 4 ? __builtin_amdgcn_readlane(window, (t0 >> bs_log2) - win_base) : -1;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int t = t0 + 4 * u + slot;
+    const int blk_any = bs_log2 >= 4 ? step_blk : window_block(window, win_base, t >> bs_log2);
+    const int blk = t < t_end ? blk_any : -1;
+    valid[u] = blk >= 0 && blk < P.pool_blocks;
+    if (valid[u]) {
+      const int64_t row = ((int64_t)blk << bs_log2) + (t & ((1 << bs_log2) - 1));
+      const int64_t off = row * row_elems + (int64_t)kvh * D + chunk * C;
+      kv[u].load(k_base + off);
+      vv[u].load(v_base + off);
+    } else {
+#pragma unroll
+      for (int w = 0; w < Vec<T, C>::kWords; ++w) kv[u].w[w] = vv[u].w[w] = 0u;
+    }
+  }
+}
+
+// Online-softmax update of one slot's state with its 4 tokens of a wave step.
+template <typename T, int D>
+CDB_DEVICE void attend_step(const float* q, const Vec<T, D / 16> (&kv)[4], const Vec<T, D / 16> (&vv)[4],
+                            const bool (&valid)[4], float& m, float& l, float* acc) {
+  constexpr int C = D / 16;
+  float sc[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < C; ++i) dot = fmaf(q[i], kv[u].get(i), dot);
+    dot = row16_sum(dot);
+    sc[u] = valid[u] ? dot : -INFINITY;
+  }
+  const float m_new = fmaxf(m, fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+  if (m_new == -INFINITY) return;
+  const float alpha = exp2f(m - m_new);
+  l *= alpha;
+#pragma unroll
+  for (int i = 0; i < C; ++i) acc[i] *= alpha;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float pu = exp2f(sc[u] - m_new);
+    l += pu;
+#pragma unroll
+    for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, vv[u].get(i), acc[i]);
+  }
+  m = m_new;
+}
+
+// Inclusive-to-exclusive prefix over B entries of `a` (a[0] = 0, a[b+1] = count of row b), by wave 0.
+CDB_DEVICE void lds_prefix(int* a, int B, int wave, int lane) {
+  if (wave == 0) {
+    int carry = 0;
+    for (int base = 0; base < B; base += 64) {
+      const int idx = base + lane;
+      int v = idx < B ? a[idx + 1] : 0;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int n = __shfl_up(v, off, 64);
+        if (lane >= off) v += n;
+      }
+      if (idx < B) a[idx + 1] = v + carry;
+      carry += __shfl(v, 63, 64);
+    }
+  }
+  __syncthreads();
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   constexpr int C = Layout<D>::kChunk;
+  // Per-row metadata, loaded once per workgroup: new-token position (-1 when the
+  // row gets no work), cache layer, block-table row and the split prefix sum.
+  __shared__ int row_pos[kMaxRowsLds];
+  __shared__ int row_layer[kMaxRowsLds];
+  __shared__ int row_trow[kMaxRowsLds];
   __shared__ int split_prefix[kMaxRowsLds + 1];
+  __shared__ int wave_pages[4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -168,34 +276,57 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   const int B = P.num_rows;
   const int bs_log2 = P.block_size_log2;
   const int block_size = 1 << bs_log2;
-  const int split_tokens = P.split_pages << bs_log2;
   const int head_groups = (P.num_heads + 3) >> 2;
 
-  // Per-row split counts -> exclusive prefix in LDS (row-major item order).
-  for (int b = tid; b < B; b += blockDim.x) split_prefix[b + 1] = row_splits(P, b, split_tokens);
+  // Pages each served row reads (including the new token's page).
+  int pages = 0;
+  for (int b = tid; b < B; b += blockDim.x) {
+    const int p = P.seqlens[b];
+    const bool ok = row_valid(P, b, p);
+    row_pos[b] = ok ? p : -1;
+    row_layer[b] = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
+    row_trow[b] = P.table_row ? P.table_row[b] : b;
+    pages += ok ? ((p + block_size) >> bs_log2) : 0;
+  }
+  for (int m = 32; m >= 1; m >>= 1) pages += __shfl_xor(pages, m, 64);
+  if (lane == 0) wave_pages[wave] = pages;
+  __syncthreads();
+  const int total_pages = wave_pages[0] + wave_pages[1] + wave_pages[2] + wave_pages[3];
+
+  int split_pages = P.split_pages;
+  if (split_pages <= 0) {
+    const int64_t target = gridDim.x;
+    const int64_t want = ((int64_t)total_pages * head_groups + target - 1) / target;
+    split_pages = P.min_split_pages;
+    while (split_pages < want && split_pages < P.max_split_pages) split_pages <<= 1;
+    // The split count is at most total_pages / split_pages + B: coarsen until the partials fit.
+    while ((int64_t)total_pages / split_pages + B > P.partial_capacity && split_pages < (1 << 20)) split_pages <<= 1;
+  }
+  const int split_tokens = split_pages << bs_log2;
+
+  for (int b = tid; b < B; b += blockDim.x) {
+    const int p = row_pos[b];
+    split_prefix[b + 1] = p >= 0 ? (p + split_tokens) / split_tokens : 0;
+  }
   if (tid == 0) split_prefix[0] = 0;
   __syncthreads();
-  // Sequential scan by wave 0 in 64-wide pieces with a carry (B <= 4096).
-  if (wave == 0) {
-    int carry = 0;
-    for (int base = 0; base < B; base += 64) {
-      int idx = base + lane;
-      int v = idx < B ? split_prefix[idx + 1] : 0;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        int n = __shfl_up(v, off, 64);
-        if (lane >= off) v += n;
-      }
-      if (idx < B) split_prefix[idx + 1] = v + carry;
-      carry += __shfl(v, 63, 64);
-    }
-  }
-  __syncthreads();
+  lds_prefix(split_prefix, B, wave, lane);
   const int total_splits = split_prefix[B];
   const int total_items = total_splits * head_groups;
-  // Rows with several splits need workspace; if it is too small, the combine
-  // kernel flags those rows with NaN instead of this kernel writing past it.
-  const bool partial_ok = total_splits <= P.partial_capacity;
+  const bool overflow = total_splits > P.partial_capacity;
+
+  if (blockIdx.x == 0) {
+    for (int b = tid; b <= B; b += blockDim.x) P.header[1 + b] = split_prefix[b];
+    if (tid == 0) P.header[0] = overflow ? -1 : split_tokens;
+  }
+
+  // Rows without work: padding rows read as zeros, rows out of range as NaN.
+  for (int b = blockIdx.x; b < B; b += gridDim.x) {
+    if (split_prefix[b + 1] != split_prefix[b]) continue;
+    const float fill = P.seqlens[b] < 0 ? 0.f : __builtin_nanf("");
+    T* o = static_cast<T*>(P.out) + (int64_t)b * P.num_heads * D;
+    for (int e = tid; e < P.num_heads * D; e += blockDim.x) Elem<T>::store(o + e, fill);
+  }
 
   const T* q_all = static_cast<const T*>(P.q);
   const T* k_new_all = static_cast<const T*>(P.k_new);
@@ -208,83 +339,72 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
     const int hg = item - split_global * head_groups;
     const int h = hg * 4 + wave;
     if (h >= P.num_heads) continue;  // wave-uniform; no block-level sync inside the item loop
-    // Row owning this split: largest b with split_prefix[b] <= split_global.
-    int lo = 0, hi = B - 1;
+    int lo = 0, hi = B - 1;  // row owning this split: largest b with split_prefix[b] <= split_global
     while (lo < hi) {
-      int mid = (lo + hi + 1) >> 1;
+      const int mid = (lo + hi + 1) >> 1;
       if (split_prefix[mid] <= split_global) lo = mid; else hi = mid - 1;
     }
     const int b = lo;
     const int s = split_global - split_prefix[b];
     const int nsplit = split_prefix[b + 1] - split_prefix[b];
-    const int p = P.seqlens[b];
+    if (nsplit > 1 && overflow) continue;  // the merge kernel writes NaN for this row
+    const int p = row_pos[b];
     const int kvh = h / kv_group;
-    const int layer = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
+    const int layer = row_layer[b];
     T* k_base = static_cast<T*>(P.k_pool) + (int64_t)layer * P.layer_stride;
     T* v_base = static_cast<T*>(P.v_pool) + (int64_t)layer * P.layer_stride;
-    const int32_t* table = P.block_table + (int64_t)(P.table_row ? P.table_row[b] : b) * P.table_width;
+    const int32_t* table = P.block_table + (int64_t)row_trow[b] * P.table_width;
 
-    // Rotated query chunk, pre-scaled into the log2 domain.
+    const int t_begin = s * split_tokens;
+    const bool last_split = s == nsplit - 1;
+    const int t_end = last_split ? p : t_begin + split_tokens;  // cached tokens only; p is handled below
+
+    int win_base = t_begin >> bs_log2;
+    int window = load_page_window(table, win_base, P.table_width, lane);
+    // Keeps the pages of the step starting at t0 inside the window (wave-uniform).
+    auto cover = [&](int t0) {
+      if (((t0 + 15) >> bs_log2) - win_base >= 64) {
+        win_base = t0 >> bs_log2;
+        window = load_page_window(table, win_base, P.table_width, lane);
+      }
+    };
+
+    // Issue the first step's loads before the query rotation so they overlap it.
+    Vec<T, C> ka[4], va[4], kb[4], vb[4];
+    bool vla[4], vlb[4];
+    if (t_begin < t_end) {
+      cover(t_begin);
+      load_step<T, D>(P, window, win_base, k_base, v_base, t_begin, t_end, slot, chunk, kvh, bs_log2, row_elems,
+                      ka, va, vla);
+    }
+
     float q[C];
     load_rotated<T, D>(P, q_all + (int64_t)b * P.q_stride + (int64_t)h * D,
                        P.q_bias ? static_cast<const T*>(P.q_bias) + (int64_t)h * D : nullptr, p, chunk, q);
 #pragma unroll
     for (int i = 0; i < C; ++i) q[i] *= P.scale_log2;
 
-    const int t_begin = s * split_tokens;
-    const bool last_split = s == nsplit - 1;
-    const int t_end = last_split ? p : t_begin + split_tokens;  // cached tokens only; p handled below
-
     float m = -INFINITY, l = 0.f;
     float acc[C];
 #pragma unroll
     for (int i = 0; i < C; ++i) acc[i] = 0.f;
 
-    // Stream the cached tokens four at a time per slot (16 per wave step).
-    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-      float sc[4];
-      bool valid[4];
-      Vec<T, C> kv[4], vv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int t = t0 + 4 * u + slot;
-        const int blk = t < t_end ? table[t >> bs_log2] : -1;
-        valid[u] = blk >= 0 && blk < P.pool_blocks;
-        if (valid[u]) {
-          const int64_t row = (int64_t)blk * block_size + (t & (block_size - 1));
-          const int64_t off = row * row_elems + (int64_t)kvh * D + chunk * C;
-          kv[u].load(k_base + off);
-          vv[u].load(v_base + off);
-        } else {
-          // Masked tokens get zero weight; zero their registers so 0 * garbage cannot make a NaN.
-#pragma unroll
-          for (int w = 0; w < Vec<T, C>::kWords; ++w) kv[u].w[w] = vv[u].w[w] = 0u;
-        }
+    // Two-stage pipeline: the next step's K/V loads are in flight while this step is reduced.
+    for (int t0 = t_begin; t0 < t_end; t0 += 32) {
+      const bool second = t0 + 16 < t_end;
+      if (second) {
+        cover(t0 + 16);
+        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 16, t_end, slot, chunk, kvh, bs_log2,
+                        row_elems, kb, vb, vlb);
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < C; ++i) dot = fmaf(q[i], kv[u].get(i), dot);
-        dot = row16_sum(dot);
-        sc[u] = valid[u] ? dot : -INFINITY;
+      attend_step<T, D>(q, ka, va, vla, m, l, acc);
+      if (!second) break;
+      if (t0 + 32 < t_end) {
+        cover(t0 + 32);
+        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 32, t_end, slot, chunk, kvh, bs_log2,
+                        row_elems, ka, va, vla);
       }
-      const float mloc = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      const float m_new = fmaxf(m, mloc);
-      if (m_new != -INFINITY) {
-        const float alpha = exp2f(m - m_new);
-        l *= alpha;
-#pragma unroll
-        for (int i = 0; i < C; ++i) acc[i] *= alpha;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float pu = exp2f(sc[u] - m_new);
-          l += pu;
-#pragma unroll
-          for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, vv[u].get(i), acc[i]);
-        }
-        m = m_new;
-      }
+      attend_step<T, D>(q, kb, vb, vlb, m, l, acc);
     }
 
     if (last_split) {
@@ -294,10 +414,11 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
       load_rotated<T, D>(P, k_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D, kbias, p, chunk, kr);
       Vec<T, C> vn;
       vn.load(v_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D + chunk * C);
-      const int new_blk = table[p >> bs_log2];
+      const int p_page = p >> bs_log2;
+      const int new_blk = p_page - win_base < 64 ? __builtin_amdgcn_readlane(window, p_page - win_base)
+                                                 : table[p_page];
       if (slot == 0 && h % kv_group == 0 && new_blk >= 0 && new_blk < P.pool_blocks) {
-        const int blk = new_blk;
-        const int64_t row = (int64_t)blk * block_size + (p & (block_size - 1));
+        const int64_t row = ((int64_t)new_blk << bs_log2) + (p & (block_size - 1));
         const int64_t off = row * row_elems + (int64_t)kvh * D + chunk * C;
         Vec<T, C> kw;
 #pragma unroll
@@ -335,77 +456,60 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
       acc[i] += shfl_xor_f32(acc[i], 32);
     }
 
-    if (slot == 0) {
-      if (nsplit == 1) {
-        const float inv = 1.f / l;
-        Vec<T, C> o;
+    if (slot != 0) continue;
+    if (nsplit == 1) {
+      T* out_row = static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D;
+      const float inv = 1.f / l;
+      Vec<T, C> o;
 #pragma unroll
-        for (int i = 0; i < C; ++i) o.set(i, acc[i] * inv);
-        o.store(static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D + chunk * C);
-      } else if (partial_ok) {
-        float* part = P.partial + ((int64_t)(split_prefix[b] + s) * P.num_heads + h) * (D + 2);
+      for (int i = 0; i < C; ++i) o.set(i, acc[i] * inv);
+      o.store(out_row + chunk * C);
+    } else {
+      float* part = P.partial + ((int64_t)split_global * P.num_heads + h) * (D + 2);
 #pragma unroll
-        for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
-        if (chunk == 0) {
-          part[D] = m_all;
-          part[D + 1] = l;
-        }
+      for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
+      if (chunk == 0) {
+        part[D] = m_all;
+        part[D + 1] = l;
       }
     }
   }
 }
 
-// Merge per-split partials of rows with more than one split; zero padding rows.
-// One wave per (row, head).
+// Merge the split partials of every (row, head) whose row has more than one
+// split; one wave per (row, head). Reads the split prefix the decode kernel
+// left in the workspace header.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams P) {
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
   const int lane = threadIdx.x & 63;
-  const int wave_global = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  const int B = P.num_rows;
-  if (wave_global >= B * P.num_heads) return;
-  const int b = wave_global / P.num_heads;
-  const int h = wave_global - b * P.num_heads;
-  const int split_tokens = P.split_pages << P.block_size_log2;
-  const int p = P.seqlens[b];
-  const int nsplit = row_splits(P, b, split_tokens);
-  T* out = static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D;
-  if (nsplit == 1) return;
-  if (nsplit == 0) {
-    const float fill = p < 0 ? 0.f : __builtin_nanf("");
-    for (int d = lane; d < D; d += 64) Elem<T>::store(out + d, fill);
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= P.num_rows * P.num_heads) return;
+  const int b = w / P.num_heads;
+  const int h = w - b * P.num_heads;
+  const int first = P.header[1 + b];
+  const int nsplit = P.header[2 + b] - first;
+  if (nsplit <= 1) return;
+  T* out_row = static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D;
+  if (P.header[0] < 0) {
+    for (int d = lane; d < D; d += 64) Elem<T>::store(out_row + d, __builtin_nanf(""));
     return;
   }
-  // Exclusive prefix of split counts over rows before b, and the total.
-  int first = 0, total = 0;
-  for (int r = lane; r < B; r += 64) {
-    const int n = row_splits(P, r, split_tokens);
-    if (r < b) first += n;
-    total += n;
-  }
-  for (int m = 32; m >= 1; m >>= 1) {
-    first += __shfl_xor(first, m, 64);
-    total += __shfl_xor(total, m, 64);
-  }
-  if (total > P.partial_capacity) {
-    for (int d = lane; d < D; d += 64) Elem<T>::store(out + d, __builtin_nanf(""));
-    return;
-  }
-  const float* part = P.partial + ((int64_t)first * P.num_heads + h) * (D + 2);
   const int64_t stride = (int64_t)P.num_heads * (D + 2);
-  float m_all = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) m_all = fmaxf(m_all, part[s * stride + D]);
+  const float* part = P.partial + (int64_t)first * stride + (int64_t)h * (D + 2);
+  float mx = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, part[s * stride + D]);
   float num0 = 0.f, num1 = 0.f, den = 0.f;
   const int d0 = lane, d1 = lane + 64;
   for (int s = 0; s < nsplit; ++s) {
     const float* ps = part + s * stride;
-    const float w = exp2f(ps[D] - m_all);
-    den = fmaf(w, ps[D + 1], den);
-    if (d0 < D) num0 = fmaf(w, ps[d0], num0);
-    if (d1 < D) num1 = fmaf(w, ps[d1], num1);
+    const float wgt = exp2f(ps[D] - mx);
+    den = fmaf(wgt, ps[D + 1], den);
+    if (d0 < D) num0 = fmaf(wgt, ps[d0], num0);
+    if (d1 < D) num1 = fmaf(wgt, ps[d1], num1);
   }
   const float inv = 1.f / den;
-  if (d0 < D) Elem<T>::store(out + d0, num0 * inv);
-  if (d1 < D) Elem<T>::store(out + d1, num1 * inv);
+  if (d0 < D) Elem<T>::store(out_row + d0, num0 * inv);
+  if (d1 < D) Elem<T>::store(out_row + d1, num1 * inv);
 }
 
 }  // namespace cdb
@@ -437,20 +541,16 @@ int ilog2_exact(int x) {
   return r;
 }
 
+int64_t header_bytes(int64_t num_rows) { return ((num_rows + 2) * 4 + 255) / 256 * 256; }
+
 template <typename T, int D>
 int launch_decode(const DecodeParams& P, int num_cus, hipStream_t stream) {
   const int grid = num_cus * resident_blocks_per_cu(paged_decode_kernel<T, D>);
   hipLaunchKernelGGL((paged_decode_kernel<T, D>), dim3(grid), dim3(256), 0, stream, P);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return CDB_ERR_HIP;
-  const int waves = P.num_rows * P.num_heads;
-  const int blocks = (waves + 3) / 4;
-  if (blocks > 0) {
-    hipLaunchKernelGGL((decode_combine_kernel<T, D>), dim3(blocks), dim3(256), 0, stream, P);
-    e = hipGetLastError();
-    if (e != hipSuccess) return CDB_ERR_HIP;
-  }
-  return CDB_OK;
+  if (hipGetLastError() != hipSuccess) return CDB_ERR_HIP;
+  const int64_t waves = (int64_t)P.num_rows * P.num_heads;
+  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, P);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 
 template <typename T>
@@ -472,8 +572,9 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
   if (num_rows < 0 || num_heads <= 0 || head_dim <= 0 || max_seqlen <= 0 || block_size <= 0 || split_pages <= 0)
     return -1;
   const int64_t split_tokens = (int64_t)split_pages * block_size;
-  const int64_t max_splits = (max_seqlen + split_tokens - 1) / split_tokens;
-  return (int64_t)num_rows * max_splits * num_heads * (head_dim + 2) * (int64_t)sizeof(float);
+  const int64_t max_splits = (max_seqlen + split_tokens - 1) / split_tokens + 1;
+  return header_bytes(num_rows) +
+         (int64_t)num_rows * max_splits * num_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
@@ -484,12 +585,16 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t rope_style, int32_t max_positions, const void* q_bias, const void* k_bias,
                                void* out, void* workspace, int64_t workspace_bytes, int32_t num_rows,
                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                               int32_t split_pages, float scale, int64_t q_stride, int64_t kv_stride,
-                               int32_t dtype, hipStream_t stream) {
+                               int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages, float scale,
+                               int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream) {
   if (num_rows == 0) return CDB_OK;
-  if (!q || !k_new || !v_new || !k_pool || !v_pool || !block_table || !seqlens || !out) return CDB_ERR_NULL;
+  if (!q || !k_new || !v_new || !k_pool || !v_pool || !block_table || !seqlens || !out || !workspace)
+    return CDB_ERR_NULL;
   if (num_rows < 0 || num_rows > kMaxRowsLds || num_heads <= 0 || num_kv_heads <= 0 ||
-      num_heads % num_kv_heads != 0 || table_width <= 0 || split_pages <= 0)
+      num_heads % num_kv_heads != 0 || table_width <= 0)
+    return CDB_ERR_SHAPE;
+  if (split_pages <= 0 && (min_split_pages <= 0 || max_split_pages < min_split_pages ||
+                           (min_split_pages & (min_split_pages - 1))))
     return CDB_ERR_SHAPE;
   const int bs_log2 = ilog2_exact(block_size);
   if (bs_log2 < 0) return CDB_ERR_SHAPE;
@@ -499,14 +604,17 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
   if (dtype != CDB_DTYPE_F32 && dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
   // Split-half rotation pairs chunk c with chunk c ^ 8, i.e. D/2 = 8 chunks.
   if (rope_style == 1 && (head_dim / 16) * 8 != head_dim / 2) return CDB_ERR_UNSUPPORTED;
-  if (workspace == nullptr && workspace_bytes != 0) return CDB_ERR_NULL;
   if (num_cache_layers <= 0 || pool_blocks <= 0 || layer_stride < 0) return CDB_ERR_SHAPE;
+  const int64_t header = header_bytes(num_rows);
+  if (workspace_bytes < header) return CDB_ERR_CAPACITY;
 
   DecodeParams P;
   P.q = q; P.k_new = k_new; P.v_new = v_new; P.k_pool = k_pool; P.v_pool = v_pool;
   P.block_table = block_table; P.table_row = table_row; P.seqlens = seqlens; P.cache_layer = cache_layer;
   P.rope_cos = rope_style ? rope_cos : nullptr; P.rope_sin = rope_style ? rope_sin : nullptr;
-  P.q_bias = q_bias; P.k_bias = k_bias; P.out = out; P.partial = static_cast<float*>(workspace);
+  P.q_bias = q_bias; P.k_bias = k_bias; P.out = out;
+  P.header = static_cast<int32_t*>(workspace);
+  P.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + header);
   P.layer_stride = layer_stride; P.cache_layer0 = cache_layer0;
   P.q_stride = q_stride > 0 ? q_stride : (int64_t)num_heads * head_dim;
   P.kv_stride = kv_stride > 0 ? kv_stride : (int64_t)num_kv_heads * head_dim;
@@ -515,7 +623,8 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
   P.table_width = table_width; P.block_size_log2 = bs_log2; P.split_pages = split_pages;
   P.rope_style = rope_style; P.max_positions = max_positions;
   P.num_cache_layers = num_cache_layers; P.pool_blocks = pool_blocks;
-  P.partial_capacity = workspace_bytes / ((int64_t)num_heads * (head_dim + 2) * (int64_t)sizeof(float));
+  P.min_split_pages = min_split_pages; P.max_split_pages = max_split_pages;
+  P.partial_capacity = (workspace_bytes - header) / ((int64_t)num_heads * (head_dim + 2) * (int64_t)sizeof(float));
   P.scale_log2 = scale * 1.4426950408889634f;
 
   if (g_num_cus == 0) {

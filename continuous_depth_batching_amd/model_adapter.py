@@ -50,8 +50,8 @@ class RecurrentLaunch:
     table_rows: torch.Tensor     # [rows] int32 block-table row of the token's request
     slot_offset: torch.Tensor    # [rows] int32 cache layer of core layer 0 at the row's step (prelude + slot * C)
     cache: PagedKVCache
-    workspace: torch.Tensor      # decode-attention split workspace (fp32)
-    split_pages: int
+    workspace: torch.Tensor      # decode-attention workspace (split header + fp32 partials)
+    split_pages: int             # pages per KV split; 0 = chosen by the kernel
     gate: GateLaunch
 
 

@@ -145,11 +145,12 @@ class ModelRunner:
         self.next_hidden_slot = 0
         max_bucket = self.decode_graph_buckets[-1]
         num_kv_heads, head_dim = model_adapter.kv_geometry()
-        self.split_pages = {b: ops.default_split_pages(b, cache.block_size) for b in self.decode_graph_buckets}
+        # Decode attention sizes its KV splits on the device (the count of pages in the launch is
+        # only known there); the workspace holds the partials of the finest split of the largest bucket.
         num_heads = max(model_adapter_num_heads(model_adapter), 1)
-        ws_bytes = max(ops.decode_workspace_bytes(b, num_heads, head_dim, engine_config.max_model_len,
-                                                  cache.block_size, sp) for b, sp in self.split_pages.items())
-        del max_bucket, num_kv_heads
+        ws_bytes = ops.decode_workspace_bytes(max_bucket, num_heads, head_dim, engine_config.max_model_len,
+                                              cache.block_size, ops.MIN_SPLIT_PAGES)
+        del num_kv_heads
         self.workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=self.device)
         self._buckets: dict[int, _RecurrentBucket] = {}
         self.graph_pool = torch.cuda.graph_pool_handle() if self.use_graphs else None
@@ -257,7 +258,8 @@ class ModelRunner:
         launch = RecurrentLaunch(
             rows=rows, bank=self.bank, bank_slots=dev_i64, positions=dev_i32[self.META_POSITIONS],
             table_rows=dev_i32[self.META_TABLE_ROWS], slot_offset=dev_i32[self.META_LAYER_OFFSET],
-            cache=self.cache, workspace=self.workspace, split_pages=self.split_pages.get(rows, 8), gate=gate)
+            cache=self.cache, workspace=self.workspace,
+            split_pages=ops.ADAPTIVE_SPLIT, gate=gate)
         b = _RecurrentBucket(rows=rows, host_i64=host_i64, host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32,
                              launch=launch)
         b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]

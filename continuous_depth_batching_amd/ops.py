@@ -18,6 +18,12 @@ from . import _lib
 
 _DTYPE_CODES = {torch.float32: _lib.CDB_DTYPE_F32, torch.bfloat16: _lib.CDB_DTYPE_BF16}
 
+# Decode-attention KV split length in pages: ADAPTIVE_SPLIT lets every launch pick a
+# power of two in [MIN_SPLIT_PAGES, MAX_SPLIT_PAGES] from its own page count.
+ADAPTIVE_SPLIT = 0
+MIN_SPLIT_PAGES = 4
+MAX_SPLIT_PAGES = 32
+
 
 def dtype_code(dtype: torch.dtype) -> int:
     try:
@@ -116,8 +122,13 @@ def paged_decode_attention_raw(
     block_size: int,
     split_pages: int,
     scale: float,
+    min_split_pages: int = MIN_SPLIT_PAGES,
+    max_split_pages: int = MAX_SPLIT_PAGES,
 ) -> torch.Tensor:
-    """Launch ``cdb_paged_decode_attention`` on explicit pool pointers (no allocation)."""
+    """Launch ``cdb_paged_decode_attention`` on explicit pool pointers (no allocation).
+
+    ``split_pages <= 0`` lets the kernel size the splits within [min, max] pages.
+    """
 
     num_rows, num_heads, head_dim = q.shape
     num_kv_heads = k_new.shape[1]
@@ -162,13 +173,15 @@ def paged_decode_attention_raw(
         _ptr(q_bias), _ptr(k_bias),
         out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4,
         num_rows, num_heads, num_kv_heads, head_dim, block_size, split_pages,
+        min_split_pages, max_split_pages,
         scale, q.stride(0), k_new.stride(0), dtype_code(q.dtype), _stream(),
     )
     _lib.check(code, "cdb_paged_decode_attention")
     return out
 
 
-@torch.library.custom_op("cdb::paged_decode_attention", mutates_args=("kv_pool", "workspace"), device_types="cuda")
+@torch.library.custom_op("cdb::paged_decode_attention", mutates_args=("kv_pool", "workspace"),
+                        device_types="cuda")
 def paged_decode_attention(
     q: torch.Tensor,
     k_new: torch.Tensor,
@@ -212,13 +225,6 @@ def paged_decode_attention(
 def _(q, k_new, v_new, kv_pool, cache_layer, cache_layer0, block_table, table_row, seqlens, rope_cos, rope_sin,
       rope_style, q_bias, k_bias, workspace, block_size, split_pages, scale):
     return torch.empty_like(q)
-
-
-def default_split_pages(num_rows: int, block_size: int) -> int:
-    """Pages per split: smaller splits for narrow batches so the grid stays full."""
-
-    tokens = 256 if num_rows >= 512 else 128 if num_rows >= 64 else 64
-    return max(1, tokens // block_size)
 
 
 def softmax_scale(head_dim: int) -> float:

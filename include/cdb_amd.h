@@ -35,8 +35,11 @@ enum {
 
 enum { CDB_DTYPE_F32 = 0, CDB_DTYPE_BF16 = 1 };
 
-/* Bytes of fp32 workspace cdb_paged_decode_attention needs for num_rows rows
- * whose new-token positions are all < max_seqlen. Returns -1 on bad input. */
+/* Bytes of decode workspace for num_rows rows whose new-token positions are
+ * all < max_seqlen when splits are at least split_pages pages long: a
+ * 256-byte-aligned int32 header of num_rows + 2 entries, then fp32 split
+ * partials. A smaller workspace (but not smaller than the header) is legal: the
+ * kernel then lengthens splits until they fit. Returns -1 on bad input. */
 int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, int32_t head_dim, int32_t max_seqlen,
                                          int32_t block_size, int32_t split_pages);
 
@@ -63,7 +66,12 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
  * output and no KV write. workspace: cdb_paged_decode_workspace_bytes(...).
  * q_stride / kv_stride: elements between consecutive rows of q and of
  * k_new/v_new (0 = dense), so q, k and v may be column slices of one fused
- * QKV projection output. */
+ * QKV projection output.
+ * Context is split into chunks of split_pages pages processed in parallel; with
+ * split_pages <= 0 the kernel picks a power of two in [min_split_pages,
+ * max_split_pages] from the launch's total pages so the work fills the GPU.
+ * Rows with several chunks are merged by a second kernel on the same stream.
+ * Returns CDB_ERR_CAPACITY when workspace_bytes cannot hold the header. */
 int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
                                int64_t layer_stride, int32_t num_cache_layers, int64_t pool_blocks,
                                const int32_t* cache_layer, int32_t cache_layer0, const int32_t* block_table,
@@ -72,7 +80,8 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t max_positions, const void* q_bias, const void* k_bias, void* out,
                                void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
-                               float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
+                               int32_t min_split_pages, int32_t max_split_pages, float scale,
+                               int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
 
 /* Fused RMSNorm sandwich over rows of `width` elements.
  *   norm_w(x) = R(w * R(x * rsqrt(mean(x^2) + eps)))  (R rounds to the storage dtype)

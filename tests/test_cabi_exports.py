@@ -6,6 +6,8 @@ import ctypes
 import re
 from pathlib import Path
 
+import pytest
+
 from continuous_depth_batching_amd import _lib
 
 INCLUDE = Path(__file__).resolve().parent.parent / "include"
@@ -38,5 +40,42 @@ def test_binding_covers_every_declared_symbol() -> None:
 
 def test_workspace_size_query_without_gpu() -> None:
     lib = _lib.lib()
-    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 4 * 4 * 16 * 130 * 4
+    # A 256-byte header (split size + split prefix of 4 rows), then ceil(100 / 32) + 1 splits
+    # per row of (D + 2) floats per head.
+    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 256 + 4 * 5 * 16 * 130 * 4
+    assert lib.cdb_paged_decode_workspace_bytes(100, 16, 128, 100, 16, 2) == 512 + 100 * 5 * 16 * 130 * 4
     assert lib.cdb_paged_decode_workspace_bytes(-1, 16, 128, 100, 16, 2) == -1
+
+
+def _decode_args(**over):
+    # Non-null stand-in addresses: every case below is rejected on the host before any
+    # device work, so the kernel never sees them.
+    fake = ctypes.c_void_p(0x1000)
+    args = dict(q=fake, k_new=fake, v_new=fake, k_pool=fake, v_pool=fake, layer_stride=1 << 20,
+                num_cache_layers=4, pool_blocks=64, cache_layer=None, cache_layer0=0, block_table=fake,
+                table_row=None, table_width=8, seqlens=fake, rope_cos=fake, rope_sin=fake, rope_style=1,
+                max_positions=128, q_bias=None, k_bias=None, out=fake, workspace=fake, workspace_bytes=1 << 20,
+                num_rows=4, num_heads=16, num_kv_heads=16, head_dim=128, block_size=16, split_pages=0,
+                min_split_pages=2, max_split_pages=64, scale=0.088, q_stride=0, kv_stride=0, dtype=1, stream=None)
+    args.update(over)
+    return list(args.values())
+
+
+def test_decode_argument_errors_without_gpu() -> None:
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("runs only where no device exists: the stand-in addresses must never reach a kernel")
+    lib = _lib.lib()
+    call = lambda **kw: lib.cdb_paged_decode_attention(*_decode_args(**kw))
+    assert call(num_rows=0) == _lib.CDB_OK
+    assert call(q=None) == _lib.CDB_ERR_NULL
+    assert call(workspace=None) == _lib.CDB_ERR_NULL
+    assert call(workspace_bytes=255) == _lib.CDB_ERR_CAPACITY  # smaller than the split header
+    assert call(block_size=24) == _lib.CDB_ERR_SHAPE
+    assert call(num_kv_heads=5) == _lib.CDB_ERR_SHAPE
+    assert call(min_split_pages=3) == _lib.CDB_ERR_SHAPE
+    assert call(head_dim=80) == _lib.CDB_ERR_UNSUPPORTED
+    assert call(dtype=7) == _lib.CDB_ERR_UNSUPPORTED
+    assert call(rope_cos=None) == _lib.CDB_ERR_NULL
+    assert call(q_stride=100) == _lib.CDB_ERR_SHAPE

@@ -21,7 +21,8 @@ TOL = {"bf16": (2e-2, 2e-3), "f32": (2e-5, 2e-6)}
 TORCH_DTYPE = {"bf16": torch.bfloat16, "f32": torch.float32}
 
 
-def run_hip(case, split_pages: int, use_table_row: bool = False):
+def run_hip(case, split_pages: int, use_table_row: bool = False, workspace_split: int | None = None,
+            repeats: int = 1):
     from continuous_depth_batching_amd import ops
 
     dev = torch.device("cuda")
@@ -37,16 +38,22 @@ def run_hip(case, split_pages: int, use_table_row: bool = False):
         table = torch.flip(table, dims=[0]).contiguous()
         table_row = torch.arange(num_rows - 1, -1, -1, dtype=torch.int32, device=dev)
     max_pos = int(case.seqlens.max()) + 1
+    ws_split = workspace_split or (split_pages if split_pages > 0 else ops.MIN_SPLIT_PAGES)
     ws = torch.empty(ops.decode_workspace_bytes(num_rows, num_heads, head_dim, max(max_pos, 1), case.block_size,
-                                                split_pages) // 4, dtype=torch.float32, device=dev)
+                                                ws_split) // 4, dtype=torch.float32, device=dev)
     cos = sin = None
     if case.rope_style:
         cos, sin = t(case.rope[0]), t(case.rope[1])
     qb = t(case.q_bias).to(dt) if case.q_bias is not None else None
     kb = t(case.k_bias).to(dt) if case.k_bias is not None else None
-    out = torch.ops.cdb.paged_decode_attention(
-        q, k, v, pool, t(case.cache_layer), 0, table, table_row, t(case.seqlens), cos, sin, case.rope_style,
-        qb, kb, ws, case.block_size, split_pages, case.scale)
+    pool0 = pool.clone()
+    for _ in range(repeats):
+        # Repeats re-run the same append onto a fresh copy of the pool: the workspace header
+        # and partials left by the previous launch must not leak into the next one.
+        pool.copy_(pool0)
+        out = torch.ops.cdb.paged_decode_attention(
+            q, k, v, pool, t(case.cache_layer), 0, table, table_row, t(case.seqlens), cos, sin, case.rope_style,
+            qb, kb, ws, case.block_size, split_pages, case.scale)
     torch.cuda.synchronize()
     return out.float().cpu().numpy(), pool.float().cpu().numpy()
 
@@ -59,8 +66,8 @@ def run_oracle(case):
     return out, pool
 
 
-def check(case, split_pages: int, use_table_row: bool = False) -> None:
-    got, got_pool = run_hip(case, split_pages, use_table_row)
+def check(case, split_pages: int, use_table_row: bool = False, **kw) -> None:
+    got, got_pool = run_hip(case, split_pages, use_table_row, **kw)
     want, want_pool = run_oracle(case)
     live = case.seqlens >= 0
     err = np.abs(got[live] - want[live])
@@ -73,11 +80,24 @@ def check(case, split_pages: int, use_table_row: bool = False) -> None:
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("split_pages", [1, 4, 64])
+@pytest.mark.parametrize("split_pages", [0, 1, 4, 64])
 def test_ouro_shape_mixed_depth(dtype: str, split_pages: int) -> None:
     case = make_case(seed=10, num_rows=24, num_heads=16, num_kv_heads=16, head_dim=128, max_context=700,
                      rope_style=1, dtype=dtype, padding_rows=3)
     check(case, split_pages)
+
+
+def test_adaptive_split_repeated_launches() -> None:
+    case = make_case(seed=16, num_rows=33, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1500,
+                     rope_style=1, dtype="bf16", padding_rows=2)
+    check(case, 0, repeats=3)
+
+
+def test_adaptive_split_grows_to_fit_small_workspace() -> None:
+    # A workspace sized for 64-page splits: the kernel must coarsen its splits to fit it.
+    case = make_case(seed=17, num_rows=12, num_heads=16, num_kv_heads=16, head_dim=128, max_context=3000,
+                     rope_style=1, dtype="bf16")
+    check(case, 0, workspace_split=64)
 
 
 def test_table_row_indirection() -> None:

@@ -140,6 +140,38 @@ def decode_attention_c2_case(prompts, outputs, device):
                                rope_cos=cos, rope_sin=sin, block_size=bs, contexts=contexts)
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per decode-attention call at this shape, from the FETCH_SIZE / WRITE_SIZE
+    counter runs (scaled by a plain copy of known size) recorded under profiles/."""
+
+    path = REPO / "profiles" / "decode_attention_c2_256rows_traffic.json"
+    if not path.exists():
+        return None
+    return int(json.loads(path.read_text())["traffic_bytes_per_call"])
+
+
+def copy_calibration(nbytes: int = 1 << 30, iters: int = 5) -> dict:
+    """A plain device-to-device copy of known size: the yardstick that scales the
+    FETCH_SIZE / WRITE_SIZE counters into HBM bytes, and the copy bandwidth
+    this part reaches in practice."""
+
+    import torch
+
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end) / iters
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms": round(ms, 4),
+            "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     """Numpy oracle decoding a bounded sample of the workload on the host cores."""
 
@@ -191,7 +223,7 @@ def main() -> int:
                                       split_pages=0, iters=args.attention_iters)
     torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(attention["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                 "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_merge_kernel",
                 "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
                 "shape": f"{attention['rows']} rows x 16 heads x 128, mean context {attention['mean_context']:.0f}"}
@@ -206,7 +238,8 @@ def main() -> int:
 
     if args.workload == "decode-attention":
         print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
-                          "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro}))
+                          "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro,
+                          "copy_calibration": copy_calibration()}))
         return 0
 
     model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)

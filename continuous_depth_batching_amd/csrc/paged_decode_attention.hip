@@ -16,10 +16,11 @@
 //   * a row's context is cut into splits of `split_pages` pages; with
 //     split_pages <= 0 every workgroup derives the same split size from the
 //     launch's total page count: the smallest power of two in [min_split_pages,
-//     max_split_pages] for which the items do not outnumber the persistent
-//     workgroups (coarsened further if the workspace is too small). Longer
-//     splits mean fewer partials to merge and fewer per-item latency chains;
-//     shorter ones keep narrow batches from leaving workgroups idle;
+//     max_split_pages] for which the items are at most four times the
+//     persistent workgroups (coarsened further if the workspace is too small).
+//     Longer splits mean fewer partials to merge and fewer per-item latency
+//     chains; shorter ones keep narrow batches from leaving workgroups idle and
+//     even out the tail;
 //   * a work item is (row, split, group of 4 query heads); one workgroup of
 //     4 waves takes an item, wave w owning query head 4*g + w;
 //   * workgroups are persistent: workgroup i processes items i, i+G, ...,
@@ -295,7 +296,7 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
 
   int split_pages = P.split_pages;
   if (split_pages <= 0) {
-    const int64_t target = gridDim.x;
+    const int64_t target = 4ll * gridDim.x;
     const int64_t want = ((int64_t)total_pages * head_groups + target - 1) / target;
     split_pages = P.min_split_pages;
     while (split_pages < want && split_pages < P.max_split_pages) split_pages <<= 1;
@@ -478,7 +479,9 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
 
 // Merge the split partials of every (row, head) whose row has more than one
 // split; one wave per (row, head). Reads the split prefix the decode kernel
-// left in the workspace header.
+// left in the workspace header. Lane s holds split s's (max, sum) so the
+// global max and the denominator are wave reductions; the accumulators are
+// read eight splits at a time so their loads are in flight together.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
   const int lane = threadIdx.x & 63;
@@ -496,16 +499,41 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
   }
   const int64_t stride = (int64_t)P.num_heads * (D + 2);
   const float* part = P.partial + (int64_t)first * stride + (int64_t)h * (D + 2);
-  float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, part[s * stride + D]);
-  float num0 = 0.f, num1 = 0.f, den = 0.f;
   const int d0 = lane, d1 = lane + 64;
-  for (int s = 0; s < nsplit; ++s) {
-    const float* ps = part + s * stride;
-    const float wgt = exp2f(ps[D] - mx);
-    den = fmaf(wgt, ps[D + 1], den);
-    if (d0 < D) num0 = fmaf(wgt, ps[d0], num0);
-    if (d1 < D) num1 = fmaf(wgt, ps[d1], num1);
+  float run_m = -INFINITY, den = 0.f, num0 = 0.f, num1 = 0.f;
+  for (int base = 0; base < nsplit; base += 64) {
+    const int cnt = min(64, nsplit - base);
+    const float* chunk_part = part + (int64_t)base * stride;
+    float ms = -INFINITY, ls = 0.f;
+    if (lane < cnt) {
+      ms = chunk_part[lane * stride + D];
+      ls = chunk_part[lane * stride + D + 1];
+    }
+    const float new_m = fmaxf(run_m, wave_max(ms));
+    const float keep = run_m == -INFINITY ? 0.f : exp2f(run_m - new_m);
+    num0 *= keep;
+    num1 *= keep;
+    den *= keep;
+    const float ws = ms == -INFINITY ? 0.f : exp2f(ms - new_m);
+    den += wave_sum(ws * ls);
+    for (int s0 = 0; s0 < cnt; s0 += 8) {
+      float a0[8], a1[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = s0 + j < cnt;
+        const float* ps = chunk_part + (int64_t)(s0 + j) * stride;
+        a0[j] = ok && d0 < D ? ps[d0] : 0.f;
+        a1[j] = ok && d1 < D ? ps[d1] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // Lanes at or past cnt hold a zero weight.
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ws), min(s0 + j, 63)));
+        num0 = fmaf(wj, a0[j], num0);
+        num1 = fmaf(wj, a1[j], num1);
+      }
+    }
+    run_m = new_m;
   }
   const float inv = 1.f / den;
   if (d0 < D) Elem<T>::store(out_row + d0, num0 * inv);

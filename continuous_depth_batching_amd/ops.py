@@ -21,7 +21,7 @@ _DTYPE_CODES = {torch.float32: _lib.CDB_DTYPE_F32, torch.bfloat16: _lib.CDB_DTYP
 # Decode-attention KV split length in pages: ADAPTIVE_SPLIT lets every launch pick a
 # power of two in [MIN_SPLIT_PAGES, MAX_SPLIT_PAGES] from its own page count.
 ADAPTIVE_SPLIT = 0
-MIN_SPLIT_PAGES = 4
+MIN_SPLIT_PAGES = 8
 MAX_SPLIT_PAGES = 32
 
 

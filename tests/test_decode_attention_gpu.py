@@ -132,6 +132,29 @@ def test_long_context_rows() -> None:
     check(case, 16)
 
 
+def test_more_than_64_splits_per_row() -> None:
+    # One-page splits over ~6000 tokens: the merge walks its partials in chunks of 64.
+    case = make_case(seed=18, num_rows=3, num_heads=4, num_kv_heads=4, head_dim=128, max_context=6000,
+                     min_context=4500, rope_style=1, dtype="bf16")
+    check(case, 1)
+
+
+@pytest.mark.parametrize("block_size,split_pages", [(4, 64), (8, 0), (2, 5)])
+def test_small_pages_cross_window_steps(block_size: int, split_pages: int) -> None:
+    # Pages shorter than a 16-token step: block ids come per lane from the page window,
+    # and steps that would leave the window reload it.
+    case = make_case(seed=19, num_rows=6, num_heads=8, num_kv_heads=4, head_dim=64, max_context=900,
+                     rope_style=1, dtype="bf16", block_size=block_size, padding_rows=1)
+    check(case, split_pages)
+
+
+def test_split_longer_than_page_window() -> None:
+    # 128-page splits: one item walks past its first 64-page window.
+    case = make_case(seed=20, num_rows=3, num_heads=16, num_kv_heads=16, head_dim=128, max_context=5000,
+                     min_context=3000, rope_style=1, dtype="bf16")
+    check(case, 128)
+
+
 def test_out_of_range_row_is_flagged_nan_and_writes_nothing() -> None:
     case = make_case(seed=16, num_rows=3, num_heads=4, num_kv_heads=4, head_dim=64, max_context=40, rope_style=0,
                      dtype="f32")

@@ -26,7 +26,7 @@ from __future__ import annotations
 import time
 from collections import Counter, deque
 from dataclasses import dataclass, field
-from typing import Any
+from typing import Any, Callable
 
 import torch
 
@@ -143,7 +143,13 @@ class ContinuousDepthBatchingEngine:
     # -- construction (continuous_api.py:274-376) -------------------------------------------------------------
     @classmethod
     def from_model(cls, model: Any, cdb_config: ContinuousDepthBatchingConfig, *, dtype: torch.dtype | None = None,
-                   model_adapter: CDBModelAdapter | None = None) -> "ContinuousDepthBatchingEngine":
+                   model_adapter: CDBModelAdapter | None = None,
+                   runner_factory: Callable[..., ModelRunner] | None = None) -> "ContinuousDepthBatchingEngine":
+        """Build the engine for ``model`` (continuous_api.py:274-376).
+
+        ``runner_factory`` replaces the device runner, with ModelRunner's keyword arguments and
+        interface; the engine's scheduling does not depend on which runner executes the stages."""
+
         del dtype
         cfg = cdb_config.get_resolved(model.config)
         adapter = resolve_cdb_model_adapter(model, model_adapter)
@@ -167,7 +173,8 @@ class ContinuousDepthBatchingEngine:
                              num_kv_heads=num_kv_heads, head_dim=head_dim, max_model_len=cfg.max_model_len,
                              max_num_batched_tokens=cfg.max_num_batched_tokens, max_requests=cfg.max_num_seqs,
                              dtype=adapter.dtype, device=adapter.device)
-        runner = ModelRunner(engine_config=cfg, cache=cache, model_adapter=adapter, exit_policy=exit_policy)
+        runner = (runner_factory or ModelRunner)(engine_config=cfg, cache=cache, model_adapter=adapter,
+                                                  exit_policy=exit_policy)
         scheduler = CDBScheduler(cache, cfg.max_recurrent_steps, safety_margin=cfg.safety_margin,
                                  kv_pressure_mode=cfg.kv_pressure_mode, max_model_len=cfg.max_model_len,
                                  max_num_seqs=cfg.max_num_seqs, min_free_slots=cfg.min_free_slots,
@@ -610,6 +617,10 @@ class ContinuousDepthBatchingEngine:
             self.runner.compute_prelude_batch(items)
             survivors = items
             exited: list[DepthWorkItem] = []
+            # On the delayed horizon a launch's decisions route the item after its next launch,
+            # exactly as in the refill loop.
+            delayed = self.exit_policy.delayed()
+            previous: dict[int, tuple[PendingFlags, int]] = {}
             for step in range(max_steps):
                 for item in survivors:
                     item.recurrent_step = step
@@ -619,11 +630,18 @@ class ContinuousDepthBatchingEngine:
                 self.last_stats.recurrent_step_histogram[step] += len(survivors)
                 continuing = []
                 for idx, item in enumerate(survivors):
-                    if step == max_steps - 1 or (item.apply_exit_gate and flags.get(idx)):
+                    if delayed:
+                        prev = previous.pop(id(item), None)
+                        gate_exit = item.apply_exit_gate and prev is not None and prev[0].get(prev[1])
+                    else:
+                        gate_exit = item.apply_exit_gate and flags.get(idx)
+                    if step == max_steps - 1 or gate_exit:
                         self._record_exit(item, step)
                         exited.append(item)
                     else:
                         continuing.append(item)
+                        if delayed:
+                            previous[id(item)] = (flags, idx)
                 self._flush_exit_kv_copies()
                 survivors = continuing
                 if not survivors:

@@ -106,6 +106,18 @@ class PendingFlags:
 
 
 @dataclass
+class PrefillMetadata:
+    tokens: np.ndarray       # [T] int64 chunk tokens
+    positions: np.ndarray    # [T] int32
+    write_rows: np.ndarray   # [T] int64 pool rows
+    cu_q: np.ndarray         # [S+1] int32
+    past: np.ndarray         # [S] int32
+    table_rows: np.ndarray   # [S] int32
+    lens: list[int]
+    last_index: np.ndarray   # [N] int64 sampling rows
+
+
+@dataclass
 class _RecurrentBucket:
     rows: int
     host_i64: torch.Tensor
@@ -277,27 +289,7 @@ class ModelRunner:
         b = self._bucket(rows)
         if b.staged is not None:
             b.staged.synchronize()  # the previous upload from these pinned buffers has completed
-        base = self.layout.core_base
-        core = self.layout.num_core_layers
-        slot_for = self.layout.slot_for_step
-        i64 = b.host_i64.numpy()
-        i32 = b.host_i32.numpy()
-        i64[:n] = [item.hidden_slot for item in items]
-        i32[self.META_POSITIONS, :n] = [item.token_position for item in items]
-        row_of = self.cache.table_row_of
-        i32[self.META_TABLE_ROWS, :n] = [row_of[item.state.request_id] for item in items]
-        steps = [item.recurrent_step for item in items]
-        i32[self.META_STEPS, :n] = steps
-        i32[self.META_LAYER_OFFSET, :n] = [base + slot_for(s) * core for s in steps]
-        i32[self.META_SYNTHETIC, :n] = [-1 if (d := item.synthetic_exit_depth) is None or not item.apply_exit_gate
-                                        else d for item in items]
-        if rows > n:
-            i64[n:] = -1
-            i32[self.META_POSITIONS, n:] = -1
-            i32[self.META_TABLE_ROWS, n:] = 0
-            i32[self.META_LAYER_OFFSET, n:] = base
-            i32[self.META_STEPS, n:] = 0
-            i32[self.META_SYNTHETIC, n:] = -1
+        self.fill_recurrent_metadata(items, b.host_i64.numpy(), b.host_i32.numpy())
         turn = b.turn
         b.turn = (turn + 1) % self.FLAG_TURNS
         if b.flag_events[turn] is not None:
@@ -316,6 +308,35 @@ class ModelRunner:
             event.record()
             b.flag_events[turn] = event
         return PendingFlags(host=host_flags, event=event)
+
+    def fill_recurrent_metadata(self, items: list[DepthWorkItem], i64: np.ndarray, i32: np.ndarray) -> None:
+        """Host metadata of one recurrent launch over a bucket of ``len(i64)`` rows.
+
+        i64[r]: bank slot of row r; i32[META_*, r]: position, block-table row, cache layer of
+        core layer 0 at the row's step (prelude + slot * core layers), loop step, replayed
+        exit depth (-1: none or gate not applied). Rows past ``len(items)`` are padding:
+        slot -1 and position -1 make every kernel skip them
+        (cdb/model_runner.py:704-754 assembles the same per-row facts)."""
+
+        n = len(items)
+        base = self.layout.core_base
+        core = self.layout.num_core_layers
+        slot_for = self.layout.slot_for_step
+        i64[:n] = [item.hidden_slot for item in items]
+        i32[self.META_POSITIONS, :n] = [item.token_position for item in items]
+        row_of = self.cache.table_row_of
+        i32[self.META_TABLE_ROWS, :n] = [row_of[item.state.request_id] for item in items]
+        steps = [item.recurrent_step for item in items]
+        i32[self.META_STEPS, :n] = steps
+        i32[self.META_LAYER_OFFSET, :n] = [base + slot_for(s) * core for s in steps]
+        i32[self.META_SYNTHETIC, :n] = [-1 if (d := item.synthetic_exit_depth) is None or not item.apply_exit_gate
+                                        else d for item in items]
+        i64[n:] = -1
+        i32[self.META_POSITIONS, n:] = -1
+        i32[self.META_TABLE_ROWS, n:] = 0
+        i32[self.META_LAYER_OFFSET, n:] = base
+        i32[self.META_STEPS, n:] = 0
+        i32[self.META_SYNTHETIC, n:] = -1
 
     def capture_all_buckets(self, buckets: Sequence[int] | None = None) -> int:
         """Capture the recurrent-stage graph of every bucket ahead of time.
@@ -400,6 +421,43 @@ class ModelRunner:
         """Full-depth prefill of the scheduled prompt chunks (cb/input_outputs.py:269-379 bookkeeping)."""
 
         cache = self.cache
+        meta = self.prefill_metadata(requests)
+        last_index = meta.last_index
+        tile_seq, tile_q0 = ops.prefill_tiles(meta.lens)
+        with torch.cuda.stream(self.stream):
+            cache.flush_table_updates()
+            launch = PrefillLaunch(
+                tokens=self._to_device(meta.tokens, torch.int64),
+                positions=self._to_device(meta.positions, torch.int32),
+                write_rows=self._to_device(meta.write_rows, torch.int64),
+                cu_q=self._to_device(meta.cu_q, torch.int32),
+                past=self._to_device(meta.past, torch.int32),
+                table_rows=self._to_device(meta.table_rows, torch.int32),
+                tile_seq=self._to_device(tile_seq, torch.int32),
+                tile_q0=self._to_device(tile_q0, torch.int32),
+                last_index=self._to_device(last_index, torch.int64),
+                cache=cache,
+            )
+            if len(last_index):
+                device_tokens = self.adapter.prefill(launch)
+            else:
+                self.adapter.prefill(launch)
+                device_tokens = torch.empty(0, dtype=torch.int64, device=self.device)
+            host = self._pinned((len(last_index),), torch.int64)
+            host.copy_(device_tokens, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+        if not allow_async:
+            event.synchronize()
+        return PendingPrefillResult(futures=list(requests), host_tokens=host, device_tokens=device_tokens,
+                                    ready_event=event)
+
+    def prefill_metadata(self, requests: list[FutureRequestState]) -> "PrefillMetadata":
+        """Host bookkeeping of one prefill launch (cb/input_outputs.py:269-379): the chunk tokens,
+        their positions and pool write rows, cu_q, past lengths, block-table rows, and the index of
+        each sampling row; advances every request's position and marks its sampled token in flight."""
+
+        cache = self.cache
         tokens: list[int] = []
         positions: list[np.ndarray] = []
         rows: list[np.ndarray] = []
@@ -424,34 +482,11 @@ class ModelRunner:
                 last_index.append(cu_q[-1] - 1)
                 state.tokens_to_process = [TMP_TOKEN_ID]
                 state.tokens_in_flight += 1
-        tile_seq, tile_q0 = ops.prefill_tiles(lens)
-        with torch.cuda.stream(self.stream):
-            cache.flush_table_updates()
-            launch = PrefillLaunch(
-                tokens=self._to_device(np.asarray(tokens, dtype=np.int64), torch.int64),
-                positions=self._to_device(np.concatenate(positions), torch.int32),
-                write_rows=self._to_device(np.concatenate(rows), torch.int64),
-                cu_q=self._to_device(np.asarray(cu_q, dtype=np.int32), torch.int32),
-                past=self._to_device(np.asarray(past, dtype=np.int32), torch.int32),
-                table_rows=self._to_device(np.asarray(table_rows, dtype=np.int32), torch.int32),
-                tile_seq=self._to_device(tile_seq, torch.int32),
-                tile_q0=self._to_device(tile_q0, torch.int32),
-                last_index=self._to_device(np.asarray(last_index, dtype=np.int64), torch.int64),
-                cache=cache,
-            )
-            if last_index:
-                device_tokens = self.adapter.prefill(launch)
-            else:
-                self.adapter.prefill(launch)
-                device_tokens = torch.empty(0, dtype=torch.int64, device=self.device)
-            host = self._pinned((len(last_index),), torch.int64)
-            host.copy_(device_tokens, non_blocking=True)
-            event = torch.cuda.Event()
-            event.record()
-        if not allow_async:
-            event.synchronize()
-        return PendingPrefillResult(futures=list(requests), host_tokens=host, device_tokens=device_tokens,
-                                    ready_event=event)
+        return PrefillMetadata(tokens=np.asarray(tokens, dtype=np.int64), positions=np.concatenate(positions),
+                               write_rows=np.concatenate(rows), cu_q=np.asarray(cu_q, dtype=np.int32),
+                               past=np.asarray(past, dtype=np.int32),
+                               table_rows=np.asarray(table_rows, dtype=np.int32), lens=lens,
+                               last_index=np.asarray(last_index, dtype=np.int64))
 
     def consume_prefill_result(self, pending: PendingPrefillResult) -> list[int]:
         if pending.ready_event is not None:

@@ -56,6 +56,25 @@ class RecurrentLaunch:
 
 
 @dataclass
+class StageLaunch:
+    """Device inputs of a prelude or coda launch over ``n`` work items.
+
+    ``positions``, ``table_rows``, ``cache`` and ``workspace`` are set when the adapter's
+    stages attend over their own KV (``stages_use_attention``; the reference's engine then
+    passes the same paged-cache arguments to the prelude and coda, cdb/model_runner.py:1285-1357)."""
+
+    n: int
+    bank: torch.Tensor                 # [capacity, hidden_width] hidden-state bank
+    slots: torch.Tensor                # [n] int64 bank slots of the items
+    tokens: torch.Tensor | None = None         # [n] int64 token ids (prelude)
+    positions: torch.Tensor | None = None      # [n] int32 token positions
+    table_rows: torch.Tensor | None = None     # [n] int32 block-table rows
+    cache: PagedKVCache | None = None
+    workspace: torch.Tensor | None = None      # decode-attention workspace
+    split_pages: int = 0
+
+
+@dataclass
 class PrefillLaunch:
     """Device inputs of one full-depth prefill forward over T prompt tokens."""
 
@@ -112,8 +131,8 @@ class CDBModelAdapter(ABC):
         return self.exit_policy_spec().rule is ExitDecisionRule.PRELOOP_DISTRIBUTION
 
     @abstractmethod
-    def prelude(self, tokens: torch.Tensor, bank: torch.Tensor, slots: torch.Tensor, n: int) -> None:
-        """Write the prelude state of tokens[:n] into bank rows slots[:n]."""
+    def prelude(self, launch: StageLaunch) -> None:
+        """Write the prelude state of launch.tokens into bank rows launch.slots."""
 
     @abstractmethod
     def recurrent_step(self, launch: RecurrentLaunch) -> None:
@@ -124,8 +143,8 @@ class CDBModelAdapter(ABC):
         """Full-depth prefill forward; returns the sampled next tokens [N] int64 of launch.last_index."""
 
     @abstractmethod
-    def coda(self, bank: torch.Tensor, slots: torch.Tensor, n: int) -> torch.Tensor:
-        """Greedy next tokens [n] int64 for the hidden states in bank rows slots[:n]."""
+    def coda(self, launch: StageLaunch) -> torch.Tensor:
+        """Greedy next tokens [n] int64 for the hidden states in bank rows launch.slots."""
 
 
 def resolve_cdb_model_adapter(model: Any, adapter: CDBModelAdapter | None = None) -> CDBModelAdapter:
@@ -141,7 +160,7 @@ def resolve_cdb_model_adapter(model: Any, adapter: CDBModelAdapter | None = None
 
         if OuroCDBAdapter.supports(model):
             return OuroCDBAdapter(model)
-    if model_type == "huginn_raven":
+    if model_type == "huginn":
         from .huginn import HuginnCDBAdapter
 
         if HuginnCDBAdapter.supports(model):

@@ -30,7 +30,7 @@ from . import ops
 from .cache import PagedKVCache
 from .config import ContinuousDepthBatchingConfig
 from .exit_policy import ExitDecisionRule, ExitPolicy
-from .model_adapter import CDBModelAdapter, GateLaunch, PrefillLaunch, RecurrentLaunch
+from .model_adapter import CDBModelAdapter, GateLaunch, PrefillLaunch, RecurrentLaunch, StageLaunch
 from .requests import TMP_TOKEN_ID, DepthWorkItem, FutureRequestState
 
 CODA_PIPELINE_DEPTH = 2
@@ -236,10 +236,28 @@ class ModelRunner:
                                        count=n - num_device)
                 tokens[num_device:].copy_(self._to_device(host_ids.reshape(-1, 1), torch.int64))
             slot_dev = self._to_device(np.asarray(slots, dtype=np.int64), torch.int64)
-            self.adapter.prelude(tokens.view(-1), self.bank, slot_dev, n)
+            self.adapter.prelude(self._stage_launch(items, slot_dev, tokens=tokens.view(-1)))
             self.gate_state.reset(slot_dev, n)
         for item, slot in zip(items, slots):
             item.hidden_slot = slot
+
+    def _stage_launch(self, items: list[DepthWorkItem], slots: torch.Tensor,
+                      tokens: torch.Tensor | None = None) -> StageLaunch:
+        """Prelude/coda inputs; stages with attention also get positions, table rows and the
+        cache, with pending block-table updates applied first."""
+
+        launch = StageLaunch(n=len(items), bank=self.bank, slots=slots, tokens=tokens)
+        if self.adapter.stages_use_attention:
+            self.cache.flush_table_updates()
+            row_of = self.cache.table_row_of
+            launch.positions = self._to_device(np.fromiter((it.token_position for it in items), dtype=np.int32,
+                                                           count=len(items)), torch.int32)
+            launch.table_rows = self._to_device(np.fromiter((row_of[it.state.request_id] for it in items),
+                                                            dtype=np.int32, count=len(items)), torch.int32)
+            launch.cache = self.cache
+            launch.workspace = self.workspace
+            launch.split_pages = ops.ADAPTIVE_SPLIT
+        return launch
 
     # -- recurrent stage -------------------------------------------------------------------------------------
     def _bucket(self, rows: int) -> _RecurrentBucket:
@@ -400,7 +418,7 @@ class ModelRunner:
         with torch.cuda.stream(self.stream):
             slots = self._to_device(np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n),
                                     torch.int64)
-            tokens = self.adapter.coda(self.bank, slots, n)
+            tokens = self.adapter.coda(self._stage_launch(items, slots))
             host = self._pinned((n,), torch.int64)
             host.copy_(tokens, non_blocking=True)
             event = torch.cuda.Event()

@@ -31,7 +31,7 @@ from torch import nn
 from . import ops
 from .exit_policy import DecisionHorizon, ExitDecisionRule, ExitPolicySpec
 from .kv_cache_policy import DEPTH_INDEXED, LoopedKvLayout
-from .model_adapter import CDBModelAdapter, PrefillLaunch, RecurrentLaunch
+from .model_adapter import CDBModelAdapter, PrefillLaunch, RecurrentLaunch, StageLaunch
 
 EXIT_GATE_TYPES = ("early_exit", "lookahead", "preloop")
 
@@ -270,8 +270,8 @@ class OuroCDBAdapter(CDBModelAdapter):
         return ops.GATE_HAZARD, self.gate_w, self.gate_b
 
     # -- stages --------------------------------------------------------------------------------------------------
-    def prelude(self, tokens: torch.Tensor, bank: torch.Tensor, slots: torch.Tensor, n: int) -> None:
-        ops.copy_rows_raw(self.embed, tokens, bank, slots, n)
+    def prelude(self, launch: StageLaunch) -> None:
+        ops.copy_rows_raw(self.embed, launch.tokens, launch.bank, launch.slots, launch.n)
 
     def _layer_stack(self, x: torch.Tensor, residual: torch.Tensor, attend) -> torch.Tensor:
         """Run every layer; x = input_layernorm(residual) on entry. Returns the final-normed hidden."""
@@ -349,8 +349,8 @@ class OuroCDBAdapter(CDBModelAdapter):
         logits = torch.mm(hidden, self.lm_head_w.t())
         return torch.ops.cdb.argmax(logits)
 
-    def coda(self, bank: torch.Tensor, slots: torch.Tensor, n: int) -> torch.Tensor:
-        hidden = torch.ops.cdb.gather_rows(bank, slots[:n])
+    def coda(self, launch: StageLaunch) -> torch.Tensor:
+        hidden = torch.ops.cdb.gather_rows(launch.bank, launch.slots[:launch.n])
         return self.coda_from_hidden(hidden)
 
 

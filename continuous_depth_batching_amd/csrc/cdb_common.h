@@ -20,12 +20,9 @@ struct bf16_t {
 
 CDB_DEVICE float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-CDB_DEVICE uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16 with round-to-nearest-even: one v_cvt_pk_bf16_f32 on gfx950
+// (no branch, so surrounding loads stay batched); NaN stays NaN.
+CDB_DEVICE uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Round an fp32 value to the nearest bf16 and return it as fp32.
 CDB_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }

@@ -25,14 +25,17 @@
 //     4 waves takes an item, wave w owning query head 4*g + w;
 //   * workgroups are persistent: workgroup i processes items i, i+G, ...,
 //     so the grid does not depend on the context lengths (graph-capturable);
-//   * each workgroup builds the per-row split prefix sum in LDS and maps an
-//     item to its row by binary search; workgroup 0 also stores it in the
-//     workspace header for the merge kernel.
+//   * each workgroup builds per-row metadata and split prefix sums in LDS;
+//     items list every full-length split first and the rows' last (shorter)
+//     splits after them, and an item finds its row by binary search;
+//     workgroup 0 also stores the split prefix in the workspace header for the
+//     merge kernel.
 // Inside a wave, lane = 16 * slot + chunk: the 16 lanes of a DPP row split the
 // head dimension into 16 chunks and the 4 rows ("slots") take interleaved
 // tokens. q.k is reduced across a row with four DPP rotate-adds; each slot keeps
-// its own online-softmax state, merged across slots at the end. K/V loads run
-// one 16-token step ahead of the softmax update (two register buffers).
+// its own online-softmax state, merged across slots at the end. An item's first
+// K/V step, its query and the new token's key/value are all issued before the
+// first wait.
 // A row with one split writes its normalized output directly; otherwise the
 // split's (unnormalized acc, max, sum) goes to the workspace and a second
 // kernel merges the splits. The merge is a separate launch on purpose: merging
@@ -114,22 +117,28 @@ CDB_DEVICE void rope_chunk(const DecodeParams& P, int pos, int chunk, const floa
   const float* cos_row = P.rope_cos + (int64_t)pos * half;
   const float* sin_row = P.rope_sin + (int64_t)pos * half;
   if (P.rope_style == 1) {
-    // q*cos + rotate_half(q)*sin with cos/sin = cat(f, f); each op rounded.
+    // q*cos + rotate_half(q)*sin with cos/sin = cat(f, f); each op rounded. A
+    // chunk lies inside one half, so its angles are C consecutive table entries.
+    const int f0 = (chunk * C) % half;
+    Vec<float, C> cv, sv;
+    cv.load(cos_row + f0);
+    sv.load(sin_row + f0);
+    const bool first_half = chunk * C < half;
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-      const int d = chunk * C + i;
-      const int f = d < half ? d : d - half;
-      const float rot = d < half ? -partner[i] : partner[i];
-      const float a = Elem<T>::round(mul_rn(own[i], cos_row[f]));
-      const float b = Elem<T>::round(mul_rn(rot, sin_row[f]));
+      const float rot = first_half ? -partner[i] : partner[i];
+      const float a = Elem<T>::round(mul_rn(own[i], __uint_as_float(cv.w[i])));
+      const float b = Elem<T>::round(mul_rn(rot, __uint_as_float(sv.w[i])));
       out[i] = Elem<T>::round(add_rn(a, b));
     }
   } else {
     // Interleaved (even, odd) pairs rotated in fp32, rounded once at the end.
+    Vec<float, C / 2> cv, sv;
+    cv.load(cos_row + chunk * C / 2);
+    sv.load(sin_row + chunk * C / 2);
 #pragma unroll
     for (int i = 0; i < C; i += 2) {
-      const int f = (chunk * C + i) >> 1;
-      const float c = cos_row[f], s = sin_row[f];
+      const float c = __uint_as_float(cv.w[i / 2]), s = __uint_as_float(sv.w[i / 2]);
       const float x0 = own[i], x1 = own[i + 1];
       out[i] = Elem<T>::round(sub_rn(mul_rn(x0, c), mul_rn(x1, s)));
       out[i + 1] = Elem<T>::round(add_rn(mul_rn(x1, c), mul_rn(x0, s)));
@@ -137,21 +146,33 @@ CDB_DEVICE void rope_chunk(const DecodeParams& P, int pos, int chunk, const floa
   }
 }
 
-// Load this lane's chunk of a [rows, heads, D] vector (plus its split-half
-// partner chunk), add an optional per-head bias, and rotate.
+// This lane's chunk of one head vector and, for split-half RoPE, its partner
+// chunk D/2 away, as loaded (rotation happens later so the loads can be issued
+// early).
 template <typename T, int D>
-CDB_DEVICE void load_rotated(const DecodeParams& P, const T* base, const T* bias, int pos, int chunk, float* out) {
+struct RawChunk {
+  Vec<T, D / 16> own, partner;
+};
+
+template <typename T, int D>
+CDB_DEVICE void load_raw(const DecodeParams& P, const T* base, int chunk, RawChunk<T, D>& r) {
+  constexpr int C = Layout<D>::kChunk;
+  r.own.load(base + chunk * C);
+  if (P.rope_style == 1 && P.rope_cos != nullptr) r.partner.load(base + (chunk ^ 8) * C);
+}
+
+// Add an optional per-head bias to a loaded chunk and rotate it.
+template <typename T, int D>
+CDB_DEVICE void rotate_raw(const DecodeParams& P, const RawChunk<T, D>& r, const T* bias, int pos, int chunk,
+                           float* out) {
   constexpr int C = Layout<D>::kChunk;
   float own[C], partner[C];
-  Vec<T, C> v;
-  v.load(base + chunk * C);
 #pragma unroll
-  for (int i = 0; i < C; ++i) own[i] = v.get(i);
+  for (int i = 0; i < C; ++i) own[i] = r.own.get(i);
   const bool split_half = P.rope_style == 1 && P.rope_cos != nullptr;
   if (split_half) {
-    v.load(base + (chunk ^ 8) * C);
 #pragma unroll
-    for (int i = 0; i < C; ++i) partner[i] = v.get(i);
+    for (int i = 0; i < C; ++i) partner[i] = r.partner.get(i);
   }
   if (bias != nullptr) {
     Vec<T, C> bv;
@@ -165,6 +186,13 @@ CDB_DEVICE void load_rotated(const DecodeParams& P, const T* base, const T* bias
     }
   }
   rope_chunk<T, D>(P, pos, chunk, own, partner, out);
+}
+
+template <typename T, int D>
+CDB_DEVICE void load_rotated(const DecodeParams& P, const T* base, const T* bias, int pos, int chunk, float* out) {
+  RawChunk<T, D> r;
+  load_raw<T, D>(P, base, chunk, r);
+  rotate_raw<T, D>(P, r, bias, pos, chunk, out);
 }
 
 // The block ids of 64 consecutive pages starting at `base`, one per lane
@@ -266,7 +294,8 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   __shared__ int row_pos[kMaxRowsLds];
   __shared__ int row_layer[kMaxRowsLds];
   __shared__ int row_trow[kMaxRowsLds];
-  __shared__ int split_prefix[kMaxRowsLds + 1];
+  __shared__ int split_prefix[kMaxRowsLds + 1];  // splits of rows before b (partial layout)
+  __shared__ int full_prefix[kMaxRowsLds + 1];   // full-length splits of rows before b
   __shared__ int wave_pages[4];
 
   const int tid = threadIdx.x;
@@ -307,13 +336,20 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
 
   for (int b = tid; b < B; b += blockDim.x) {
     const int p = row_pos[b];
-    split_prefix[b + 1] = p >= 0 ? (p + split_tokens) / split_tokens : 0;
+    const int n = p >= 0 ? (p + split_tokens) / split_tokens : 0;
+    split_prefix[b + 1] = n;
+    full_prefix[b + 1] = n > 0 ? n - 1 : 0;
   }
-  if (tid == 0) split_prefix[0] = 0;
+  if (tid == 0) split_prefix[0] = full_prefix[0] = 0;
   __syncthreads();
   lds_prefix(split_prefix, B, wave, lane);
+  lds_prefix(full_prefix, B, wave, lane);
   const int total_splits = split_prefix[B];
-  const int total_items = total_splits * head_groups;
+  const int total_full = full_prefix[B];
+  // Items: every full-length split first (row order), then each row's last,
+  // shorter split, so that round-robin assignment hands out the long items
+  // first and the tail of the grid is made of short ones.
+  const int total_items = (total_full + B) * head_groups;
   const bool overflow = total_splits > P.partial_capacity;
 
   if (blockIdx.x == 0) {
@@ -336,17 +372,25 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   const int64_t row_elems = (int64_t)P.num_kv_heads * D;  // one cached token, all kv heads
 
   for (int item = blockIdx.x; item < total_items; item += gridDim.x) {
-    const int split_global = item / head_groups;
-    const int hg = item - split_global * head_groups;
+    const int g = item / head_groups;
+    const int hg = item - g * head_groups;
     const int h = hg * 4 + wave;
     if (h >= P.num_heads) continue;  // wave-uniform; no block-level sync inside the item loop
-    int lo = 0, hi = B - 1;  // row owning this split: largest b with split_prefix[b] <= split_global
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (split_prefix[mid] <= split_global) lo = mid; else hi = mid - 1;
+    int b, s;
+    if (g < total_full) {
+      int lo = 0, hi = B - 1;  // row owning full split g: largest b with full_prefix[b] <= g
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (full_prefix[mid] <= g) lo = mid; else hi = mid - 1;
+      }
+      b = lo;
+      s = g - full_prefix[b];
+    } else {
+      b = g - total_full;
+      if (row_pos[b] < 0) continue;  // padding or out-of-range row: no work
+      s = split_prefix[b + 1] - split_prefix[b] - 1;
     }
-    const int b = lo;
-    const int s = split_global - split_prefix[b];
+    const int split_global = split_prefix[b] + s;
     const int nsplit = split_prefix[b + 1] - split_prefix[b];
     if (nsplit > 1 && overflow) continue;  // the merge kernel writes NaN for this row
     const int p = row_pos[b];
@@ -371,12 +415,21 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
     };
 
     // Issue the first step's loads before the query rotation so they overlap it.
-    Vec<T, C> ka[4], va[4], kb[4], vb[4];
-    bool vla[4], vlb[4];
+    Vec<T, C> ka[4], va[4];
+    bool vla[4];
     if (t_begin < t_end) {
       cover(t_begin);
       load_step<T, D>(P, window, win_base, k_base, v_base, t_begin, t_end, slot, chunk, kvh, bs_log2, row_elems,
                       ka, va, vla);
+    }
+
+    // The new token's key and value are needed only after the loop; issue their
+    // loads now so they are not one more round trip at the end of the item.
+    RawChunk<T, D> k_raw;
+    Vec<T, C> vn;
+    if (last_split) {
+      load_raw<T, D>(P, k_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D, chunk, k_raw);
+      vn.load(v_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D + chunk * C);
     }
 
     float q[C];
@@ -390,31 +443,22 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
 #pragma unroll
     for (int i = 0; i < C; ++i) acc[i] = 0.f;
 
-    // Two-stage pipeline: the next step's K/V loads are in flight while this step is reduced.
-    for (int t0 = t_begin; t0 < t_end; t0 += 32) {
-      const bool second = t0 + 16 < t_end;
-      if (second) {
-        cover(t0 + 16);
-        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 16, t_end, slot, chunk, kvh, bs_log2,
-                        row_elems, kb, vb, vlb);
+    // One 16-token step per iteration; with three or more waves per SIMD the
+    // other waves' loads cover this wave's wait.
+    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
+      if (t0 != t_begin) {
+        cover(t0);
+        load_step<T, D>(P, window, win_base, k_base, v_base, t0, t_end, slot, chunk, kvh, bs_log2, row_elems,
+                        ka, va, vla);
       }
       attend_step<T, D>(q, ka, va, vla, m, l, acc);
-      if (!second) break;
-      if (t0 + 32 < t_end) {
-        cover(t0 + 32);
-        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 32, t_end, slot, chunk, kvh, bs_log2,
-                        row_elems, ka, va, vla);
-      }
-      attend_step<T, D>(q, kb, vb, vlb, m, l, acc);
     }
 
     if (last_split) {
       // The new token: rotate and append its key/value, then attend to it from registers.
       float kr[C];
       const T* kbias = P.k_bias ? static_cast<const T*>(P.k_bias) + (int64_t)kvh * D : nullptr;
-      load_rotated<T, D>(P, k_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D, kbias, p, chunk, kr);
-      Vec<T, C> vn;
-      vn.load(v_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D + chunk * C);
+      rotate_raw<T, D>(P, k_raw, kbias, p, chunk, kr);
       const int p_page = p >> bs_log2;
       const int new_blk = p_page - win_base < 64 ? __builtin_amdgcn_readlane(window, p_page - win_base)
                                                  : table[p_page];

@@ -50,7 +50,7 @@ def parse_args() -> argparse.Namespace:
                    help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-microbench", action="store_true")
-    p.add_argument("--cpu-sample-tokens", type=int, default=64)
+    p.add_argument("--cpu-sample-tokens", type=int, default=160)
     p.add_argument("--attention-iters", type=int, default=20)
     return p.parse_args()
 

@@ -237,18 +237,45 @@ CDB_DEVICE void load_step(const DecodeParams& P, int window, int win_base, const
   }
 }
 
-// Online-softmax update of one slot's state with its 4 tokens of a wave step.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// a.x * b.x + a.y * b.y + c over packed bf16 pairs, fp32 accumulate (v_dot2c_f32_bf16).
+CDB_DEVICE float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+
+// The query in the form the step loop consumes: fp32 pre-scaled by
+// scale*log2(e) for fp32 pools; for bf16 pools the rotated query's bf16 pairs
+// (exact: RoPE output is rounded to bf16) with the scale applied to each score.
 template <typename T, int D>
-CDB_DEVICE void attend_step(const float* q, const Vec<T, D / 16> (&kv)[4], const Vec<T, D / 16> (&vv)[4],
-                            const bool (&valid)[4], float& m, float& l, float* acc) {
+struct QueryReg {
+  float f[D / 16];
+  uint32_t p[D / 32 > 0 ? D / 32 : 1];
+};
+
+// Online-softmax update of one slot's state with its 4 tokens of a wave step.
+// bf16: q.k is four v_dot2 per token; P.V pairs two tokens' probabilities,
+// rounded to bf16 as flash-attention feeds P to its PV product, against the two
+// tokens' values interleaved with v_perm.
+template <typename T, int D>
+CDB_DEVICE void attend_step(const QueryReg<T, D>& q, float scale_log2, const Vec<T, D / 16> (&kv)[4],
+                            const Vec<T, D / 16> (&vv)[4], const bool (&valid)[4], float& m, float& l, float* acc) {
   constexpr int C = D / 16;
+  constexpr bool kBf16 = sizeof(T) == 2;
   float sc[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     float dot = 0.f;
+    if constexpr (kBf16) {
 #pragma unroll
-    for (int i = 0; i < C; ++i) dot = fmaf(q[i], kv[u].get(i), dot);
-    dot = row16_sum(dot);
+      for (int w = 0; w < C / 2; ++w) dot = dot2_bf16(q.p[w], kv[u].w[w], dot);
+      dot = row16_sum(dot) * scale_log2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < C; ++i) dot = fmaf(q.f[i], kv[u].get(i), dot);
+      dot = row16_sum(dot);
+    }
     sc[u] = valid[u] ? dot : -INFINITY;
   }
   const float m_new = fmaxf(m, fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
@@ -257,46 +284,84 @@ CDB_DEVICE void attend_step(const float* q, const Vec<T, D / 16> (&kv)[4], const
   l *= alpha;
 #pragma unroll
   for (int i = 0; i < C; ++i) acc[i] *= alpha;
+  if constexpr (kBf16) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const float pu = exp2f(sc[u] - m_new);
-    l += pu;
+    for (int u = 0; u < 4; u += 2) {
+      const float p0 = exp2f(sc[u] - m_new), p1 = exp2f(sc[u + 1] - m_new);
+      l += p0 + p1;
+      const bf16x2_t pp = {(__bf16)p0, (__bf16)p1};
+      const uint32_t pk = __builtin_bit_cast(uint32_t, pp);
 #pragma unroll
-    for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, vv[u].get(i), acc[i]);
+      for (int w = 0; w < C / 2; ++w) {
+        const uint32_t a = vv[u].w[w], b = vv[u + 1].w[w];
+        acc[2 * w] = dot2_bf16(pk, __builtin_amdgcn_perm(b, a, 0x05040100u), acc[2 * w]);       // (a.lo, b.lo)
+        acc[2 * w + 1] = dot2_bf16(pk, __builtin_amdgcn_perm(b, a, 0x07060302u), acc[2 * w + 1]);  // (a.hi, b.hi)
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float pu = exp2f(sc[u] - m_new);
+      l += pu;
+#pragma unroll
+      for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, vv[u].get(i), acc[i]);
+    }
   }
   m = m_new;
 }
 
-// Inclusive-to-exclusive prefix over B entries of `a` (a[0] = 0, a[b+1] = count of row b), by wave 0.
-CDB_DEVICE void lds_prefix(int* a, int B, int wave, int lane) {
-  if (wave == 0) {
-    int carry = 0;
-    for (int base = 0; base < B; base += 64) {
-      const int idx = base + lane;
-      int v = idx < B ? a[idx + 1] : 0;
+// In-place exclusive prefix of two count arrays at once: on entry a[b + 1] and
+// c[b + 1] hold row b's counts (a[0] = c[0] = 0); on exit they hold the sums
+// over rows before b + 1. Each of the 256 threads owns a contiguous run of
+// rows; one wave-level scan of the run totals and the wave totals in LDS give
+// every run its offset.
+CDB_DEVICE void block_prefix2(int* a, int* c, int B, int tid, int wave, int lane, int* wave_tot) {
+  const int per = (B + 255) >> 8;
+  const int lo = min(tid * per, B), hi = min(lo + per, B);
+  int sa = 0, sc = 0;
+  for (int b = lo; b < hi; ++b) {
+    sa += a[b + 1];
+    sc += c[b + 1];
+  }
+  int ia = sa, ic = sc;
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int n = __shfl_up(v, off, 64);
-        if (lane >= off) v += n;
-      }
-      if (idx < B) a[idx + 1] = v + carry;
-      carry += __shfl(v, 63, 64);
+  for (int off = 1; off < 64; off <<= 1) {
+    const int na = __shfl_up(ia, off, 64), nc = __shfl_up(ic, off, 64);
+    if (lane >= off) {
+      ia += na;
+      ic += nc;
     }
+  }
+  if (lane == 63) {
+    wave_tot[wave] = ia;
+    wave_tot[4 + wave] = ic;
+  }
+  __syncthreads();
+  int ra = ia - sa, rc = ic - sc;
+  for (int w = 0; w < wave; ++w) {
+    ra += wave_tot[w];
+    rc += wave_tot[4 + w];
+  }
+  for (int b = lo; b < hi; ++b) {
+    ra += a[b + 1];
+    rc += c[b + 1];
+    a[b + 1] = ra;
+    c[b + 1] = rc;
   }
   __syncthreads();
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
+__global__ void __launch_bounds__(256, 4) paged_decode_kernel(DecodeParams P) {
   constexpr int C = Layout<D>::kChunk;
   // Per-row metadata, loaded once per workgroup: new-token position (-1 when the
   // row gets no work), cache layer, block-table row and the split prefix sum.
   __shared__ int row_pos[kMaxRowsLds];
-  __shared__ int row_layer[kMaxRowsLds];
-  __shared__ int row_trow[kMaxRowsLds];
+  __shared__ int row_where[kMaxRowsLds];  // cache layer | block-table row << 16
   __shared__ int split_prefix[kMaxRowsLds + 1];  // splits of rows before b (partial layout)
   __shared__ int full_prefix[kMaxRowsLds + 1];   // full-length splits of rows before b
   __shared__ int wave_pages[4];
+  __shared__ int wave_tot[8];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -312,10 +377,10 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   int pages = 0;
   for (int b = tid; b < B; b += blockDim.x) {
     const int p = P.seqlens[b];
-    const bool ok = row_valid(P, b, p);
+    const int trow = P.table_row ? P.table_row[b] : b;
+    const bool ok = row_valid(P, b, p) && trow >= 0 && trow <= 0xffff;
     row_pos[b] = ok ? p : -1;
-    row_layer[b] = P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0);
-    row_trow[b] = P.table_row ? P.table_row[b] : b;
+    row_where[b] = (P.cache_layer0 + (P.cache_layer ? P.cache_layer[b] : 0)) | (trow << 16);
     pages += ok ? ((p + block_size) >> bs_log2) : 0;
   }
   for (int m = 32; m >= 1; m >>= 1) pages += __shfl_xor(pages, m, 64);
@@ -342,8 +407,7 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   }
   if (tid == 0) split_prefix[0] = full_prefix[0] = 0;
   __syncthreads();
-  lds_prefix(split_prefix, B, wave, lane);
-  lds_prefix(full_prefix, B, wave, lane);
+  block_prefix2(split_prefix, full_prefix, B, tid, wave, lane, wave_tot);
   const int total_splits = split_prefix[B];
   const int total_full = full_prefix[B];
   // Items: every full-length split first (row order), then each row's last,
@@ -395,10 +459,11 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
     if (nsplit > 1 && overflow) continue;  // the merge kernel writes NaN for this row
     const int p = row_pos[b];
     const int kvh = h / kv_group;
-    const int layer = row_layer[b];
+    const int where = row_where[b];
+    const int layer = where & 0xffff;
     T* k_base = static_cast<T*>(P.k_pool) + (int64_t)layer * P.layer_stride;
     T* v_base = static_cast<T*>(P.v_pool) + (int64_t)layer * P.layer_stride;
-    const int32_t* table = P.block_table + (int64_t)row_trow[b] * P.table_width;
+    const int32_t* table = P.block_table + (int64_t)((uint32_t)where >> 16) * P.table_width;
 
     const int t_begin = s * split_tokens;
     const bool last_split = s == nsplit - 1;
@@ -432,11 +497,17 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
       vn.load(v_new_all + (int64_t)b * P.kv_stride + (int64_t)kvh * D + chunk * C);
     }
 
-    float q[C];
+    QueryReg<T, D> q;
     load_rotated<T, D>(P, q_all + (int64_t)b * P.q_stride + (int64_t)h * D,
-                       P.q_bias ? static_cast<const T*>(P.q_bias) + (int64_t)h * D : nullptr, p, chunk, q);
+                       P.q_bias ? static_cast<const T*>(P.q_bias) + (int64_t)h * D : nullptr, p, chunk, q.f);
+    if constexpr (sizeof(T) == 2) {
 #pragma unroll
-    for (int i = 0; i < C; ++i) q[i] *= P.scale_log2;
+      for (int w = 0; w < C / 2; ++w)
+        q.p[w] = (uint32_t)f32_to_bf16(q.f[2 * w]) | ((uint32_t)f32_to_bf16(q.f[2 * w + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < C; ++i) q.f[i] *= P.scale_log2;
+    }
 
     float m = -INFINITY, l = 0.f;
     float acc[C];
@@ -451,7 +522,7 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
         load_step<T, D>(P, window, win_base, k_base, v_base, t0, t_end, slot, chunk, kvh, bs_log2, row_elems,
                         ka, va, vla);
       }
-      attend_step<T, D>(q, ka, va, vla, m, l, acc);
+      attend_step<T, D>(q, P.scale_log2, ka, va, vla, m, l, acc);
     }
 
     if (last_split) {
@@ -473,8 +544,9 @@ __global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
       }
       float dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < C; ++i) dot = fmaf(q[i], kr[i], dot);
+      for (int i = 0; i < C; ++i) dot = fmaf(q.f[i], kr[i], dot);
       dot = row16_sum(dot);
+      if constexpr (sizeof(T) == 2) dot *= P.scale_log2;
       if (slot == 0) {
         const float m_new = fmaxf(m, dot);
         const float alpha = exp2f(m - m_new);
@@ -676,7 +748,8 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
   if (dtype != CDB_DTYPE_F32 && dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
   // Split-half rotation pairs chunk c with chunk c ^ 8, i.e. D/2 = 8 chunks.
   if (rope_style == 1 && (head_dim / 16) * 8 != head_dim / 2) return CDB_ERR_UNSUPPORTED;
-  if (num_cache_layers <= 0 || pool_blocks <= 0 || layer_stride < 0) return CDB_ERR_SHAPE;
+  if (num_cache_layers <= 0 || num_cache_layers > 0xffff || pool_blocks <= 0 || layer_stride < 0)
+    return CDB_ERR_SHAPE;
   const int64_t header = header_bytes(num_rows);
   if (workspace_bytes < header) return CDB_ERR_CAPACITY;
 

@@ -200,6 +200,8 @@ CDB_DEVICE bool better(float a, int ia, float b, int ib) {
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads) argmax_kernel(const T* logits, int64_t* out, int64_t rows, int32_t vocab) {
+  constexpr int V = 16 / sizeof(T);  // elements per 16-byte vector
+  constexpr int kUnroll = 8;         // vectors in flight per thread
   __shared__ float lv[kThreads / 64];
   __shared__ int li[kThreads / 64];
   const int64_t row = blockIdx.x;
@@ -207,7 +209,31 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const T* logits, int64
   const T* x = logits + row * vocab;
   float best = -INFINITY;
   int bi = 0x7fffffff;
-  for (int j = threadIdx.x; j < vocab; j += kThreads) {
+  // Whole 16-byte vectors when the row is aligned, issued kUnroll at a time; the
+  // order in which a thread meets its elements does not matter since ties are
+  // broken by index.
+  const bool aligned = (vocab % V) == 0 && ((uintptr_t)x & 15) == 0;
+  const int nvec = aligned ? vocab / V : 0;
+  for (int base = threadIdx.x; base < nvec; base += kThreads * kUnroll) {
+    Vec<T, V> buf[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int vi = base + u * kThreads;
+      if (vi < nvec) buf[u].load(x + (int64_t)vi * V);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int vi = base + u * kThreads;
+      if (vi >= nvec) continue;
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const float v = buf[u].get(e);
+        const int j = vi * V + e;
+        if (better(v, j, best, bi)) { best = v; bi = j; }
+      }
+    }
+  }
+  for (int j = nvec * V + threadIdx.x; j < vocab; j += kThreads) {
     const float v = Elem<T>::load(x + j);
     if (better(v, j, best, bi)) { best = v; bi = j; }
   }

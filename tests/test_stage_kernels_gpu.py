@@ -101,9 +101,20 @@ def test_argmax_first_max_bit_exact(dtype: str) -> None:
     rng = np.random.default_rng(2)
     logits = rounder(dtype)(rng.standard_normal((65, 49152)).astype(np.float32))
     logits[3, [10, 20000, 49151]] = 50.0  # ties: first wins
+    logits[4, [7, 30000]] = np.nan  # a NaN counts as the maximum, first one wins
+    logits[5, :] = -np.inf
     got = torch.ops.cdb.argmax(dev(logits, DT[dtype])).cpu().numpy()
     np.testing.assert_array_equal(got, stage.argmax(logits))
     np.testing.assert_array_equal(got, torch.from_numpy(logits).argmax(-1).numpy())
+
+
+@pytest.mark.parametrize("vocab", [1001, 8, 65536 + 5])
+def test_argmax_unaligned_and_tail_vocab(vocab: int) -> None:
+    rng = np.random.default_rng(vocab)
+    logits = rounder("bf16")(rng.standard_normal((9, vocab)).astype(np.float32))
+    logits[0, vocab - 1] = 99.0  # the maximum in the scalar tail
+    got = torch.ops.cdb.argmax(dev(logits, DT["bf16"])).cpu().numpy()
+    np.testing.assert_array_equal(got, stage.argmax(logits))
 
 
 @pytest.mark.parametrize("delayed", [False, True])

@@ -37,6 +37,7 @@ REPO = Path(__file__).resolve().parent
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s
 EXIT_PROBS = (0.15, 0.25, 0.30, 0.30)
 
 
@@ -150,6 +151,51 @@ def measured_traffic() -> int | None:
     return int(json.loads(path.read_text())["traffic_bytes_per_call"])
 
 
+def time_prefill_attention(prompt_lens, iters: int) -> dict:
+    """Average duration of one prefill-attention launch over a batch of fresh prompts, on its stream."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops, workloads
+
+    case = workloads.prefill_attention_batch(lens=prompt_lens)
+    view = ops.KVPoolView(case.kv_pool, case.block_size)
+    out = torch.empty_like(case.q)
+    stream = torch.cuda.Stream()
+
+    def launch():
+        ops.prefill_attention_raw(case.q, view, 0, case.block_table, case.table_row, case.cu_q, case.past,
+                                  case.tile_seq, case.tile_q0, out, case.q.shape[-1] ** -0.5)
+
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            launch()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            launch()
+        end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / iters
+    flops = case.flops()
+    return {"ms": round(ms, 4), "flops": flops, "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "tokens": int(case.lens.sum()),
+            "sequences": int(case.lens.size), "max_len": int(case.lens.max())}
+
+
+def first_prefill_batch(prompts, token_budget: int = 8192) -> list[int]:
+    """Prompt lengths of the workload's first full prefill batch (prompts admitted in order while
+    they fit the engine's token budget)."""
+
+    lens, total = [], 0
+    for p in prompts:
+        if total + len(p) > token_budget:
+            break
+        lens.append(len(p))
+        total += len(p)
+    return lens
+
+
 def copy_calibration(nbytes: int = 1 << 30, iters: int = 5) -> dict:
     """A plain device-to-device copy of known size: the yardstick that scales the
     FETCH_SIZE / WRITE_SIZE counters into HBM bytes, and the copy bandwidth
@@ -236,9 +282,15 @@ def main() -> int:
         del case
         torch.cuda.empty_cache()
 
+    prefill = time_prefill_attention(first_prefill_batch(prompts), iters=max(3, args.attention_iters // 4))
+    prefill["shape"] = (f"{prefill['sequences']} fresh prompts, {prefill['tokens']} tokens (max {prefill['max_len']}), "
+                        "16 heads x 128, causal")
+    torch.cuda.empty_cache()
+
     if args.workload == "decode-attention":
         print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
                           "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro,
+                          "prefill_attention": prefill,
                           "copy_calibration": copy_calibration()}))
         return 0
 
@@ -283,6 +335,7 @@ def main() -> int:
                    "global_batch": args.num_seqs, "parallelism": "none"},
         "roofline": roofline,
         "decode_attention_microbench": micro,
+        "prefill_attention": prefill,
         "engine": {"generated_tokens": generated, "recurrent_batches": stats.recurrent_batches,
                    "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),
                    "coda_batches": stats.coda_batches, "prefill_batches": stats.prefill_batches,

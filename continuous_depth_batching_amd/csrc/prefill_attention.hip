@@ -54,6 +54,7 @@ struct PrefillParams {
 
 constexpr int kKeys = 32;      // keys per block
 constexpr int kQTile = 64;     // queries per workgroup
+constexpr int kLdsPages = 1024;  // block ids kept in LDS per workgroup (longer prefixes read the table)
 
 template <typename T> struct Mfma;
 
@@ -87,8 +88,11 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
   constexpr int kVtPad = V;
   static_assert(D % (4 * V) == 0, "head_dim must split into 4 lane groups of 16-byte vectors");
 
-  __shared__ __attribute__((aligned(16))) T k_lds[kKeys][D + kKPad];
-  __shared__ __attribute__((aligned(16))) T vt_lds[D][kKeys + kVtPad];
+  // Two key blocks in flight: the next block's K/V is loaded into registers
+  // while the current one is multiplied, then stored to the other buffer.
+  __shared__ __attribute__((aligned(16))) T k_lds[2][kKeys][D + kKPad];
+  __shared__ __attribute__((aligned(16))) T vt_lds[2][D][kKeys + kVtPad];
+  __shared__ int page_lds[kLdsPages];
 
   const int tile = blockIdx.x;
   const int h = blockIdx.y;
@@ -143,36 +147,72 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
   const int wave_last = min(tile_q0 + wave * 16 + 15, q_len - 1);  // last query of this wave
   const int wave_key_end = past + wave_last + 1;
 
-  for (int kb = 0; kb < key_end; kb += kKeys) {
-    // Stage K (row-major) and V (transposed) of keys kb .. kb+31 in LDS.
-    constexpr int kUnitsPerKey = D / V;
+  // Block ids of the prefix, once per workgroup.
+  const int key_pages = (key_end + bs_mask) >> bs_log2;
+  const bool pages_in_lds = key_pages <= kLdsPages;
+  if (pages_in_lds) {
+    for (int i = tid; i < key_pages; i += 256) page_lds[i] = i < P.table_width ? table[i] : -1;
+  }
+  __syncthreads();
+
+  constexpr int kUnitsPerKey = D / V;
+  constexpr int kUnits = kKeys * kUnitsPerKey;
+  constexpr int kUnitsPerThread = (kUnits + 255) / 256;
+  Vec<T, V> kreg[kUnitsPerThread], vreg[kUnitsPerThread];
+  // Global -> registers for keys kb .. kb+31 (zeros past key_end or for unmapped pages).
+  auto load_block = [&](int kb) {
 #pragma unroll
-    for (int u = tid; u < kKeys * kUnitsPerKey; u += 256) {
+    for (int r = 0; r < kUnitsPerThread; ++r) {
+      const int u = tid + r * 256;
       const int key = u / kUnitsPerKey;
       const int dc = (u - key * kUnitsPerKey) * V;
       const int kp = kb + key;
-      Vec<T, V> kvv, vvv;
-      const int blk = (kp < key_end && (kp >> bs_log2) < P.table_width) ? table[kp >> bs_log2] : -1;
+      int blk = -1;
+      if (u < kUnits && kp < key_end) {
+        const int page = kp >> bs_log2;
+        blk = pages_in_lds ? page_lds[page] : (page < P.table_width ? table[page] : -1);
+      }
       if (blk >= 0 && blk < P.pool_blocks) {
         const int64_t off = ((int64_t)blk * (bs_mask + 1) + (kp & bs_mask)) * row_elems + (int64_t)kvh * D + dc;
-        kvv.load(k_base + off);
-        vvv.load(v_base + off);
+        kreg[r].load(k_base + off);
+        vreg[r].load(v_base + off);
       } else {
 #pragma unroll
-        for (int w = 0; w < Vec<T, V>::kWords; ++w) kvv.w[w] = vvv.w[w] = 0u;
+        for (int w = 0; w < Vec<T, V>::kWords; ++w) kreg[r].w[w] = vreg[r].w[w] = 0u;
       }
-      kvv.store(&k_lds[key][dc]);
+    }
+  };
+  // Registers -> LDS buffer `buf`: K row-major, V transposed.
+  auto store_block = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < kUnitsPerThread; ++r) {
+      const int u = tid + r * 256;
+      if (u >= kUnits) continue;
+      const int key = u / kUnitsPerKey;
+      const int dc = (u - key * kUnitsPerKey) * V;
+      kreg[r].store(&k_lds[buf][key][dc]);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         if constexpr (sizeof(T) == 2) {
-          reinterpret_cast<uint16_t*>(&vt_lds[dc + i][key])[0] =
-              (uint16_t)((vvv.w[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
+          reinterpret_cast<uint16_t*>(&vt_lds[buf][dc + i][key])[0] =
+              (uint16_t)((vreg[r].w[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
         } else {
-          reinterpret_cast<uint32_t*>(&vt_lds[dc + i][key])[0] = vvv.w[i];
+          reinterpret_cast<uint32_t*>(&vt_lds[buf][dc + i][key])[0] = vreg[r].w[i];
         }
       }
     }
-    __syncthreads();
+  };
+
+  if (key_end > 0) {
+    load_block(0);
+    store_block(0);
+  }
+  __syncthreads();
+
+  int buf = 0;
+  for (int kb = 0; kb < key_end; kb += kKeys, buf ^= 1) {
+    const bool has_next = kb + kKeys < key_end;
+    if (has_next) load_block(kb + kKeys);  // in flight during this block's products
 
     if (kb < wave_key_end) {
       // S^T for key tiles 0 (keys kb..kb+15) and 1 (kb+16..kb+31): lane holds keys 4*grp+i.
@@ -183,7 +223,7 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
 #pragma unroll
         for (int c = 0; c < kChunks; ++c) {
           Vec<T, V> kv;
-          kv.load(&k_lds[t * 16 + col][c * 4 * V + grp * V]);
+          kv.load(&k_lds[buf][t * 16 + col][c * 4 * V + grp * V]);
           st[t] = Mfma<T>::mma(kv, qv[c], st[t]);
         }
       }
@@ -228,7 +268,7 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
 #pragma unroll
         for (int j = 0; j < kDTiles; ++j) {
           Vec<T, 8> va;
-          const T* vrow = &vt_lds[j * 16 + col][0];
+          const T* vrow = &vt_lds[buf][j * 16 + col][0];
           const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 4 * grp);
           const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + 4 * grp);
           va.w[0] = lo.x; va.w[1] = lo.y; va.w[2] = hi.x; va.w[3] = hi.y;
@@ -244,12 +284,13 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
 #pragma unroll
           for (int j = 0; j < kDTiles; ++j) {
             Vec<T, 4> va;
-            va.load(&vt_lds[j * 16 + col][16 * t + 4 * grp]);
+            va.load(&vt_lds[buf][j * 16 + col][16 * t + 4 * grp]);
             o[j] = Mfma<T>::mma(va, pb, o[j]);
           }
         }
       }
     }
+    if (has_next) store_block(buf ^ 1);
     __syncthreads();
   }
 

@@ -108,6 +108,55 @@ def decode_attention_microbench(
     )
 
 
+@dataclass
+class PrefillAttentionCase:
+    """A fresh-prompt prefill batch: every sequence attends causally over its own prompt."""
+
+    q: torch.Tensor            # [T, H, D] rotated queries
+    kv_pool: torch.Tensor      # [1, 2, rows, Hkv, D]
+    block_table: torch.Tensor  # [S, W] int32
+    table_row: torch.Tensor    # [S] int32
+    cu_q: torch.Tensor         # [S+1] int32
+    past: torch.Tensor         # [S] int32 (zeros: fresh prompts)
+    tile_seq: torch.Tensor
+    tile_q0: torch.Tensor
+    lens: np.ndarray
+    block_size: int
+
+    def flops(self) -> int:
+        """4 * H * D * causal (query, key) pairs: QK^T and PV, 2 flops per multiply-add."""
+
+        _, h, d = self.q.shape
+        pairs = int((self.lens * (self.lens + 1) // 2).sum())
+        return 4 * h * d * pairs
+
+
+def prefill_attention_batch(*, lens: np.ndarray, num_heads: int = 16, head_dim: int = 128, block_size: int = 16,
+                            seed: int = 0, dtype: torch.dtype = torch.bfloat16,
+                            device: torch.device | str = "cuda") -> PrefillAttentionCase:
+    from . import ops
+
+    device = torch.device(device)
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    pages = (lens + block_size - 1) // block_size
+    perm = rng.permutation(int(pages.sum())).astype(np.int32)
+    table = np.full((lens.size, int(pages.max())), -1, dtype=np.int32)
+    off = np.concatenate([[0], np.cumsum(pages)])
+    for s in range(lens.size):
+        table[s, : pages[s]] = perm[off[s]: off[s + 1]]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    pool = torch.empty((1, 2, int(pages.sum()) * block_size, num_heads, head_dim), dtype=dtype, device=device)
+    pool.normal_(generator=gen)
+    q = torch.randn((int(lens.sum()), num_heads, head_dim), generator=gen, device=device).to(dtype)
+    tile_seq, tile_q0 = ops.prefill_tiles(lens)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(device)
+    return PrefillAttentionCase(q=q, kv_pool=pool, block_table=i32(table), table_row=i32(np.arange(lens.size)),
+                                cu_q=i32(np.concatenate([[0], np.cumsum(lens)])), past=i32(np.zeros(lens.size)),
+                                tile_seq=i32(tile_seq), tile_q0=i32(tile_q0), lens=lens, block_size=block_size)
+
+
 def lognormal_lengths(rng: np.random.Generator, n: int, mu: float, sigma: float, lo: int, hi: int) -> np.ndarray:
     return np.clip(np.rint(rng.lognormal(mu, sigma, size=n)), lo, hi).astype(np.int64)
 

@@ -85,7 +85,9 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
   constexpr int kChunks = D / (4 * V);      // 16-byte vectors per lane across D
   constexpr int kDTiles = D / 16;           // output tiles of 16 head-dim rows
   constexpr int kKPad = V;                  // LDS row padding (elements) against bank conflicts
-  constexpr int kVtPad = V;
+  // V^T rows of 36 elements: the transposed stores below (one dword per key pair,
+  // 16 pairs x 4 d-chunks per wave) then land in 64 distinct banks.
+  constexpr int kVtPad = 4;
   static_assert(D % (4 * V) == 0, "head_dim must split into 4 lane groups of 16-byte vectors");
 
   // Two key blocks in flight: the next block's K/V is loaded into registers
@@ -155,49 +157,64 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
   }
   __syncthreads();
 
-  constexpr int kUnitsPerKey = D / V;
-  constexpr int kUnits = kKeys * kUnitsPerKey;
-  constexpr int kUnitsPerThread = (kUnits + 255) / 256;
-  Vec<T, V> kreg[kUnitsPerThread], vreg[kUnitsPerThread];
+  // Staging work: (16-byte d-chunk, key pair) combinations. A thread loads both
+  // keys of its pair so it can store V^T one key pair per dword (bf16) or per
+  // 8 bytes (fp32) instead of one element at a time.
+  constexpr int kChunksPerKey = D / V;
+  constexpr int kPairs = kKeys / 2;
+  constexpr int kCombos = kChunksPerKey * kPairs;
+  constexpr int kCombosPerThread = (kCombos + 255) / 256;
+  Vec<T, V> kreg[2 * kCombosPerThread], vreg[2 * kCombosPerThread];
   // Global -> registers for keys kb .. kb+31 (zeros past key_end or for unmapped pages).
   auto load_block = [&](int kb) {
 #pragma unroll
-    for (int r = 0; r < kUnitsPerThread; ++r) {
-      const int u = tid + r * 256;
-      const int key = u / kUnitsPerKey;
-      const int dc = (u - key * kUnitsPerKey) * V;
-      const int kp = kb + key;
-      int blk = -1;
-      if (u < kUnits && kp < key_end) {
-        const int page = kp >> bs_log2;
-        blk = pages_in_lds ? page_lds[page] : (page < P.table_width ? table[page] : -1);
-      }
-      if (blk >= 0 && blk < P.pool_blocks) {
-        const int64_t off = ((int64_t)blk * (bs_mask + 1) + (kp & bs_mask)) * row_elems + (int64_t)kvh * D + dc;
-        kreg[r].load(k_base + off);
-        vreg[r].load(v_base + off);
-      } else {
+    for (int r = 0; r < kCombosPerThread; ++r) {
+      const int combo = tid + r * 256;
+      const int c = combo / kPairs;
+      const int pair = combo - c * kPairs;
 #pragma unroll
-        for (int w = 0; w < Vec<T, V>::kWords; ++w) kreg[r].w[w] = vreg[r].w[w] = 0u;
+      for (int e = 0; e < 2; ++e) {
+        const int kp = kb + 2 * pair + e;
+        int blk = -1;
+        if (combo < kCombos && kp < key_end) {
+          const int page = kp >> bs_log2;
+          blk = pages_in_lds ? page_lds[page] : (page < P.table_width ? table[page] : -1);
+        }
+        Vec<T, V>& kr = kreg[2 * r + e];
+        Vec<T, V>& vr = vreg[2 * r + e];
+        if (blk >= 0 && blk < P.pool_blocks) {
+          const int64_t off =
+              ((int64_t)blk * (bs_mask + 1) + (kp & bs_mask)) * row_elems + (int64_t)kvh * D + c * V;
+          kr.load(k_base + off);
+          vr.load(v_base + off);
+        } else {
+#pragma unroll
+          for (int w = 0; w < Vec<T, V>::kWords; ++w) kr.w[w] = vr.w[w] = 0u;
+        }
       }
     }
   };
   // Registers -> LDS buffer `buf`: K row-major, V transposed.
   auto store_block = [&](int buf) {
 #pragma unroll
-    for (int r = 0; r < kUnitsPerThread; ++r) {
-      const int u = tid + r * 256;
-      if (u >= kUnits) continue;
-      const int key = u / kUnitsPerKey;
-      const int dc = (u - key * kUnitsPerKey) * V;
-      kreg[r].store(&k_lds[buf][key][dc]);
+    for (int r = 0; r < kCombosPerThread; ++r) {
+      const int combo = tid + r * 256;
+      if (combo >= kCombos) continue;
+      const int c = combo / kPairs;
+      const int pair = combo - c * kPairs;
+      kreg[2 * r].store(&k_lds[buf][2 * pair][c * V]);
+      kreg[2 * r + 1].store(&k_lds[buf][2 * pair + 1][c * V]);
 #pragma unroll
       for (int i = 0; i < V; ++i) {
         if constexpr (sizeof(T) == 2) {
-          reinterpret_cast<uint16_t*>(&vt_lds[buf][dc + i][key])[0] =
-              (uint16_t)((vreg[r].w[i >> 1] >> ((i & 1) * 16)) & 0xffffu);
+          const uint32_t a = vreg[2 * r].w[i >> 1], b = vreg[2 * r + 1].w[i >> 1];
+          // (key 2*pair, key 2*pair+1) of element i: low or high halves of a and b.
+          const uint32_t packed = (i & 1) ? __builtin_amdgcn_perm(b, a, 0x07060302u)
+                                          : __builtin_amdgcn_perm(b, a, 0x05040100u);
+          *reinterpret_cast<uint32_t*>(&vt_lds[buf][c * V + i][2 * pair]) = packed;
         } else {
-          reinterpret_cast<uint32_t*>(&vt_lds[buf][dc + i][key])[0] = vreg[r].w[i];
+          *reinterpret_cast<uint2*>(&vt_lds[buf][c * V + i][2 * pair]) =
+              make_uint2(vreg[2 * r].w[i], vreg[2 * r + 1].w[i]);
         }
       }
     }

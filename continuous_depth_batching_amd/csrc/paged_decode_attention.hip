@@ -35,7 +35,8 @@
 // tokens. q.k is reduced across a row with four DPP rotate-adds; each slot keeps
 // its own online-softmax state, merged across slots at the end. An item's first
 // K/V step, its query and the new token's key/value are all issued before the
-// first wait.
+// first wait, and every later step's loads are issued one step ahead (two
+// register buffers).
 // A row with one split writes its normalized output directly; otherwise the
 // split's (unnormalized acc, max, sum) goes to the workspace and a second
 // kernel merges the splits. The merge is a separate launch on purpose: merging
@@ -352,7 +353,7 @@ CDB_DEVICE void block_prefix2(int* a, int* c, int B, int tid, int wave, int lane
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 4) paged_decode_kernel(DecodeParams P) {
+__global__ void __launch_bounds__(256) paged_decode_kernel(DecodeParams P) {
   constexpr int C = Layout<D>::kChunk;
   // Per-row metadata, loaded once per workgroup: new-token position (-1 when the
   // row gets no work), cache layer, block-table row and the split prefix sum.
@@ -480,8 +481,8 @@ __global__ void __launch_bounds__(256, 4) paged_decode_kernel(DecodeParams P) {
     };
 
     // Issue the first step's loads before the query rotation so they overlap it.
-    Vec<T, C> ka[4], va[4];
-    bool vla[4];
+    Vec<T, C> ka[4], va[4], kb[4], vb[4];
+    bool vla[4], vlb[4];
     if (t_begin < t_end) {
       cover(t_begin);
       load_step<T, D>(P, window, win_base, k_base, v_base, t_begin, t_end, slot, chunk, kvh, bs_log2, row_elems,
@@ -514,15 +515,22 @@ __global__ void __launch_bounds__(256, 4) paged_decode_kernel(DecodeParams P) {
 #pragma unroll
     for (int i = 0; i < C; ++i) acc[i] = 0.f;
 
-    // One 16-token step per iteration; with three or more waves per SIMD the
-    // other waves' loads cover this wave's wait.
-    for (int t0 = t_begin; t0 < t_end; t0 += 16) {
-      if (t0 != t_begin) {
-        cover(t0);
-        load_step<T, D>(P, window, win_base, k_base, v_base, t0, t_end, slot, chunk, kvh, bs_log2, row_elems,
-                        ka, va, vla);
+    // Two-stage pipeline: the next step's K/V loads are in flight while this step is reduced.
+    for (int t0 = t_begin; t0 < t_end; t0 += 32) {
+      const bool second = t0 + 16 < t_end;
+      if (second) {
+        cover(t0 + 16);
+        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 16, t_end, slot, chunk, kvh, bs_log2,
+                        row_elems, kb, vb, vlb);
       }
       attend_step<T, D>(q, P.scale_log2, ka, va, vla, m, l, acc);
+      if (!second) break;
+      if (t0 + 32 < t_end) {
+        cover(t0 + 32);
+        load_step<T, D>(P, window, win_base, k_base, v_base, t0 + 32, t_end, slot, chunk, kvh, bs_log2,
+                        row_elems, ka, va, vla);
+      }
+      attend_step<T, D>(q, P.scale_log2, kb, vb, vlb, m, l, acc);
     }
 
     if (last_split) {

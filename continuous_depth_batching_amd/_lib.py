@@ -84,6 +84,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P,  # H, Hkv, D, block_size, scale, dtype, stream
         ],
     ),
+    "cdb_linear_pack_weight": (c_int32, [_P, c_int64, _P, c_int64, c_int32, c_int32, _P]),
+    "cdb_linear": (
+        c_int32,
+        [
+            _P, c_int64, _P, _P, c_int64,  # x, ldx, w_packed, y, ldy
+            c_int32, c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, gated, dtype, stream
+        ],
+    ),
 }
 
 

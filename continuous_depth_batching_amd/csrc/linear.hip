@@ -1,0 +1,283 @@
+// Decode-batch dense projection y = x W^T on MFMA tiles (CDNA4), for the few
+// rows a recurrent launch carries.
+//
+// Replaces the nn.Linear projections of a recurrent step as the reference runs
+// them through torch (q/k/v/o_proj ouro/modeling_ouro.py:371-374,390-392,431;
+// gate/up/down_proj :162-168; Huginn Wqkv/proj/fc/adapter
+// huginn/modeling_huginn.py:239-242,310-316,372). With at most 64 rows the
+// product is bound by streaming W from HBM (2 flops per weight element per
+// row, far under the MFMA ridge), so the kernel is built to keep that stream
+// deep rather than to reuse tiles:
+//   * W is stored pre-packed in MFMA operand order (cdb_linear_pack_weight):
+//     for each tile of 16 rows and each 32-element contraction step, the 1 KiB
+//     block that one wave loads as its A operand -- lane (r, g) holding
+//     W[16 t + r][32 s + 8 g .. +8] -- is contiguous, and a tile's blocks follow
+//     each other along K. Every weight load is one fully contiguous 1 KiB wave
+//     access, and a wave's batch of S steps is S KiB in a row;
+//   * a workgroup owns NB tiles of 16 output columns and splits the contraction
+//     dimension K between its waves; every weight element is read exactly once,
+//     with non-temporal loads so x stays resident in L2;
+//   * MFMA 16x16x32 bf16 with A = 16 rows of W and B = x^T (up to 4 tiles of
+//     16 rows of x): lane (m, g) loads x[m][32 s + 8 g .. +8], the same
+//     contraction indices as its A vector, and the accumulator C[n][m] lands
+//     in lane (m % 16, n / 4);
+//   * the waves' partial tiles are summed in LDS in a fixed order (slot w holds
+//     wave w + wave w+8), so results do not depend on scheduling;
+//   * gated mode (the MLP's gate_up): the workgroup also owns the matching 16
+//     up-projection rows W[N + n] and writes R(R(silu(R(g))) * R(u)) directly,
+//     the rounding chain of torch's bf16 silu and multiply, so the [rows, 2N]
+//     gate_up activation never reaches memory.
+// Output rows are rounded to bf16 once, after the fp32 sum over all of K.
+
+#include "cdb_common.h"
+#include "../../include/cdb_amd.h"
+
+namespace cdb {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+struct LinearParams {
+  const bf16_t* x;  // [M, K], row stride ldx elements
+  const bf16_t* w;  // packed [N, K] (gated: [2N, K], gate rows then up rows)
+  bf16_t* y;        // [M, N], row stride ldy
+  int64_t ldx, ldy;
+  int32_t M, N, K;
+  int32_t steps_per_wave;  // 32-element contraction steps per wave
+};
+
+constexpr int kLinearMaxRows = 64;
+constexpr int kLinearMaxWaves = 16;
+
+CDB_DEVICE bf16x8_t load_w(const bf16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(p));
+}
+CDB_DEVICE bf16x8_t load_x(const bf16_t* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
+
+// MT: 16-row tiles of x (1, 2 or 4). NB: 16-column tiles of y per workgroup; every
+// wave computes all of them, so each x vector it loads feeds NB (gated: 2*NB)
+// MFMAs. S: contraction steps loaded per batch. SLOTS: LDS partial tiles (waves
+// w, w + SLOTS, w + 2*SLOTS, ... add into slot w in that order).
+template <int MT, int NB, int S, int SLOTS, bool GATED, int MAXT>
+__global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
+  constexpr int NT = GATED ? 2 * NB : NB;  // W row tiles: gate tiles, then up tiles
+  __shared__ f32x4_t red[SLOTS][NT][MT][kWave];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  // Wave-uniform in a scalar register, so the step loop and its bounds stay scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nwaves = blockDim.x / kWave;
+  const int r = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16 * NB;
+
+  // Packed W: the block of tile t, step s starts at element (t * steps + s) * 512.
+  const int total = p.K / 32;
+  const bf16_t* wrow[NT];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    wrow[j] = p.w + ((int64_t)(n0 / 16 + j) * total) * 512 + 8 * lane;
+    if constexpr (GATED) wrow[NB + j] = p.w + ((int64_t)((p.N + n0) / 16 + j) * total) * 512 + 8 * lane;
+  }
+  const bf16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = p.x + (int64_t)min(mt * 16 + r, p.M - 1) * p.ldx + 8 * g;
+
+  f32x4_t acc[NT][MT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int s_begin = wave * p.steps_per_wave;
+  const int s_end = min(s_begin + p.steps_per_wave, total);
+  for (int s = s_begin; s < s_end; s += S) {
+    // Straight-line batch of S steps: steps past the wave's range (only in the last
+    // wave's last batch) reload its last step in bounds and contribute a zero W tile.
+    bf16x8_t wv[NT][S], xv[MT][S];
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      const int64_t blk = (int64_t)min(s + t, s_end - 1) * 512;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wv[nt][t] = load_w(wrow[nt] + blk);
+    }
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      const int64_t k = (int64_t)min(s + t, s_end - 1) * 32;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xv[mt][t] = load_x(xrow[mt] + k);
+    }
+    // Keep the whole batch of loads in flight before the first MFMA waits on one.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      const bool valid = s + t < s_end;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8_t a = valid ? wv[nt][t] : bf16x8_t{};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xv[mt][t], acc[nt][mt], 0, 0, 0);
+      }
+    }
+  }
+
+  // Fixed-order reduction of the waves' partial tiles.
+  if (wave < SLOTS) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[wave][nt][mt][lane] = acc[nt][mt];
+  }
+  for (int grp = 1; grp * SLOTS < nwaves; ++grp) {
+    __syncthreads();
+    if (wave / SLOTS == grp) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[wave - grp * SLOTS][nt][mt][lane] += acc[nt][mt];
+    }
+  }
+  __syncthreads();
+
+  // Epilogue: one thread per (column tile, row tile, lane) of the output.
+  const int slots = min(nwaves, SLOTS);
+  for (int idx = threadIdx.x; idx < NB * MT * kWave; idx += blockDim.x) {
+    const int j = idx / (MT * kWave);
+    const int mt = (idx / kWave) % MT;
+    const int l = idx & (kWave - 1);
+    const int m = mt * 16 + (l & 15);
+    if (m < p.M) {
+      f32x4_t v = red[0][j][mt][l], u = {};
+      for (int sl = 1; sl < slots; ++sl) v += red[sl][j][mt][l];
+      if constexpr (GATED) {
+        u = red[0][NB + j][mt][l];
+        for (int sl = 1; sl < slots; ++sl) u += red[sl][NB + j][mt][l];
+      }
+      Vec<bf16_t, 4> o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (GATED) {
+          const float gate = round_bf16(v[i]);
+          const float act = round_bf16(gate / (1.0f + expf(-gate)));
+          o.set(i, act * round_bf16(u[i]));
+        } else {
+          o.set(i, v[i]);
+        }
+      }
+      o.store(p.y + (int64_t)m * p.ldy + n0 + 16 * j + 4 * (l >> 4));
+    }
+  }
+}
+
+// W [rows, K] (row stride ldw) -> packed MFMA operand order; one thread per 16 bytes.
+__global__ void __launch_bounds__(256) linear_pack_kernel(const bf16_t* w, int64_t ldw, bf16_t* out, int64_t rows,
+                                                          int32_t K) {
+  const int64_t steps = K / 32;
+  const int64_t total = rows / 16 * steps * kWave;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & (kWave - 1));
+    const int64_t blk = i / kWave;  // tile * steps + step
+    const int64_t tile = blk / steps, step = blk - tile * steps;
+    const bf16_t* src = w + (tile * 16 + (lane & 15)) * ldw + step * 32 + 8 * (lane >> 4);
+    *reinterpret_cast<uint4*>(out + i * 8) = *reinterpret_cast<const uint4*>(src);
+  }
+}
+
+// Launch shape of one instantiation: threads per workgroup are capped so the
+// accumulators and a batch of loads fit without spilling, and the LDS partial
+// tiles (SLOTS x NT x MT x 1 KiB) stay within 64 KiB.
+template <int MT, int NB, int S, bool GATED> struct LinearShape {
+  static constexpr int kNT = GATED ? 2 * NB : NB;
+  static constexpr int kRegs = 4 * (kNT * S + MT * S + kNT * MT);
+  static constexpr int kThreads = kRegs <= 96 ? 1024 : 512;
+  static constexpr int kSlots = 64 / (kNT * MT) < 8 ? 64 / (kNT * MT) : 8;
+  static constexpr int kMaxWaves = kThreads / kWave < kLinearMaxWaves ? kThreads / kWave : kLinearMaxWaves;
+};
+
+// Steps per wave: an even share of K over at most max_waves waves, rounded up to
+// whole batches of `batch` steps.
+inline int linear_steps_per_wave(int32_t in_features, int batch, int max_waves) {
+  const int total = in_features / 32;
+  const int per_wave = (total + max_waves - 1) / max_waves;
+  return (per_wave + batch - 1) / batch * batch;
+}
+
+template <int MT, int NB, int S, bool GATED>
+int launch_linear(LinearParams prm, hipStream_t stream, int max_waves = kLinearMaxWaves) {
+  using Shape = LinearShape<MT, NB, S, GATED>;
+  if (prm.N % (16 * NB)) return CDB_ERR_SHAPE;
+  const int waves_cap = max_waves < Shape::kMaxWaves ? max_waves : Shape::kMaxWaves;
+  prm.steps_per_wave = linear_steps_per_wave(prm.K, S, waves_cap);
+  const int nwaves = (prm.K / 32 + prm.steps_per_wave - 1) / prm.steps_per_wave;
+  hipLaunchKernelGGL((linear_kernel<MT, NB, S, Shape::kSlots, GATED, Shape::kThreads>), dim3(prm.N / (16 * NB)),
+                     dim3(nwaves * kWave), 0, stream, prm);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
+}
+
+}  // namespace cdb
+
+using namespace cdb;
+
+namespace {
+
+// Tile choice, from a sweep over (NB, S, waves) at the Ouro-1.4B and Huginn-0125
+// projection shapes with cold weights: two column tiles per workgroup once N is
+// wide enough to keep more than 128 workgroups; otherwise one, so N = 2048
+// still spreads over 128 CUs. Batches of 4 steps (2 at four row tiles, for
+// registers); 8 waves per workgroup for one row tile, 4 above.
+template <int MT, int S>
+int dispatch_rows(const LinearParams& prm, bool gated, int max_waves, hipStream_t stream) {
+  const bool wide = prm.N >= 4096 && prm.N % 32 == 0;
+  if (wide) {
+    return gated ? launch_linear<MT, 2, S, true>(prm, stream, max_waves)
+                 : launch_linear<MT, 2, S, false>(prm, stream, max_waves);
+  }
+  return gated ? launch_linear<MT, 1, S, true>(prm, stream, max_waves)
+               : launch_linear<MT, 1, S, false>(prm, stream, max_waves);
+}
+
+int dispatch_linear(const LinearParams& prm, bool gated, hipStream_t stream) {
+  if (prm.M <= 16) return dispatch_rows<1, 4>(prm, gated, 8, stream);
+  if (prm.M <= 32) return dispatch_rows<2, 4>(prm, gated, 4, stream);
+  return dispatch_rows<4, 2>(prm, gated, 4, stream);
+}
+
+}  // namespace
+
+extern "C" int cdb_linear_pack_weight(const void* w, int64_t ldw, void* w_packed, int64_t rows, int32_t in_features,
+                                     int32_t dtype, hipStream_t stream) {
+  if (!w || !w_packed) return CDB_ERR_NULL;
+  if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
+  if (rows < 16 || rows % 16 || in_features < 32 || in_features % 32 || ldw < in_features || ldw % 8)
+    return CDB_ERR_SHAPE;
+  if (((uintptr_t)w & 15) || ((uintptr_t)w_packed & 15)) return CDB_ERR_SHAPE;
+  const int64_t units = rows * (int64_t)in_features / 8;
+  const int64_t blocks = (units + 255) / 256 < 65536 ? (units + 255) / 256 : 65536;
+  hipLaunchKernelGGL(linear_pack_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const bf16_t*>(w), ldw, static_cast<bf16_t*>(w_packed), rows, in_features);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
+}
+
+extern "C" int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void* y, int64_t ldy, int32_t rows,
+                          int32_t out_features, int32_t in_features, int32_t gated, int32_t dtype,
+                          hipStream_t stream) {
+  if (!x || !w_packed || !y) return CDB_ERR_NULL;
+  if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
+  if (rows < 1 || rows > kLinearMaxRows || out_features < 16 || out_features % 16 || in_features < 32 ||
+      in_features % 32)
+    return CDB_ERR_SHAPE;
+  if (ldx < in_features || ldy < out_features || ldx % 8 || ldy % 4) return CDB_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)y & 7)) return CDB_ERR_SHAPE;
+
+  LinearParams prm;
+  prm.x = static_cast<const bf16_t*>(x);
+  prm.w = static_cast<const bf16_t*>(w_packed);
+  prm.y = static_cast<bf16_t*>(y);
+  prm.ldx = ldx;
+  prm.ldy = ldy;
+  prm.M = rows;
+  prm.N = out_features;
+  prm.K = in_features;
+  prm.steps_per_wave = 0;
+  return dispatch_linear(prm, gated != 0, stream);
+}

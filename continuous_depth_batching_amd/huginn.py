@@ -246,6 +246,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             self.core_blocks = [self._pack_block(b) for b in tr["core_block"]]
             self.coda_blocks = [self._pack_block(b) for b in tr["coda"]]
             self.adapter_w = tr["adapter"].weight.contiguous()
+            self.adapter_p = ops.maybe_pack_linear_weight(self.adapter_w)
             self.adapter_b = tr["adapter"].bias.contiguous() if tr["adapter"].bias is not None else None
             self.ln_f = tr["ln_f"].weight.contiguous()
             self.embed = tr["wte"].weight
@@ -264,7 +265,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
     def _pack_block(self, b: HuginnBlock) -> dict[str, torch.Tensor | None]:
         at = b.attn
         qk = getattr(at, "qk_bias", None)
-        return dict(
+        w = dict(
             wqkv=at.Wqkv.weight.contiguous(), wo=at.proj.weight.contiguous(),
             wgu=b.mlp.fc.weight.contiguous(), wd=b.mlp.proj.weight.contiguous(),
             n1=b.norm_1.weight.contiguous(), n2=b.norm_2.weight.contiguous(),
@@ -272,6 +273,10 @@ class HuginnCDBAdapter(CDBModelAdapter):
             q_bias=None if qk is None else qk[0, 0].contiguous(),
             k_bias=None if qk is None else qk[1, 0, : self.num_kv_heads].contiguous(),
         )
+        # Operand-ordered copies for the decode-batch projection kernel.
+        for name in ("wqkv", "wo", "wgu", "wd"):
+            w["p" + name[1:]] = ops.maybe_pack_linear_weight(w[name])
+        return w
 
     @staticmethod
     def supports(model: nn.Module) -> bool:
@@ -332,12 +337,12 @@ class HuginnCDBAdapter(CDBModelAdapter):
         rows = x.shape[0]
         y_last = None
         for i, w in enumerate(blocks):
-            qkv = torch.mm(n1, w["wqkv"].t())
+            qkv = torch.ops.cdb.linear(n1, w["wqkv"], w["pqkv"], False)
             a = attend(i, w, qkv)
-            o = torch.mm(a.view(rows, self.q_width), w["wo"].t())
+            o = torch.ops.cdb.linear(a.view(rows, self.q_width), w["wo"], w["po"], False)
             x1, y = self._norm(o, w["n2"], w["n3"], residual=x)
-            act = torch.ops.cdb.silu_mul(torch.mm(y, w["wgu"].t()))
-            m = torch.mm(act, w["wd"].t())
+            act = torch.ops.cdb.linear(y, w["wgu"], w["pgu"], True)
+            m = torch.ops.cdb.linear(act, w["wd"], w["pd"], False)
             nxt = blocks[i + 1]["n1"] if i + 1 < len(blocks) else final_norm
             x, n1 = self._norm(m, w["n4"], nxt, residual=x1)
             y_last = n1
@@ -407,7 +412,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
         flat = cat.view(2 * rows, self.E)
         ops.copy_rows_raw(state, None, flat, even, rows)
         ops.copy_rows_raw(injection_src, injection_index, flat, odd, rows)
-        x = torch.mm(cat, self.adapter_w.t())
+        x = torch.ops.cdb.linear(cat, self.adapter_w, self.adapter_p, False)
         if self.adapter_b is not None:
             x = x + self.adapter_b
         return x

@@ -315,6 +315,97 @@ def _(gate_up):
     return gate_up.new_empty((*gate_up.shape[:-1], gate_up.shape[-1] // 2))
 
 
+# Rows up to which a projection runs on cdb_linear; larger batches use torch.mm (hipBLASLt).
+LINEAR_MAX_ROWS = 64
+
+
+def linear_packable(weight: torch.Tensor) -> bool:
+    return (weight.dtype == torch.bfloat16 and weight.dim() == 2 and weight.shape[0] % 16 == 0
+            and weight.shape[1] % 32 == 0)
+
+
+def pack_linear_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The operand-ordered copy of a [rows, in_features] bf16 weight that cdb_linear reads."""
+
+    _require_cuda(weight)
+    if not linear_packable(weight):
+        raise ValueError(f"cannot pack a {weight.dtype} weight of shape {tuple(weight.shape)} "
+                         "(bfloat16, rows a multiple of 16, in_features a multiple of 32)")
+    if weight.stride(1) != 1:
+        weight = weight.contiguous()
+    packed = torch.empty(weight.numel(), dtype=weight.dtype, device=weight.device)
+    _lib.check(_lib.lib().cdb_linear_pack_weight(weight.data_ptr(), weight.stride(0), packed.data_ptr(),
+                                                 weight.shape[0], weight.shape[1], _lib.CDB_DTYPE_BF16, _stream()),
+               "cdb_linear_pack_weight")
+    return packed
+
+
+def maybe_pack_linear_weight(weight: torch.Tensor) -> torch.Tensor | None:
+    """pack_linear_weight for a bf16 device weight cdb_linear can take, else None (torch.mm serves it)."""
+
+    if weight.device.type != "cuda" or not linear_packable(weight):
+        return None
+    return pack_linear_weight(weight)
+
+
+def linear_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, *, gated: bool = False) -> None:
+    """out = x @ W.T on the decode-batch projection kernel, W given packed (gated: silu(gate) * up)."""
+
+    _require_cuda(x, packed, out)
+    rows, in_features = x.shape
+    out_features = out.shape[1]
+    if x.dtype != torch.bfloat16 or packed.dtype != x.dtype or out.dtype != x.dtype:
+        raise TypeError("cdb_linear takes bfloat16 x, weight and out")
+    if packed.numel() != (2 if gated else 1) * out_features * in_features or out.shape[0] != rows:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, packed weight of {packed.numel()} elements, "
+                         f"out {tuple(out.shape)}")
+    if x.stride(1) != 1 or out.stride(1) != 1 or not packed.is_contiguous():
+        raise ValueError("x and out must have unit stride along their last dimension; the packed weight is dense")
+    _lib.check(_lib.lib().cdb_linear(x.data_ptr(), x.stride(0), packed.data_ptr(), out.data_ptr(), out.stride(0),
+                                     rows, out_features, in_features, int(gated), _lib.CDB_DTYPE_BF16, _stream()),
+               "cdb_linear")
+
+
+def linear_prefers_kernel(rows: int, out_features: int, gated: bool) -> bool:
+    """Whether cdb_linear beats torch.mm for this batch: always up to 32 rows; up to 64
+    for the gated MLP projection (its fused SiLU saves a pass) and for wide outputs
+    (N >= 4096), where the kernel keeps enough workgroups busy."""
+
+    return 1 <= rows <= 32 or (rows <= LINEAR_MAX_ROWS and (gated or out_features >= 4096))
+
+
+def _linear_fits(x: torch.Tensor, out_features: int, gated: bool) -> bool:
+    return (x.dtype == torch.bfloat16 and linear_prefers_kernel(x.shape[0], out_features, gated)
+            and x.shape[1] % 32 == 0 and out_features % 16 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0)
+
+
+@torch.library.custom_op("cdb::linear", mutates_args=(), device_types="cuda")
+def linear(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, gated: bool) -> torch.Tensor:
+    """x @ weight.T for a decode batch; gated: silu(x @ gate.T) * (x @ up.T) with weight = [gate; up].
+
+    bf16 batches that linear_prefers_kernel picks run on cdb_linear over `packed`
+    (pack_linear_weight(weight)); others, or a missing packed copy, on torch.mm
+    (followed by cdb_silu_mul when gated)."""
+
+    out_features = weight.shape[0] // 2 if gated else weight.shape[0]
+    if packed is not None and _linear_fits(x, out_features, gated):
+        out = x.new_empty((x.shape[0], out_features))
+        linear_raw(x, packed, out, gated=gated)
+        return out
+    y = torch.mm(x, weight.t())
+    if not gated:
+        return y
+    out = x.new_empty((x.shape[0], out_features))
+    silu_mul_raw(y, out)
+    return out
+
+
+@linear.register_fake
+def _(x, weight, packed, gated):
+    return x.new_empty((x.shape[0], weight.shape[0] // 2 if gated else weight.shape[0]))
+
+
 def copy_rows_raw(src: torch.Tensor, src_index: torch.Tensor | None, dst: torch.Tensor,
                   dst_index: torch.Tensor | None, rows: int) -> None:
     """dst[dst_index[i]] = src[src_index[i]] over whole rows of the first dimension (no allocation)."""

@@ -15,8 +15,10 @@ SwiGLU MLP, a final norm after every loop step, and Linear(E, 1) exit gates.
     stream, capturable as one HIP graph per bucket;
   * coda = bank gather, LM head, greedy argmax;
   * prefill = the same stack over prompt tokens with the MFMA varlen attention.
-Dense projections are torch matmuls (hipBLASLt); everything else is
-``torch.ops.cdb.*`` / the C ABI.
+Dense projections of decode batches up to 64 rows run on the weight-streaming
+``cdb::linear`` kernel (the gated form writes silu(gate) * up directly);
+larger batches (prefill) and the LM head use torch matmuls (hipBLASLt).
+Everything else is ``torch.ops.cdb.*`` / the C ABI.
 """
 
 from __future__ import annotations
@@ -212,6 +214,10 @@ class OuroCDBAdapter(CDBModelAdapter):
                     n_post=layer.post_attention_layernorm.weight.contiguous(),
                     n_post2=layer.post_attention_layernorm_2.weight.contiguous(),
                 ))
+            # Operand-ordered copies for the decode-batch projection kernel.
+            for w in self.layers:
+                for name in ("wqkv", "wo", "wgu", "wd"):
+                    w["p" + name[1:]] = ops.maybe_pack_linear_weight(w[name])
             self.final_norm = self.decoder.norm.weight.contiguous()
             self.gate_w = gate.weight.reshape(-1).contiguous()
             self.gate_b = gate.bias.reshape(-1).contiguous() if gate.bias is not None else None
@@ -279,14 +285,13 @@ class OuroCDBAdapter(CDBModelAdapter):
         num_layers = len(self.layers)
         rows = x.shape[0]
         for li, w in enumerate(self.layers):
-            qkv = torch.mm(x, w["wqkv"].t())
+            qkv = torch.ops.cdb.linear(x, w["wqkv"], w["pqkv"], False)
             attn = attend(li, qkv)
-            o = torch.mm(attn.view(rows, self.q_width), w["wo"].t())
+            o = torch.ops.cdb.linear(attn.view(rows, self.q_width), w["wo"], w["po"], False)
             residual, x = torch.ops.cdb.residual_rmsnorm(o, residual, w["n_in2"], w["n_post"], self.eps, self.eps,
                                                          ops.NORM_OURO_SANDWICH)
-            gu = torch.mm(x, w["wgu"].t())
-            act = torch.ops.cdb.silu_mul(gu)
-            m = torch.mm(act, w["wd"].t())
+            act = torch.ops.cdb.linear(x, w["wgu"], w["pgu"], True)
+            m = torch.ops.cdb.linear(act, w["wd"], w["pd"], False)
             nxt = self.layers[li + 1]["n_in"] if li + 1 < num_layers else self.final_norm
             residual, x = torch.ops.cdb.residual_rmsnorm(m, residual, w["n_post2"], nxt, self.eps, self.eps,
                                                          ops.NORM_OURO_SANDWICH)

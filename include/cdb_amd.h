@@ -174,6 +174,29 @@ int cdb_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
                           void* out, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           float scale, int32_t dtype, hipStream_t stream);
 
+/* Repack a bf16 weight w [rows, in_features] (row stride ldw) into the operand
+ * order cdb_linear reads: for each tile of 16 rows and each 32-element step of
+ * in_features, a contiguous 1 KiB block whose 16-byte unit l holds
+ * w[16 t + l % 16][32 s + 8 (l / 16) .. +8]; tiles follow each other, steps
+ * within a tile likewise. w_packed holds rows * in_features elements. rows must
+ * be a multiple of 16 and in_features of 32. Run once per weight at load time. */
+int cdb_linear_pack_weight(const void* w, int64_t ldw, void* w_packed, int64_t rows, int32_t in_features,
+                           int32_t dtype, hipStream_t stream);
+
+/* Dense projection of a decode batch: y[r, n] = R(sum_k x[r, k] * w[n, k]) for
+ * r < rows <= 64, n < out_features, bf16 only (fp32 accumulation, one rounding),
+ * with w given packed by cdb_linear_pack_weight.
+ * Replaces the nn.Linear calls of a recurrent step (ouro/modeling_ouro.py:162-168,
+ * :371-374,390-392,431; huginn/modeling_huginn.py:239-242,310-316,372).
+ * gated != 0: w holds 2*out_features rows, gate rows then up rows (the MLP's
+ * concatenated gate/up projection), and y[r, n] = R(R(silu(g)) * u) with
+ * g = R(x.w[n]) and u = R(x.w[out_features + n]) (ouro/modeling_ouro.py:168,
+ * huginn/modeling_huginn.py:315-316). Row strides ldx, ldy are in elements
+ * (multiples of 8 and 4); out_features must be a multiple of 16 and
+ * in_features a multiple of 32. */
+int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void* y, int64_t ldy, int32_t rows,
+               int32_t out_features, int32_t in_features, int32_t gated, int32_t dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,3 +79,38 @@ def test_decode_argument_errors_without_gpu() -> None:
     assert call(dtype=7) == _lib.CDB_ERR_UNSUPPORTED
     assert call(rope_cos=None) == _lib.CDB_ERR_NULL
     assert call(q_stride=100) == _lib.CDB_ERR_SHAPE
+
+
+def test_linear_argument_errors_without_gpu() -> None:
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("runs only where no device exists: the stand-in addresses must never reach a kernel")
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+
+    def call(**over):
+        args = dict(x=fake, ldx=2048, w=fake, y=fake, ldy=2048, rows=8, out_features=2048, in_features=2048, gated=0,
+                    dtype=_lib.CDB_DTYPE_BF16, stream=None)
+        args.update(over)
+        return lib.cdb_linear(*args.values())
+
+    assert call(x=None) == _lib.CDB_ERR_NULL
+    assert call(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
+    assert call(rows=0) == _lib.CDB_ERR_SHAPE
+    assert call(rows=65) == _lib.CDB_ERR_SHAPE
+    assert call(out_features=2040) == _lib.CDB_ERR_SHAPE
+    assert call(in_features=2000, ldx=2000) == _lib.CDB_ERR_SHAPE
+    assert call(ldx=2044) == _lib.CDB_ERR_SHAPE
+    assert call(ldy=2046) == _lib.CDB_ERR_SHAPE
+    assert call(w=ctypes.c_void_p(0x1008)) == _lib.CDB_ERR_SHAPE
+
+    def pack(**over):
+        args = dict(w=fake, ldw=2048, out=fake, rows=2048, in_features=2048, dtype=_lib.CDB_DTYPE_BF16, stream=None)
+        args.update(over)
+        return lib.cdb_linear_pack_weight(*args.values())
+
+    assert pack(out=None) == _lib.CDB_ERR_NULL
+    assert pack(rows=2040) == _lib.CDB_ERR_SHAPE
+    assert pack(ldw=2000) == _lib.CDB_ERR_SHAPE
+    assert pack(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED

@@ -1,0 +1,140 @@
+"""Decode-batch projection kernel (cdb_linear) against float32 matmul.
+
+The kernel sums in fp32 over all of K and rounds once, so each output must be
+the bf16 rounding of the exact product up to the last bit (a different fp32
+summation order may flip a rounding that sits within fp32 noise of a tie).
+The gated form follows torch's bf16 chain: g and u rounded, silu rounded,
+product rounded.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (in_features, out_features): Ouro-1.4B QKV, O, down; Huginn-0125 QKV, adapter; one- and two-wave K
+    (2048, 6144), (2048, 2048), (5632, 2048), (5280, 15840), (10560, 5280), (64, 32), (32, 16)]
+ROWS = [1, 5, 16, 17, 32, 33, 48, 64]
+
+
+def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 values at |x| (8 significant bits)."""
+
+    e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -126)))
+    return torch.exp2(e - 7)
+
+
+def _inputs(rows: int, k: int, n: int, seed: int):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((rows, k), generator=g, device="cuda").bfloat16()
+    w = (torch.randn((n, k), generator=g, device="cuda") * 0.02).bfloat16()
+    return x, w
+
+
+def _sum_error(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Bound on fp32 summation-order differences: 2^-22 * sum_k |x_k w_k| (it only matters
+    for results that nearly cancel)."""
+
+    return (x.float().abs() @ w.float().abs().t()) * 2.0 ** -22
+
+
+def _check_rounded(y: torch.Tensor, ref: torch.Tensor, *, max_mismatch: float, extra: torch.Tensor) -> None:
+    """y within one bf16 step of ref plus `extra`; at most max_mismatch of y differs from bf16(ref)."""
+
+    exact = ref.bfloat16()
+    diff = (y.float() - exact.float()).abs()
+    tol = _bf16_ulp(ref) * 1.0001 + extra
+    assert (diff <= tol).all(), f"max excess {(diff - tol).max().item()}"
+    assert (y != exact).float().mean().item() <= max_mismatch
+
+
+@pytest.mark.parametrize("k,n", SHAPES)
+@pytest.mark.parametrize("rows", ROWS)
+def test_linear_matches_rounded_fp32_product(rows: int, k: int, n: int) -> None:
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(rows, k, n, seed=rows * 7 + k)
+    y = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, ops.pack_linear_weight(w), y)
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().t()
+    _check_rounded(y, ref, max_mismatch=0.01, extra=_sum_error(x, w))
+
+
+@pytest.mark.parametrize("rows", [1, 16, 20, 48, 64])
+@pytest.mark.parametrize("k,f", [(2048, 5632), (5280, 17920), (64, 16)])
+def test_gated_linear_follows_bf16_silu_chain(rows: int, k: int, f: int) -> None:
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(rows, k, 2 * f, seed=rows + f)
+    y = torch.empty((rows, f), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, ops.pack_linear_weight(w), y, gated=True)
+    torch.cuda.synchronize()
+    gu = (x.float() @ w.float().t()).bfloat16().float()
+    g, u = gu[:, :f], gu[:, f:]
+    act = (g * torch.sigmoid(g)).bfloat16().float()
+    ref = act * u
+    # A g or u rounding that flips (see above) moves g or u by one bf16 step, which
+    # propagates through silu(g) * u (|silu'| < 1.1); all else matches the chain exactly.
+    err = _sum_error(x, w)
+    dg = _bf16_ulp(g) + err[:, :f]
+    du = _bf16_ulp(u) + err[:, f:]
+    _check_rounded(y, ref, max_mismatch=0.02, extra=1.1 * u.abs() * dg + (act.abs() + dg) * du)
+    # And the unfused path (torch.mm + cdb_silu_mul) agrees to the same bar.
+    unfused = torch.empty_like(y)
+    ops.silu_mul_raw(torch.mm(x, w.t()), unfused)
+    torch.cuda.synchronize()
+    assert ((y.float() - unfused.float()).abs() <= 2 * _bf16_ulp(ref) + 1e-6).float().mean().item() >= 0.98
+
+
+def test_linear_strided_operands_and_determinism() -> None:
+    from continuous_depth_batching_amd import ops
+
+    rows, k, n = 24, 2048, 2048
+    x_big, w = _inputs(rows, 3 * k, n, seed=5)
+    x = x_big[:, k:2 * k]                   # row stride 3K
+    w_big = torch.zeros((n, k + 64), dtype=torch.bfloat16, device="cuda")
+    w_big[:, :k] = w[:, :k]
+    w_view = w_big[:, :k]                   # row stride K + 64
+    y_big = torch.full((rows, n + 16), 7.0, dtype=torch.bfloat16, device="cuda")
+    y = y_big[:, :n]
+    packed = ops.pack_linear_weight(w_view)
+    assert torch.equal(packed, ops.pack_linear_weight(w[:, :k].contiguous()))  # the pack honours the row stride
+    ops.linear_raw(x, packed, y)
+    again = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x.contiguous(), packed, again)
+    torch.cuda.synchronize()
+    assert torch.equal(y, again)            # strides change no arithmetic; repeat runs are bit-identical
+    assert (y_big[:, n:] == 7.0).all()      # columns past out_features untouched
+    wk = w[:, :k]
+    _check_rounded(y, x.float() @ wk.float().t(), max_mismatch=0.01, extra=_sum_error(x, wk))
+
+
+def test_linear_op_dispatch_matches_torch_above_the_row_limit() -> None:
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(ops.LINEAR_MAX_ROWS + 8, 2048, 2048, seed=9)
+    packed = ops.pack_linear_weight(w)
+    y = torch.ops.cdb.linear(x, w, packed, False)
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.mm(x, w.t()))
+    assert torch.equal(torch.ops.cdb.linear(x[:8], w, None, False), torch.mm(x[:8], w.t()))
+    small = torch.ops.cdb.linear(x[:8], w, packed, False)
+    torch.cuda.synchronize()
+    _check_rounded(small, x[:8].float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x[:8], w))
+
+
+@pytest.mark.parametrize("n,k", [(32, 64), (2048, 2048), (48, 5632)])
+def test_pack_layout_is_the_mfma_operand_order(n: int, k: int) -> None:
+    """Unit l of the 1 KiB block (tile t, step s) holds w[16 t + l % 16][32 s + 8 (l // 16) .. +8]."""
+
+    from continuous_depth_batching_amd import ops
+
+    w = torch.randn((n, k), device="cuda").bfloat16()
+    packed = ops.pack_linear_weight(w)
+    torch.cuda.synchronize()
+    expected = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
+    assert torch.equal(packed, expected)

@@ -183,6 +183,50 @@ def time_prefill_attention(prompt_lens, iters: int) -> dict:
             "sequences": int(case.lens.size), "max_len": int(case.lens.max())}
 
 
+def time_decode_projections(rows: int = 16, layers: int = 24, reps: int = 4) -> dict:
+    """The Ouro-1.4B layer's four projections on cdb_linear at `rows` rows, each over
+    `layers` distinct weights (one per layer, so every launch streams cold weights as
+    in a layer stack), timed from a captured graph so launch gaps are the GPU's own."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+
+    shapes = {"qkv": (2048, 6144, False), "o": (2048, 2048, False), "gate_up_silu": (2048, 5632, True),
+              "down": (5632, 2048, False)}
+    result = {}
+    for name, (k, n, gated) in shapes.items():
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(3)
+        weights = [ops.pack_linear_weight((torch.randn(((2 if gated else 1) * n, k), generator=gen, device="cuda")
+                                           * 0.02).bfloat16()) for _ in range(layers)]
+        x = torch.randn((rows, k), generator=gen, device="cuda").bfloat16()
+        y = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+        stream = torch.cuda.Stream()
+        with torch.cuda.stream(stream):
+            for w in weights[:2]:
+                ops.linear_raw(x, w, y, gated=gated)
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for w in weights:
+                    ops.linear_raw(x, w, y, gated=gated)
+            graph.replay()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            end.record(stream)
+        end.synchronize()
+        us = start.elapsed_time(end) / (reps * layers) * 1e3
+        nbytes = weights[0].numel() * 2 + rows * (k + n) * 2
+        result[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+        del weights
+    torch.cuda.empty_cache()
+    return {"rows": rows, "shapes": result}
+
+
 def first_prefill_batch(prompts, token_budget: int = 8192) -> list[int]:
     """Prompt lengths of the workload's first full prefill batch (prompts admitted in order while
     they fit the engine's token budget)."""
@@ -282,6 +326,7 @@ def main() -> int:
         del case
         torch.cuda.empty_cache()
 
+    projections = time_decode_projections()
     prefill = time_prefill_attention(first_prefill_batch(prompts), iters=max(3, args.attention_iters // 4))
     prefill["shape"] = (f"{prefill['sequences']} fresh prompts, {prefill['tokens']} tokens (max {prefill['max_len']}), "
                         "16 heads x 128, causal")
@@ -290,7 +335,7 @@ def main() -> int:
     if args.workload == "decode-attention":
         print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
                           "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro,
-                          "prefill_attention": prefill,
+                          "prefill_attention": prefill, "decode_projections": projections,
                           "copy_calibration": copy_calibration()}))
         return 0
 
@@ -336,6 +381,7 @@ def main() -> int:
         "roofline": roofline,
         "decode_attention_microbench": micro,
         "prefill_attention": prefill,
+        "decode_projections": projections,
         "engine": {"generated_tokens": generated, "recurrent_batches": stats.recurrent_batches,
                    "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),
                    "coda_batches": stats.coda_batches, "prefill_batches": stats.prefill_batches,

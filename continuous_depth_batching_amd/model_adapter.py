@@ -51,7 +51,7 @@ class RecurrentLaunch:
     slot_offset: torch.Tensor    # [rows] int32 cache layer of core layer 0 at the row's step (prelude + slot * C)
     cache: PagedKVCache
     workspace: torch.Tensor      # decode-attention workspace (split header + fp32 partials)
-    split_pages: int             # pages per KV split; 0 = chosen by the kernel
+    split_pages: int             # pages per KV split; 0 = chosen by the kernel, -m = chosen with at least m
     gate: GateLaunch
 
 

@@ -256,7 +256,7 @@ class ModelRunner:
                                                             dtype=np.int32, count=len(items)), torch.int32)
             launch.cache = self.cache
             launch.workspace = self.workspace
-            launch.split_pages = ops.ADAPTIVE_SPLIT
+            launch.split_pages = ops.decode_split_pages(len(items))
         return launch
 
     # -- recurrent stage -------------------------------------------------------------------------------------
@@ -289,7 +289,7 @@ class ModelRunner:
             rows=rows, bank=self.bank, bank_slots=dev_i64, positions=dev_i32[self.META_POSITIONS],
             table_rows=dev_i32[self.META_TABLE_ROWS], slot_offset=dev_i32[self.META_LAYER_OFFSET],
             cache=self.cache, workspace=self.workspace,
-            split_pages=ops.ADAPTIVE_SPLIT, gate=gate)
+            split_pages=ops.decode_split_pages(rows), gate=gate)
         b = _RecurrentBucket(rows=rows, host_i64=host_i64, host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32,
                              launch=launch)
         b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]

@@ -80,7 +80,7 @@ def check(case, split_pages: int, use_table_row: bool = False, **kw) -> None:
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("split_pages", [0, 1, 4, 64])
+@pytest.mark.parametrize("split_pages", [0, 1, 4, 64, -4, -1])  # -m: adaptive with at least m pages
 def test_ouro_shape_mixed_depth(dtype: str, split_pages: int) -> None:
     case = make_case(seed=10, num_rows=24, num_heads=16, num_kv_heads=16, head_dim=128, max_context=700,
                      rope_style=1, dtype=dtype, padding_rows=3)

@@ -169,6 +169,170 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Tiled variant for batches of tens to hundreds of rows. Re-reading x from L2 in
+// every workgroup (the kernel above) grows with M; here a workgroup owns an
+// output tile of 32*MTW rows x 32*NTW columns with the full K, so x is staged
+// once per workgroup and shared:
+//   * 4 waves in a 2 x 2 grid; wave (wm, wn) owns MTW row tiles x NTW column
+//     tiles (gated: NTW gate and NTW matching up tiles), so no partial sums
+//     cross waves;
+//   * x chunks of 32*SC columns go through LDS, double-buffered, in the same
+//     operand order as packed W (16-byte unit (r, g) of block (row tile, step)
+//     holds x[16 t + r][32 s + 8 g ..]), so every operand read is one
+//     conflict-free ds_read_b128 of a contiguous 1 KiB block;
+//   * W blocks come straight from the packed weight into registers, one chunk
+//     ahead of the MFMAs that use them; a W block is loaded by the two waves
+//     of its column (the second read hits the CU's L1);
+//   * workgroups that share a column tile (different row tiles) are placed on
+//     the same XCD (dispatch order round-robins workgroups over the 8 XCDs), so
+//     the weight tile crosses HBM once and is re-read from that XCD's L2.
+// ---------------------------------------------------------------------------
+template <int MTW, int NTW, int SC, bool GATED>
+__global__ void __launch_bounds__(256) linear_tile_kernel(LinearParams p) {
+  constexpr int NT = GATED ? 2 * NTW : NTW;
+  constexpr int MT_WG = 2 * MTW;         // row tiles per workgroup
+  constexpr int ROWS = 16 * MT_WG;       // x rows per workgroup
+  constexpr int KC = 32 * SC;            // contraction elements per chunk
+  constexpr int UNITS = ROWS * KC / 8;   // 16-byte units of one x chunk
+  static_assert(UNITS % 256 == 0, "x chunk must split evenly over the workgroup");
+  constexpr int UPT = UNITS / 256;
+  __shared__ bf16x8_t xs[2][MT_WG][SC][kWave];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  const int n_tiles = p.N / (32 * NTW);
+  const int m_tiles = (p.M + ROWS - 1) / ROWS;
+  const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
+  const int mi = q % m_tiles;
+  const int ni = (q / m_tiles) * 8 + xcd;
+  if (ni >= n_tiles) return;  // padding workgroup of the XCD-major order: exits before any barrier
+  const int m0 = mi * ROWS;
+  const int n0 = ni * 32 * NTW;
+
+  const int total = p.K / 32;
+  const int nchunks = (total + SC - 1) / SC;
+  const bf16_t* wp[NT];
+#pragma unroll
+  for (int j = 0; j < NTW; ++j) {
+    wp[j] = p.w + ((int64_t)(n0 / 16 + wn * NTW + j) * total) * 512 + 8 * lane;
+    if constexpr (GATED) wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wn * NTW + j) * total) * 512 + 8 * lane;
+  }
+  // x staging: unit u -> (row, 8-element group k8) of the chunk; row clamped to M - 1.
+  const bf16_t* xsrc[UPT];
+  int xk[UPT], xdst[UPT];
+#pragma unroll
+  for (int i = 0; i < UPT; ++i) {
+    const int u = tid + 256 * i;
+    const int row = u / (KC / 8), k8 = u % (KC / 8);
+    xsrc[i] = p.x + (int64_t)min(m0 + row, p.M - 1) * p.ldx;
+    xk[i] = 8 * k8;
+    xdst[i] = (((row >> 4) * SC + (k8 >> 2)) * kWave) + (row & 15) + 16 * (k8 & 3);
+  }
+
+  auto load_x_chunk = [&](int c, bf16x8_t (&xr)[UPT]) {
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) {
+      // Columns past K (last chunk only) reload in-bounds data; those steps are zeroed below.
+      xr[i] = load_x(xsrc[i] + min(c * KC + xk[i], p.K - 8));
+    }
+  };
+  auto load_w_chunk = [&](int c, bf16x8_t (&wr)[NT][SC]) {
+#pragma unroll
+    for (int t = 0; t < SC; ++t) {
+      const int64_t blk = (int64_t)min(c * SC + t, total - 1) * 512;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wr[nt][t] = load_w(wp[nt] + blk);
+    }
+  };
+  auto store_x_chunk = [&](int buf, const bf16x8_t (&xr)[UPT]) {
+    bf16x8_t* base = &xs[buf][0][0][0];
+#pragma unroll
+    for (int i = 0; i < UPT; ++i) base[xdst[i]] = xr[i];
+  };
+
+  f32x4_t acc[NT][MTW];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8_t xr[UPT];
+  bf16x8_t wcur[NT][SC], wnext[NT][SC];
+  load_x_chunk(0, xr);
+  load_w_chunk(0, wcur);
+  store_x_chunk(0, xr);
+  __syncthreads();
+
+  for (int c = 0; c < nchunks; ++c) {
+    const int cur = c & 1;
+    const bool more = c + 1 < nchunks;
+    if (more) {
+      load_x_chunk(c + 1, xr);
+      load_w_chunk(c + 1, wnext);
+    }
+#pragma unroll
+    for (int t = 0; t < SC; ++t) {
+      const bool valid = c * SC + t < total;
+      bf16x8_t b[MTW];
+#pragma unroll
+      for (int mt = 0; mt < MTW; ++mt) b[mt] = valid ? xs[cur][wm * MTW + mt][t][lane] : bf16x8_t{};
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const bf16x8_t a = valid ? wcur[nt][t] : bf16x8_t{};
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+      }
+    }
+    if (more) {
+      store_x_chunk(cur ^ 1, xr);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int t = 0; t < SC; ++t) wcur[nt][t] = wnext[nt][t];
+    }
+    __syncthreads();
+  }
+
+  // Lane (r, g) holds C[n = 16 tile + 4 g + i][m = 16 row_tile + r].
+#pragma unroll
+  for (int mt = 0; mt < MTW; ++mt) {
+    const int m = m0 + 16 * (wm * MTW + mt) + (lane & 15);
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      Vec<bf16_t, 4> o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (GATED) {
+          const float gate = round_bf16(acc[j][mt][i]);
+          const float act = round_bf16(gate / (1.0f + expf(-gate)));
+          o.set(i, act * round_bf16(acc[NTW + j][mt][i]));
+        } else {
+          o.set(i, acc[j][mt][i]);
+        }
+      }
+      o.store(p.y + (int64_t)m * p.ldy + n0 + 16 * (wn * NTW + j) + 4 * (lane >> 4));
+    }
+  }
+}
+
+template <int MTW, int NTW, int SC, bool GATED>
+int launch_linear_tile(LinearParams prm, hipStream_t stream) {
+  constexpr int kRows = 32 * MTW;
+  if (prm.N % (32 * NTW)) return CDB_ERR_SHAPE;
+  const int n_tiles = prm.N / (32 * NTW);
+  const int m_tiles = (prm.M + kRows - 1) / kRows;
+  const int groups = (n_tiles + 7) / 8;
+  hipLaunchKernelGGL((linear_tile_kernel<MTW, NTW, SC, GATED>), dim3(groups * 8 * m_tiles), dim3(256), 0, stream,
+                     prm);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
+}
+
 // W [rows, K] (row stride ldw) -> packed MFMA operand order; one thread per 16 bytes.
 __global__ void __launch_bounds__(256) linear_pack_kernel(const bf16_t* w, int64_t ldw, bf16_t* out, int64_t rows,
                                                           int32_t K) {

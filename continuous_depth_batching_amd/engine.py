@@ -363,11 +363,12 @@ class ContinuousDepthBatchingEngine:
             return
         stats = self.last_stats
         stats.mixed_recurrent_batches += 1
-        depth_counts = Counter(item.recurrent_step for item in items)
+        launch_steps = [item.recurrent_step for item in items]
+        depth_counts = Counter(launch_steps)
         stats.max_mixed_depths_per_batch = max(stats.max_mixed_depths_per_batch, len(depth_counts))
         for step, count in depth_counts.items():
             stats.mixed_recurrent_depth_histogram[step] += count
-        launch_steps = [item.recurrent_step for item in items]
+            stats.recurrent_step_histogram[step] += count
         flags = self.runner.compute_recurrent_batch(items)
         stats.recurrent_batches += 1
         stats.recurrent_steps += len(items)
@@ -377,7 +378,6 @@ class ContinuousDepthBatchingEngine:
         exits: list[bool] = []
         for idx, item in enumerate(items):
             step = item.recurrent_step
-            stats.recurrent_step_histogram[step] += 1
             if delayed:
                 previous = self._pending_flags.pop(id(item), None)
                 should_exit = step == max_steps - 1 or (

@@ -466,11 +466,11 @@ class HuginnCDBAdapter(CDBModelAdapter):
 
     def coda(self, launch: StageLaunch) -> torch.Tensor:
         n = launch.n
-        state = torch.ops.cdb.gather_rows(launch.bank, launch.slots[:n])
+        state = ops.gather_rows_raw(launch.bank, launch.slots[:n])
         layout = self.kv_cache_layout()
         attend = self._decode_attend(launch, lambda i: (None, layout.coda_layer_index(i)))
         hidden = self._coda_hidden(state, attend)
-        return torch.ops.cdb.argmax(torch.mm(hidden, self.lm_head_w.t()))
+        return ops.argmax_rows(torch.mm(hidden, self.lm_head_w.t()))
 
     def prefill(self, launch: PrefillLaunch) -> torch.Tensor:
         tokens = launch.tokens.numel()

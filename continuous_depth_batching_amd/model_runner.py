@@ -97,12 +97,18 @@ class PendingFlags:
 
     host: torch.Tensor
     event: Any | None
+    _values: list[int] | None = None
 
     def get(self, index: int) -> bool:
-        if self.event is not None:
-            self.event.synchronize()
-            self.event = None
-        return bool(self.host[index])
+        values = self._values
+        if values is None:
+            # Wait once, then read the pinned bytes as a Python list: per-row tensor
+            # indexing costs microseconds each on the routing path.
+            if self.event is not None:
+                self.event.synchronize()
+                self.event = None
+            values = self._values = self.host.tolist()
+        return bool(values[index])
 
 
 @dataclass
@@ -120,7 +126,9 @@ class PrefillMetadata:
 @dataclass
 class _RecurrentBucket:
     rows: int
-    host_i64: torch.Tensor
+    host_meta: torch.Tensor  # pinned int32 [7 * rows]: the int64 bank slots, then the int32 rows
+    dev_meta: torch.Tensor
+    host_i64: torch.Tensor   # views of host_meta / dev_meta
     host_i32: torch.Tensor
     dev_i64: torch.Tensor
     dev_i32: torch.Tensor
@@ -221,22 +229,30 @@ class ModelRunner:
         if any(item.token_id != TMP_TOKEN_ID for item in items[:num_device]):
             raise AssertionError("device_groups must cover a prefix of items")
         slots = self.allocate_hidden_slots(n)
+        # One upload: [bank slots (n) | tokens (n) | each device group's row indices]. The first
+        # num_device token entries are placeholders, overwritten on the device by gathers from the
+        # staged results' device tokens; the rest are the host token ids.
+        upload = np.empty(2 * n + num_device, dtype=np.int64)
+        upload[:n] = slots
+        upload[n:n + num_device] = 0
+        upload[n + num_device:2 * n] = [item.token_id for item in items[num_device:]]
+        offset = 2 * n
+        for _, rows in device_groups:
+            upload[offset:offset + len(rows)] = rows
+            offset += len(rows)
         with torch.cuda.stream(self.stream):
-            tokens = torch.empty((n, 1), dtype=torch.int64, device=self.device)
-            offset = 0
+            dev = self._to_device(upload, torch.int64)
+            slot_dev, tokens = dev[:n], dev[n:2 * n]
+            offset, index = 0, 2 * n
             for result, rows in device_groups:
                 if result.device_tokens is None:
                     raise RuntimeError("Cannot gather prelude tokens from a staged result that carries none")
-                idx = self._to_device(np.asarray(rows, dtype=np.int64), torch.int64)
-                src = result.device_tokens.view(-1, 1)
-                ops.copy_rows_raw(src, idx, tokens[offset:offset + len(rows)], None, len(rows))
-                offset += len(rows)
-            if n > num_device:
-                host_ids = np.fromiter((item.token_id for item in items[num_device:]), dtype=np.int64,
-                                       count=n - num_device)
-                tokens[num_device:].copy_(self._to_device(host_ids.reshape(-1, 1), torch.int64))
-            slot_dev = self._to_device(np.asarray(slots, dtype=np.int64), torch.int64)
-            self.adapter.prelude(self._stage_launch(items, slot_dev, tokens=tokens.view(-1)))
+                k = len(rows)
+                ops.copy_rows_raw(result.device_tokens.view(-1, 1), dev[index:index + k],
+                                  tokens[offset:offset + k].view(-1, 1), None, k)
+                offset += k
+                index += k
+            self.adapter.prelude(self._stage_launch(items, slot_dev, tokens=tokens))
             self.gate_state.reset(slot_dev, n)
         for item, slot in zip(items, slots):
             item.hidden_slot = slot
@@ -264,10 +280,13 @@ class ModelRunner:
         b = self._buckets.get(rows)
         if b is not None:
             return b
-        host_i64 = self._pinned((rows,), torch.int64)
-        host_i32 = self._pinned((5, rows), torch.int32)
-        dev_i64 = torch.full((rows,), -1, dtype=torch.int64, device=self.device)
-        dev_i32 = torch.zeros((5, rows), dtype=torch.int32, device=self.device)
+        # One pinned buffer and one device buffer per bucket, so a launch uploads its
+        # metadata with a single copy.
+        host_meta = self._pinned((7 * rows,), torch.int32)
+        dev_meta = torch.zeros((7 * rows,), dtype=torch.int32, device=self.device)
+        host_i64, host_i32 = host_meta[:2 * rows].view(torch.int64), host_meta[2 * rows:].view(5, rows)
+        dev_i64, dev_i32 = dev_meta[:2 * rows].view(torch.int64), dev_meta[2 * rows:].view(5, rows)
+        dev_i64.fill_(-1)
         dev_i32[self.META_POSITIONS].fill_(-1)
         dev_i32[self.META_SYNTHETIC].fill_(-1)
         policy = self.exit_policy
@@ -290,8 +309,8 @@ class ModelRunner:
             table_rows=dev_i32[self.META_TABLE_ROWS], slot_offset=dev_i32[self.META_LAYER_OFFSET],
             cache=self.cache, workspace=self.workspace,
             split_pages=ops.decode_split_pages(rows), gate=gate)
-        b = _RecurrentBucket(rows=rows, host_i64=host_i64, host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32,
-                             launch=launch)
+        b = _RecurrentBucket(rows=rows, host_meta=host_meta, dev_meta=dev_meta, host_i64=host_i64,
+                             host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32, launch=launch)
         b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]
         b.flag_events = [None] * self.FLAG_TURNS
         self._buckets[rows] = b
@@ -314,8 +333,7 @@ class ModelRunner:
             b.flag_events[turn].synchronize()
         with torch.cuda.stream(self.stream):
             self.cache.flush_table_updates()
-            b.dev_i64.copy_(b.host_i64, non_blocking=True)
-            b.dev_i32.copy_(b.host_i32, non_blocking=True)
+            b.dev_meta.copy_(b.host_meta, non_blocking=True)
             if b.staged is None:
                 b.staged = torch.cuda.Event()
             b.staged.record()

@@ -24,16 +24,18 @@ _DTYPE_CODES = {torch.float32: _lib.CDB_DTYPE_F32, torch.bfloat16: _lib.CDB_DTYP
 ADAPTIVE_SPLIT = 0
 MIN_SPLIT_PAGES = 8
 MAX_SPLIT_PAGES = 32
-# Launches of at most this many rows have too few 8-page items to cover the
-# chip and take 4-page splits (a single 1200-token row: 17.4 -> 14.3 us).
-SMALL_LAUNCH_ROWS = 4
-SMALL_LAUNCH_MIN_SPLIT_PAGES = 4
 
 
 def decode_split_pages(rows: int) -> int:
-    """The split_pages argument a decode launch of `rows` rows passes (adaptive)."""
+    """The split_pages argument a decode launch of `rows` rows passes.
 
-    return -SMALL_LAUNCH_MIN_SPLIT_PAGES if rows <= SMALL_LAUNCH_ROWS else ADAPTIVE_SPLIT
+    Always the adaptive default. A smaller lower bound for small launches was
+    measured (one 1193-token row: 17.4 -> 14.3 us) but makes a row's split -- and
+    so its rounding -- depend on the size of the launch it lands in; with one
+    bound for every launch, rows whose context stays under the bound compute
+    identically in any batch composition."""
+
+    return ADAPTIVE_SPLIT
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -43,8 +45,14 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"CDB kernels support float32 and bfloat16, got {dtype}") from exc
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_getDevice"):
+    def _stream() -> int:
+        # The raw handle of torch's current stream without building a Stream object
+        # (that costs ~10 us per call on the per-tick host path).
+        return torch._C._cuda_getCurrentRawStream(torch._C._cuda_getDevice())
+else:  # pragma: no cover - older torch builds
+    def _stream() -> int:
+        return torch.cuda.current_stream().cuda_stream
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -437,13 +445,19 @@ def copy_rows_raw(src: torch.Tensor, src_index: torch.Tensor | None, dst: torch.
                "cdb_copy_rows")
 
 
-@torch.library.custom_op("cdb::gather_rows", mutates_args=(), device_types="cuda")
-def gather_rows(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
-    """src[index] along dim 0; negative indices give zero rows."""
+def gather_rows_raw(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """src[index] along dim 0 (negative indices give zero rows), without op dispatch."""
 
     out = src.new_empty((index.numel(), *src.shape[1:]))
     copy_rows_raw(src, index.contiguous(), out, None, index.numel())
     return out
+
+
+@torch.library.custom_op("cdb::gather_rows", mutates_args=(), device_types="cuda")
+def gather_rows(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """src[index] along dim 0; negative indices give zero rows."""
+
+    return gather_rows_raw(src, index)
 
 
 @gather_rows.register_fake
@@ -468,14 +482,20 @@ def argmax_raw(logits: torch.Tensor, out: torch.Tensor) -> None:
                                      _stream()), "cdb_argmax")
 
 
-@torch.library.custom_op("cdb::argmax", mutates_args=(), device_types="cuda")
-def argmax(logits: torch.Tensor) -> torch.Tensor:
-    """Greedy token per row of a [rows, vocab] logits matrix (first index of the max)."""
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy token per row (first index of the max), without op dispatch."""
 
     l2 = logits.reshape(-1, logits.shape[-1])
     out = torch.empty((l2.shape[0],), dtype=torch.int64, device=logits.device)
     argmax_raw(l2, out)
     return out.view(logits.shape[:-1])
+
+
+@torch.library.custom_op("cdb::argmax", mutates_args=(), device_types="cuda")
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy token per row of a [rows, vocab] logits matrix (first index of the max)."""
+
+    return argmax_rows(logits)
 
 
 @argmax.register_fake

@@ -352,10 +352,11 @@ class OuroCDBAdapter(CDBModelAdapter):
 
     def coda_from_hidden(self, hidden: torch.Tensor) -> torch.Tensor:
         logits = torch.mm(hidden, self.lm_head_w.t())
-        return torch.ops.cdb.argmax(logits)
+        return ops.argmax_rows(logits)
 
     def coda(self, launch: StageLaunch) -> torch.Tensor:
-        hidden = torch.ops.cdb.gather_rows(launch.bank, launch.slots[:launch.n])
+        # Eager, once per coda tick: direct calls rather than op dispatch.
+        hidden = ops.gather_rows_raw(launch.bank, launch.slots[:launch.n])
         return self.coda_from_hidden(hidden)
 
 

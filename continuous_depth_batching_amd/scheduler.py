@@ -125,9 +125,13 @@ class CDBScheduler:
         self.in_flight_request_ids.discard(request_id)
 
     def _mark_request_in_flight(self, request_id: str) -> None:
-        self.in_flight_request_ids.add(request_id)
-        self.max_in_flight_requests = max(self.max_in_flight_requests, len(self.in_flight_request_ids))
-        self.max_live_requests = max(self.max_live_requests, len(self.active_requests) + len(self.waiting_requests))
+        in_flight = self.in_flight_request_ids
+        in_flight.add(request_id)
+        if len(in_flight) > self.max_in_flight_requests:
+            self.max_in_flight_requests = len(in_flight)
+        live = len(self.active_requests) + len(self.waiting_requests)
+        if live > self.max_live_requests:
+            self.max_live_requests = live
 
     # -- admission (scheduler_base.py:171-201, 416-531) --------------------------------------------------------
     def has_prefill_headroom(self) -> bool:
@@ -229,10 +233,21 @@ class CDBScheduler:
         self.max_depth_queue_size = max(self.max_depth_queue_size, len(self.ready_queue))
 
     def enqueue_depth_front(self, items: list[DepthWorkItem]) -> None:
-        """Return items to the queue head preserving their order."""
+        """Return items to the queue head preserving their order (enqueue_depth(front=True)
+        applied from the last item to the first, in one pass)."""
 
+        queue = self.ready_queue
+        limit = self.max_recurrent_steps
         for item in reversed(items):
-            self.enqueue_depth(item, front=True)
+            step = item.recurrent_step
+            if not 0 <= step < limit:
+                raise ValueError(f"recurrent_step must be in [0, {limit}), got {step}")
+            self._mark_request_in_flight(item.state.request_id)
+            if step == 0 and queue:
+                self.refill_events += 1
+            queue.appendleft(item)
+        if len(queue) > self.max_depth_queue_size:
+            self.max_depth_queue_size = len(queue)
 
     def enqueue_coda(self, item: DepthWorkItem) -> None:
         self._mark_request_in_flight(item.state.request_id)

@@ -209,10 +209,11 @@ class ContinuousDepthBatchingEngine:
         for s in states:
             self.scheduler.add_waiting_request(s)
         try:
-            if self.cdb_config.refill:
-                self._run_scheduler_loop()
-            else:
-                self._run_no_refill_loop()
+            with self.runner.stream_scope():
+                if self.cdb_config.refill:
+                    self._run_scheduler_loop()
+                else:
+                    self._run_no_refill_loop()
         finally:
             self.runner.synchronize()
             self.scheduler.free_unfinished_requests()

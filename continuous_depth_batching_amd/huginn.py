@@ -251,6 +251,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             self.ln_f = tr["ln_f"].weight.contiguous()
             self.embed = tr["wte"].weight
             self.lm_head_w = model.lm_head.weight
+            self.lm_head_p = ops.maybe_pack_linear_weight(self.lm_head_w)
         positions = max_positions or int(getattr(cfg, "block_size", 4096))
         self.max_positions = positions
         self.rope_cos, self.rope_sin = huginn_rope_tables(self.head_dim, float(cfg.rope_base), positions,
@@ -337,12 +338,12 @@ class HuginnCDBAdapter(CDBModelAdapter):
         rows = x.shape[0]
         y_last = None
         for i, w in enumerate(blocks):
-            qkv = torch.ops.cdb.linear(n1, w["wqkv"], w["pqkv"], False)
+            qkv = ops.linear_auto(n1, w["wqkv"], w["pqkv"], False)
             a = attend(i, w, qkv)
-            o = torch.ops.cdb.linear(a.view(rows, self.q_width), w["wo"], w["po"], False)
+            o = ops.linear_auto(a.view(rows, self.q_width), w["wo"], w["po"], False)
             x1, y = self._norm(o, w["n2"], w["n3"], residual=x)
-            act = torch.ops.cdb.linear(y, w["wgu"], w["pgu"], True)
-            m = torch.ops.cdb.linear(act, w["wd"], w["pd"], False)
+            act = ops.linear_auto(y, w["wgu"], w["pgu"], True)
+            m = ops.linear_auto(act, w["wd"], w["pd"], False)
             nxt = blocks[i + 1]["n1"] if i + 1 < len(blocks) else final_norm
             x, n1 = self._norm(m, w["n4"], nxt, residual=x1)
             y_last = n1
@@ -412,7 +413,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
         flat = cat.view(2 * rows, self.E)
         ops.copy_rows_raw(state, None, flat, even, rows)
         ops.copy_rows_raw(injection_src, injection_index, flat, odd, rows)
-        x = torch.ops.cdb.linear(cat, self.adapter_w, self.adapter_p, False)
+        x = ops.linear_auto(cat, self.adapter_w, self.adapter_p, False)
         if self.adapter_b is not None:
             x = x + self.adapter_b
         return x
@@ -470,7 +471,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
         layout = self.kv_cache_layout()
         attend = self._decode_attend(launch, lambda i: (None, layout.coda_layer_index(i)))
         hidden = self._coda_hidden(state, attend)
-        return ops.argmax_rows(torch.mm(hidden, self.lm_head_w.t()))
+        return ops.argmax_rows(ops.linear_auto(hidden, self.lm_head_w, self.lm_head_p, False))
 
     def prefill(self, launch: PrefillLaunch) -> torch.Tensor:
         tokens = launch.tokens.numel()
@@ -489,7 +490,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             state, _ = self._blocks(self.core_blocks, h, n1, attend, None)
         hidden = self._coda_hidden(state, self._prefill_attend(launch, layout.coda_layer_index))
         last = torch.ops.cdb.gather_rows(hidden, launch.last_index)
-        return torch.ops.cdb.argmax(torch.mm(last, self.lm_head_w.t()))
+        return ops.argmax_rows(ops.linear_auto(last, self.lm_head_w, self.lm_head_p, False))
 
 
 __all__ = ["HuginnConfig", "HuginnForCausalLM", "HuginnCDBAdapter", "build_huginn", "init_huginn_weights",

@@ -19,7 +19,7 @@ follow from the MI355X design:
 from __future__ import annotations
 
 import gc
-from contextlib import contextmanager
+from contextlib import contextmanager, nullcontext
 from dataclasses import dataclass, field
 from typing import Any, Iterator, Sequence
 
@@ -157,6 +157,8 @@ class ModelRunner:
         self.use_graphs = bool(engine_config.use_cuda_graph)
         self.layout = cache.layout
         self.stream = torch.cuda.Stream(device=self.device)
+        self._stream_handle = self.stream.cuda_stream
+        self._device_index = self.stream.device_index
         self.bank_capacity = 4 * self.max_num_seqs + 64
         self.bank = torch.zeros((self.bank_capacity, model_adapter.hidden_width), dtype=self.dtype,
                                 device=self.device)
@@ -208,6 +210,19 @@ class ModelRunner:
                 item.hidden_slot = None
 
     # -- helpers --------------------------------------------------------------------------------------------------
+    def stream_scope(self):
+        """Make the compute stream current for a whole generate_batch, so the per-call
+        scopes below find it already set."""
+
+        return torch.cuda.stream(self.stream)
+
+    def _on_stream(self):
+        """Scope of one runner call on the compute stream: free when it is already current."""
+
+        if torch._C._cuda_getCurrentRawStream(self._device_index) == self._stream_handle:
+            return nullcontext()
+        return torch.cuda.stream(self.stream)
+
     def _pinned(self, shape: tuple[int, ...] | int, dtype: torch.dtype) -> torch.Tensor:
         return torch.empty(shape, dtype=dtype, pin_memory=True)
 
@@ -240,7 +255,7 @@ class ModelRunner:
         for _, rows in device_groups:
             upload[offset:offset + len(rows)] = rows
             offset += len(rows)
-        with torch.cuda.stream(self.stream):
+        with self._on_stream():
             dev = self._to_device(upload, torch.int64)
             slot_dev, tokens = dev[:n], dev[n:2 * n]
             offset, index = 0, 2 * n
@@ -331,7 +346,7 @@ class ModelRunner:
         b.turn = (turn + 1) % self.FLAG_TURNS
         if b.flag_events[turn] is not None:
             b.flag_events[turn].synchronize()
-        with torch.cuda.stream(self.stream):
+        with self._on_stream():
             self.cache.flush_table_updates()
             b.dev_meta.copy_(b.host_meta, non_blocking=True)
             if b.staged is None:
@@ -397,7 +412,7 @@ class ModelRunner:
             i32[self.META_LAYER_OFFSET] = self.layout.core_base
             i32[self.META_STEPS] = 0
             i32[self.META_SYNTHETIC] = -1
-            with torch.cuda.stream(self.stream):
+            with self._on_stream():
                 b.dev_i64.copy_(b.host_i64, non_blocking=True)
                 b.dev_i32.copy_(b.host_i32, non_blocking=True)
                 if b.staged is None:
@@ -433,7 +448,7 @@ class ModelRunner:
         for item in items:
             item.state.tokens_in_flight += 1
         n = len(items)
-        with torch.cuda.stream(self.stream):
+        with self._on_stream():
             slots = self._to_device(np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n),
                                     torch.int64)
             tokens = self.adapter.coda(self._stage_launch(items, slots))
@@ -460,7 +475,7 @@ class ModelRunner:
         meta = self.prefill_metadata(requests)
         last_index = meta.last_index
         tile_seq, tile_q0 = ops.prefill_tiles(meta.lens)
-        with torch.cuda.stream(self.stream):
+        with self._on_stream():
             cache.flush_table_updates()
             launch = PrefillLaunch(
                 tokens=self._to_device(meta.tokens, torch.int64),
@@ -534,7 +549,7 @@ class ModelRunner:
         if not rows:
             return
         slots = [self.layout.slot_for_step(s) for s in exit_steps]
-        with torch.cuda.stream(self.stream):
+        with self._on_stream():
             ops.exit_kv_copy_raw(self.cache.view, self._to_device(np.asarray(rows, dtype=np.int64), torch.int64),
                                  self._to_device(np.asarray(slots, dtype=np.int32), torch.int32), len(rows),
                                  layer_base=self.layout.core_base, core_layers=self.layout.num_core_layers,

@@ -387,11 +387,12 @@ def linear_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, *, gate
 
 
 def linear_prefers_kernel(rows: int, out_features: int, gated: bool) -> bool:
-    """Whether cdb_linear beats torch.mm for this batch: always up to 32 rows; up to 64
-    for the gated MLP projection (its fused SiLU saves a pass) and for wide outputs
-    (N >= 4096), where the kernel keeps enough workgroups busy."""
+    """Whether cdb_linear beats torch.mm for this batch (measured on cold weights): always
+    up to 32 rows; up to 64 for the gated MLP projection (its fused SiLU saves a pass) and
+    for outputs of 4096 to 16384 columns, wide enough to keep the kernel's workgroups
+    busy. The LM head (49152 columns) at 33-64 rows is faster on hipBLASLt."""
 
-    return 1 <= rows <= 32 or (rows <= LINEAR_MAX_ROWS and (gated or out_features >= 4096))
+    return 1 <= rows <= 32 or (rows <= LINEAR_MAX_ROWS and (gated or 4096 <= out_features <= 16384))
 
 
 def _linear_fits(x: torch.Tensor, out_features: int, gated: bool) -> bool:
@@ -400,13 +401,8 @@ def _linear_fits(x: torch.Tensor, out_features: int, gated: bool) -> bool:
             and x.data_ptr() % 16 == 0)
 
 
-@torch.library.custom_op("cdb::linear", mutates_args=(), device_types="cuda")
-def linear(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, gated: bool) -> torch.Tensor:
-    """x @ weight.T for a decode batch; gated: silu(x @ gate.T) * (x @ up.T) with weight = [gate; up].
-
-    bf16 batches that linear_prefers_kernel picks run on cdb_linear over `packed`
-    (pack_linear_weight(weight)); others, or a missing packed copy, on torch.mm
-    (followed by cdb_silu_mul when gated)."""
+def linear_auto(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, gated: bool) -> torch.Tensor:
+    """The body of cdb::linear, callable without op dispatch (eager per-tick paths)."""
 
     out_features = weight.shape[0] // 2 if gated else weight.shape[0]
     if packed is not None and _linear_fits(x, out_features, gated):
@@ -419,6 +415,17 @@ def linear(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, g
     out = x.new_empty((x.shape[0], out_features))
     silu_mul_raw(y, out)
     return out
+
+
+@torch.library.custom_op("cdb::linear", mutates_args=(), device_types="cuda")
+def linear(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, gated: bool) -> torch.Tensor:
+    """x @ weight.T for a decode batch; gated: silu(x @ gate.T) * (x @ up.T) with weight = [gate; up].
+
+    bf16 batches that linear_prefers_kernel picks run on cdb_linear over `packed`
+    (pack_linear_weight(weight)); others, or a missing packed copy, on torch.mm
+    (followed by cdb_silu_mul when gated)."""
+
+    return linear_auto(x, weight, packed, gated)
 
 
 @linear.register_fake

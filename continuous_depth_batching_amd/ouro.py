@@ -17,7 +17,8 @@ SwiGLU MLP, a final norm after every loop step, and Linear(E, 1) exit gates.
   * prefill = the same stack over prompt tokens with the MFMA varlen attention.
 Dense projections of decode batches up to 64 rows run on the weight-streaming
 ``cdb::linear`` kernel (the gated form writes silu(gate) * up directly);
-larger batches (prefill) and the LM head use torch matmuls (hipBLASLt).
+larger batches (prefill) use torch matmuls (hipBLASLt); the LM head takes the
+same split (its packed copy serves coda batches of up to 32 rows).
 Everything else is ``torch.ops.cdb.*`` / the C ABI.
 """
 
@@ -223,6 +224,7 @@ class OuroCDBAdapter(CDBModelAdapter):
             self.gate_b = gate.bias.reshape(-1).contiguous() if gate.bias is not None else None
             self.embed = self.decoder.embed_tokens.weight
             self.lm_head_w = model.lm_head.weight
+            self.lm_head_p = ops.maybe_pack_linear_weight(self.lm_head_w)
         positions = max_positions or int(getattr(cfg, "max_position_embeddings", 65536))
         self.rope_cos, self.rope_sin = rope_tables(self.head_dim, float(cfg.rope_theta), positions, self._dtype,
                                                    self._device)
@@ -285,13 +287,13 @@ class OuroCDBAdapter(CDBModelAdapter):
         num_layers = len(self.layers)
         rows = x.shape[0]
         for li, w in enumerate(self.layers):
-            qkv = torch.ops.cdb.linear(x, w["wqkv"], w["pqkv"], False)
+            qkv = ops.linear_auto(x, w["wqkv"], w["pqkv"], False)
             attn = attend(li, qkv)
-            o = torch.ops.cdb.linear(attn.view(rows, self.q_width), w["wo"], w["po"], False)
+            o = ops.linear_auto(attn.view(rows, self.q_width), w["wo"], w["po"], False)
             residual, x = torch.ops.cdb.residual_rmsnorm(o, residual, w["n_in2"], w["n_post"], self.eps, self.eps,
                                                          ops.NORM_OURO_SANDWICH)
-            act = torch.ops.cdb.linear(x, w["wgu"], w["pgu"], True)
-            m = torch.ops.cdb.linear(act, w["wd"], w["pd"], False)
+            act = ops.linear_auto(x, w["wgu"], w["pgu"], True)
+            m = ops.linear_auto(act, w["wd"], w["pd"], False)
             nxt = self.layers[li + 1]["n_in"] if li + 1 < num_layers else self.final_norm
             residual, x = torch.ops.cdb.residual_rmsnorm(m, residual, w["n_post2"], nxt, self.eps, self.eps,
                                                          ops.NORM_OURO_SANDWICH)
@@ -351,7 +353,7 @@ class OuroCDBAdapter(CDBModelAdapter):
         return self.coda_from_hidden(last)
 
     def coda_from_hidden(self, hidden: torch.Tensor) -> torch.Tensor:
-        logits = torch.mm(hidden, self.lm_head_w.t())
+        logits = ops.linear_auto(hidden, self.lm_head_w, self.lm_head_p, False)
         return ops.argmax_rows(logits)
 
     def coda(self, launch: StageLaunch) -> torch.Tensor:

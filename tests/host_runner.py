@@ -16,6 +16,8 @@ delayed horizon the engine itself applies a launch's decisions one launch late.
 
 from __future__ import annotations
 
+from contextlib import nullcontext
+
 import numpy as np
 import torch
 
@@ -208,6 +210,9 @@ class HostLoopRunner(ModelRunner):
 
     def synchronize(self) -> None:
         pass
+
+    def stream_scope(self):
+        return nullcontext()
 
 
 def make_engine(**cfg_over):

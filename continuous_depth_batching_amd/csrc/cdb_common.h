@@ -100,6 +100,14 @@ template <typename T, int N> struct Vec {
   }
 };
 
+// Workgroup barrier for LDS hand-offs that leaves global loads in flight:
+// waits only for this wave's LDS operations (lgkmcnt) and then meets the other
+// waves. __syncthreads() is a release/acquire fence plus barrier, which also
+// waits for every outstanding global load (vmcnt 0) and so drains any
+// prefetch pipeline at each barrier. The "memory" clobber keeps the compiler
+// from moving LDS accesses across it.
+CDB_DEVICE void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // DPP row rotate by n within each 16-lane row. Used only for all-lane row reductions,
 // which give every lane of the row the same result whichever way the rotation runs.
 template <int kCtrl> CDB_DEVICE float dpp_f32(float v) {

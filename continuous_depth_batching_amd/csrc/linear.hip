@@ -47,6 +47,7 @@ struct LinearParams {
 };
 
 constexpr int kLinearMaxRows = 64;
+constexpr int kLinearWideMaxRows = 256;
 constexpr int kLinearMaxWaves = 16;
 
 CDB_DEVICE bf16x8_t load_w(const bf16_t* p) {
@@ -170,58 +171,54 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Tiled variant for batches of tens to hundreds of rows. Re-reading x from L2 in
-// every workgroup (the kernel above) grows with M; here a workgroup owns an
-// output tile of 32*MTW rows x 32*NTW columns with the full K, so x is staged
-// once per workgroup and shared:
-//   * 4 waves in a 2 x 2 grid; wave (wm, wn) owns MTW row tiles x NTW column
-//     tiles (gated: NTW gate and NTW matching up tiles), so no partial sums
-//     cross waves;
-//   * x chunks of 32*SC columns go through LDS, double-buffered, in the same
-//     operand order as packed W (16-byte unit (r, g) of block (row tile, step)
-//     holds x[16 t + r][32 s + 8 g ..]), so every operand read is one
-//     conflict-free ds_read_b128 of a contiguous 1 KiB block;
-//   * W blocks come straight from the packed weight into registers, one chunk
-//     ahead of the MFMAs that use them; a W block is loaded by the two waves
-//     of its column (the second read hits the CU's L1);
-//   * workgroups that share a column tile (different row tiles) are placed on
-//     the same XCD (dispatch order round-robins workgroups over the 8 XCDs), so
-//     the weight tile crosses HBM once and is re-read from that XCD's L2.
+// Wide-tile variant for batches of 33 to 256 rows. A workgroup owns 16*MT rows
+// x 4*16*NTW columns with the full K; wave w owns column tiles w*NTW .. and
+// every row tile, so each weight byte is loaded by exactly one wave:
+//   * weight blocks stream from the packed layout into a ring of STAGES chunks
+//     of registers (SC steps each), STAGES chunks ahead of the MFMAs that use
+//     them, so the HBM latency is covered without waiting per chunk;
+//   * x chunks go through LDS, double-buffered, in operand order (16-byte
+//     unit (r, g) of block (row tile, step) holds x[16 t + r][32 s + 8 g ..]);
+//   * workgroups of one column range (different row ranges) sit on one XCD,
+//     so the weights cross HBM once.
 // ---------------------------------------------------------------------------
-template <int MTW, int NTW, int SC, bool GATED>
-__global__ void __launch_bounds__(256) linear_tile_kernel(LinearParams p) {
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS>
+__global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   constexpr int NT = GATED ? 2 * NTW : NTW;
-  constexpr int MT_WG = 2 * MTW;         // row tiles per workgroup
-  constexpr int ROWS = 16 * MT_WG;       // x rows per workgroup
-  constexpr int KC = 32 * SC;            // contraction elements per chunk
-  constexpr int UNITS = ROWS * KC / 8;   // 16-byte units of one x chunk
+  constexpr int ROWS = 16 * MT;
+  constexpr int KC = 32 * SC;
+  constexpr int UNITS = ROWS * KC / 8;
   static_assert(UNITS % 256 == 0, "x chunk must split evenly over the workgroup");
   constexpr int UPT = UNITS / 256;
-  __shared__ bf16x8_t xs[2][MT_WG][SC][kWave];
+  __shared__ bf16x8_t xs[2][MT][SC][kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-  const int wm = wave >> 1, wn = wave & 1;
 
-  const int n_tiles = p.N / (32 * NTW);
+  const int n_tiles = p.N / (64 * NTW);
   const int m_tiles = (p.M + ROWS - 1) / ROWS;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int mi = q % m_tiles;
   const int ni = (q / m_tiles) * 8 + xcd;
   if (ni >= n_tiles) return;  // padding workgroup of the XCD-major order: exits before any barrier
   const int m0 = mi * ROWS;
-  const int n0 = ni * 32 * NTW;
+  const int n0 = ni * 64 * NTW;
 
-  const int total = p.K / 32;
-  const int nchunks = (total + SC - 1) / SC;
+  // K is a compile-time constant so the chunk loop unrolls completely: the
+  // compiler's wait-count pass then sees every load of the register rings in
+  // order and waits exactly for the chunk it is about to use.
+  constexpr int total = KSTEPS;
+  constexpr int nchunks = (total + SC - 1) / SC;
   const bf16_t* wp[NT];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    wp[j] = p.w + ((int64_t)(n0 / 16 + wn * NTW + j) * total) * 512 + 8 * lane;
-    if constexpr (GATED) wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wn * NTW + j) * total) * 512 + 8 * lane;
+    wp[j] = p.w + ((int64_t)(n0 / 16 + wave * NTW + j) * total) * 512 + 8 * lane;
+    if constexpr (GATED) wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wave * NTW + j) * total) * 512 + 8 * lane;
   }
-  // x staging: unit u -> (row, 8-element group k8) of the chunk; row clamped to M - 1.
+  // x staging: thread unit u reads 16 bytes of one row (units of a row are
+  // consecutive, so the global reads coalesce) and stores them to that row's
+  // operand slot in LDS.
   const bf16_t* xsrc[UPT];
   int xk[UPT], xdst[UPT];
 #pragma unroll
@@ -232,76 +229,75 @@ __global__ void __launch_bounds__(256) linear_tile_kernel(LinearParams p) {
     xk[i] = 8 * k8;
     xdst[i] = (((row >> 4) * SC + (k8 >> 2)) * kWave) + (row & 15) + 16 * (k8 & 3);
   }
-
-  auto load_x_chunk = [&](int c, bf16x8_t (&xr)[UPT]) {
+  auto load_x = [&](int c, bf16x8_t (&xr)[UPT]) {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) {
-      // Columns past K (last chunk only) reload in-bounds data; those steps are zeroed below.
-      xr[i] = load_x(xsrc[i] + min(c * KC + xk[i], p.K - 8));
-    }
+    for (int i = 0; i < UPT; ++i) xr[i] = cdb::load_x(xsrc[i] + min(c * KC + xk[i], p.K - 8));
   };
-  auto load_w_chunk = [&](int c, bf16x8_t (&wr)[NT][SC]) {
-#pragma unroll
-    for (int t = 0; t < SC; ++t) {
-      const int64_t blk = (int64_t)min(c * SC + t, total - 1) * 512;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wr[nt][t] = load_w(wp[nt] + blk);
-    }
-  };
-  auto store_x_chunk = [&](int buf, const bf16x8_t (&xr)[UPT]) {
+  auto store_x = [&](int buf, const bf16x8_t (&xr)[UPT]) {
     bf16x8_t* base = &xs[buf][0][0][0];
 #pragma unroll
     for (int i = 0; i < UPT; ++i) base[xdst[i]] = xr[i];
   };
+  auto load_w = [&](int c, bf16x8_t (&wr)[NT][SC]) {
+#pragma unroll
+    for (int t = 0; t < SC; ++t) {
+      const int64_t blk = (int64_t)min(c * SC + t, total - 1) * 512;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wr[nt][t] = cdb::load_w(wp[nt] + blk);
+    }
+  };
 
-  f32x4_t acc[NT][MTW];
+  f32x4_t acc[NT][MT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-    for (int mt = 0; mt < MTW; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  bf16x8_t xr[UPT];
-  bf16x8_t wcur[NT][SC], wnext[NT][SC];
-  load_x_chunk(0, xr);
-  load_w_chunk(0, wcur);
-  store_x_chunk(0, xr);
+  // Chunk j's weights live in ring[j % STAGES] and its x in xring[j % STAGES] from STAGES
+  // chunks before it is used; x moves to LDS one chunk ahead of its MFMAs.
+  bf16x8_t ring[STAGES][NT][SC];
+  bf16x8_t xring[STAGES][UPT];
+#pragma unroll
+  for (int st = 0; st < STAGES; ++st) {  // chunks past the end reload in-bounds data
+    load_w(st, ring[st]);
+    load_x(st, xring[st]);
+  }
+  store_x(0, xring[0]);
   __syncthreads();
 
-  for (int c = 0; c < nchunks; ++c) {
-    const int cur = c & 1;
-    const bool more = c + 1 < nchunks;
-    if (more) {
-      load_x_chunk(c + 1, xr);
-      load_w_chunk(c + 1, wnext);
-    }
 #pragma unroll
-    for (int t = 0; t < SC; ++t) {
-      const bool valid = c * SC + t < total;
-      bf16x8_t b[MTW];
+  for (int c0 = 0; c0 < nchunks; c0 += STAGES) {
 #pragma unroll
-      for (int mt = 0; mt < MTW; ++mt) b[mt] = valid ? xs[cur][wm * MTW + mt][t][lane] : bf16x8_t{};
+    for (int st = 0; st < STAGES; ++st) {
+      const int c = c0 + st;
+      if (c < nchunks) {
+        const int cur = c & 1;
+        const bool more = c + 1 < nchunks;
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        const bf16x8_t a = valid ? wcur[nt][t] : bf16x8_t{};
+        for (int t = 0; t < SC; ++t) {
+          const bool valid = c * SC + t < total;
+          bf16x8_t b[MT];
 #pragma unroll
-        for (int mt = 0; mt < MTW; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+          for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[cur][mt][t][lane] : bf16x8_t{};
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const bf16x8_t a = valid ? ring[st][nt][t] : bf16x8_t{};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+              acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+          }
+        }
+        if (c + STAGES < nchunks) load_w(c + STAGES, ring[st]);
+        if (more) store_x(cur ^ 1, xring[(st + 1) % STAGES]);
+        if (c + STAGES < nchunks) load_x(c + STAGES, xring[st]);
+        lds_barrier();
       }
     }
-    if (more) {
-      store_x_chunk(cur ^ 1, xr);
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-        for (int t = 0; t < SC; ++t) wcur[nt][t] = wnext[nt][t];
-    }
-    __syncthreads();
   }
 
-  // Lane (r, g) holds C[n = 16 tile + 4 g + i][m = 16 row_tile + r].
 #pragma unroll
-  for (int mt = 0; mt < MTW; ++mt) {
-    const int m = m0 + 16 * (wm * MTW + mt) + (lane & 15);
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = m0 + 16 * mt + (lane & 15);
     if (m >= p.M) continue;
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
@@ -316,20 +312,18 @@ __global__ void __launch_bounds__(256) linear_tile_kernel(LinearParams p) {
           o.set(i, acc[j][mt][i]);
         }
       }
-      o.store(p.y + (int64_t)m * p.ldy + n0 + 16 * (wn * NTW + j) + 4 * (lane >> 4));
+      o.store(p.y + (int64_t)m * p.ldy + n0 + 16 * (wave * NTW + j) + 4 * (lane >> 4));
     }
   }
 }
 
-template <int MTW, int NTW, int SC, bool GATED>
-int launch_linear_tile(LinearParams prm, hipStream_t stream) {
-  constexpr int kRows = 32 * MTW;
-  if (prm.N % (32 * NTW)) return CDB_ERR_SHAPE;
-  const int n_tiles = prm.N / (32 * NTW);
-  const int m_tiles = (prm.M + kRows - 1) / kRows;
-  const int groups = (n_tiles + 7) / 8;
-  hipLaunchKernelGGL((linear_tile_kernel<MTW, NTW, SC, GATED>), dim3(groups * 8 * m_tiles), dim3(256), 0, stream,
-                     prm);
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS>
+int launch_linear_wide(LinearParams prm, hipStream_t stream) {
+  if (prm.N % (64 * NTW) || prm.K != 32 * KSTEPS) return CDB_ERR_SHAPE;
+  const int n_tiles = prm.N / (64 * NTW);
+  const int m_tiles = (prm.M + 16 * MT - 1) / (16 * MT);
+  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS>),
+                     dim3((n_tiles + 7) / 8 * 8 * m_tiles), dim3(256), 0, stream, prm);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 
@@ -400,7 +394,28 @@ int dispatch_rows(const LinearParams& prm, bool gated, int max_waves, hipStream_
                : launch_linear<MT, 1, S, false>(prm, stream, max_waves);
 }
 
+// Wide-tile path: batches of 33 to 256 rows over 2048-wide inputs with outputs
+// of 4096+ columns (the Ouro-1.4B QKV and gate/up projections). Tiles from a
+// sweep over (row tiles, column tiles, chunk, stages) with cold weights.
+bool wide_path(const LinearParams& prm) {
+  return prm.M > 32 && prm.M <= kLinearWideMaxRows && prm.K == 2048 && prm.N >= 4096 && prm.N % 128 == 0;
+}
+
+int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
+  if (prm.M <= 64) {
+    return gated ? launch_linear_wide<2, 1, 4, 4, true, 64>(prm, stream)
+                 : launch_linear_wide<2, 1, 4, 4, false, 64>(prm, stream);
+  }
+  if (prm.M <= 128) {
+    return gated ? launch_linear_wide<4, 1, 4, 2, true, 64>(prm, stream)
+                 : launch_linear_wide<2, 2, 4, 4, false, 64>(prm, stream);
+  }
+  return gated ? launch_linear_wide<4, 2, 2, 4, true, 64>(prm, stream)
+               : launch_linear_wide<4, 2, 4, 2, false, 64>(prm, stream);
+}
+
 int dispatch_linear(const LinearParams& prm, bool gated, hipStream_t stream) {
+  if (wide_path(prm)) return dispatch_wide(prm, gated, stream);
   if (prm.M <= 16) return dispatch_rows<1, 4>(prm, gated, 8, stream);
   if (prm.M <= 32) return dispatch_rows<2, 4>(prm, gated, 4, stream);
   return dispatch_rows<4, 2>(prm, gated, 4, stream);
@@ -427,7 +442,7 @@ extern "C" int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void
                           hipStream_t stream) {
   if (!x || !w_packed || !y) return CDB_ERR_NULL;
   if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
-  if (rows < 1 || rows > kLinearMaxRows || out_features < 16 || out_features % 16 || in_features < 32 ||
+  if (rows < 1 || rows > kLinearWideMaxRows || out_features < 16 || out_features % 16 || in_features < 32 ||
       in_features % 32)
     return CDB_ERR_SHAPE;
   if (ldx < in_features || ldy < out_features || ldx % 8 || ldy % 4) return CDB_ERR_SHAPE;
@@ -443,5 +458,6 @@ extern "C" int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void
   prm.N = out_features;
   prm.K = in_features;
   prm.steps_per_wave = 0;
+  if (rows > kLinearMaxRows && !wide_path(prm)) return CDB_ERR_SHAPE;
   return dispatch_linear(prm, gated != 0, stream);
 }

@@ -386,17 +386,27 @@ def linear_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, *, gate
                "cdb_linear")
 
 
-def linear_prefers_kernel(rows: int, out_features: int, gated: bool) -> bool:
+# Batches up to this many rows run the wide-tile kernel when the shape qualifies.
+LINEAR_WIDE_MAX_ROWS = 256
+
+
+def linear_prefers_kernel(rows: int, out_features: int, gated: bool, in_features: int = 0) -> bool:
     """Whether cdb_linear beats torch.mm for this batch (measured on cold weights): always
     up to 32 rows; up to 64 for the gated MLP projection (its fused SiLU saves a pass) and
-    for outputs of 4096 to 16384 columns, wide enough to keep the kernel's workgroups
-    busy. The LM head (49152 columns) at 33-64 rows is faster on hipBLASLt."""
+    for outputs of 4096 to 16384 columns; and up to 256 rows on the wide-tile kernel for
+    2048-wide inputs with such outputs (a multiple of 128 columns). The LM head (49152
+    columns) above 32 rows is faster on hipBLASLt, as are O and down projections."""
 
-    return 1 <= rows <= 32 or (rows <= LINEAR_MAX_ROWS and (gated or 4096 <= out_features <= 16384))
+    if 1 <= rows <= 32:
+        return True
+    mid = 4096 <= out_features <= 16384
+    if rows <= LINEAR_MAX_ROWS and (gated or mid):
+        return True
+    return rows <= LINEAR_WIDE_MAX_ROWS and mid and out_features % 128 == 0 and in_features == 2048
 
 
 def _linear_fits(x: torch.Tensor, out_features: int, gated: bool) -> bool:
-    return (x.dtype == torch.bfloat16 and linear_prefers_kernel(x.shape[0], out_features, gated)
+    return (x.dtype == torch.bfloat16 and linear_prefers_kernel(x.shape[0], out_features, gated, x.shape[1])
             and x.shape[1] % 32 == 0 and out_features % 16 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0
             and x.data_ptr() % 16 == 0)
 

@@ -184,8 +184,10 @@ int cdb_linear_pack_weight(const void* w, int64_t ldw, void* w_packed, int64_t r
                            int32_t dtype, hipStream_t stream);
 
 /* Dense projection of a decode batch: y[r, n] = R(sum_k x[r, k] * w[n, k]) for
- * r < rows <= 64, n < out_features, bf16 only (fp32 accumulation, one rounding),
- * with w given packed by cdb_linear_pack_weight.
+ * r < rows, n < out_features, bf16 only (fp32 accumulation, one rounding),
+ * with w given packed by cdb_linear_pack_weight. rows <= 64, or up to 256 when
+ * in_features is 2048 and out_features a multiple of 128 of at least 4096 (a
+ * wide-tile kernel); other shapes above 64 rows return CDB_ERR_SHAPE.
  * Replaces the nn.Linear calls of a recurrent step (ouro/modeling_ouro.py:162-168,
  * :371-374,390-392,431; huginn/modeling_huginn.py:239-242,310-316,372).
  * gated != 0: w holds 2*out_features rows, gate rows then up rows (the MLP's

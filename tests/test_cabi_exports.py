@@ -98,7 +98,9 @@ def test_linear_argument_errors_without_gpu() -> None:
     assert call(x=None) == _lib.CDB_ERR_NULL
     assert call(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
     assert call(rows=0) == _lib.CDB_ERR_SHAPE
-    assert call(rows=65) == _lib.CDB_ERR_SHAPE
+    assert call(rows=65) == _lib.CDB_ERR_SHAPE                      # 2048 -> 2048 has no wide-tile path
+    assert call(rows=257, out_features=6144, ldy=6144) == _lib.CDB_ERR_SHAPE
+    assert call(rows=100, in_features=4096, ldx=4096) == _lib.CDB_ERR_SHAPE
     assert call(out_features=2040) == _lib.CDB_ERR_SHAPE
     assert call(in_features=2000, ldx=2000) == _lib.CDB_ERR_SHAPE
     assert call(ldx=2044) == _lib.CDB_ERR_SHAPE

@@ -64,10 +64,26 @@ def test_linear_matches_rounded_fp32_product(rows: int, k: int, n: int) -> None:
     _check_rounded(y, ref, max_mismatch=0.01, extra=_sum_error(x, w))
 
 
-@pytest.mark.parametrize("rows", [1, 16, 20, 48, 64])
+@pytest.mark.parametrize("rows,k,n", [(r, 2048, n) for r in (33, 65, 96, 128, 129, 200, 256) for n in (6144, 4096)])
+def test_wide_tile_path_matches_rounded_fp32_product(rows: int, k: int, n: int) -> None:
+    """Batches above 32 rows with 2048-wide inputs and 4096+ outputs take the wide-tile kernel."""
+
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(rows, k, n, seed=rows + n)
+    y = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, ops.pack_linear_weight(w), y)
+    torch.cuda.synchronize()
+    _check_rounded(y, x.float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x, w))
+
+
+@pytest.mark.parametrize("rows", [1, 16, 20, 48, 64, 100, 256])
 @pytest.mark.parametrize("k,f", [(2048, 5632), (5280, 17920), (64, 16)])
 def test_gated_linear_follows_bf16_silu_chain(rows: int, k: int, f: int) -> None:
     from continuous_depth_batching_amd import ops
+
+    if rows > ops.LINEAR_MAX_ROWS and not (k == 2048 and f % 128 == 0 and f >= 4096):
+        pytest.skip("above 64 rows only the wide-tile shapes run on cdb_linear")
 
     x, w = _inputs(rows, k, 2 * f, seed=rows + f)
     y = torch.empty((rows, f), dtype=torch.bfloat16, device="cuda")

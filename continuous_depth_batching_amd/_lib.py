@@ -49,6 +49,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "cdb_rmsnorm_fused": (
         c_int32, [_P, _P, _P, _P, _P, _P, c_int64, c_int32, c_int32, c_float, c_float, c_int32, _P]),
+    "cdb_rmsnorm_fused_parts": (
+        c_int32,
+        [
+            _P, c_int32, _P, _P, _P, _P, _P,  # x_parts, splits, residual, w_a, w_b, out_h, out_y
+            c_int64, c_int32, c_int32, c_float, c_float, c_int32, _P,  # rows, width, mode, eps_a, eps_b, dtype, stream
+        ],
+    ),
     "cdb_silu_mul": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
     "cdb_copy_rows": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P]),
     "cdb_argmax": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
@@ -90,6 +97,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [
             _P, c_int64, _P, _P, c_int64,  # x, ldx, w_packed, y, ldy
             c_int32, c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, gated, dtype, stream
+        ],
+    ),
+    "cdb_linear_parts_splits": (c_int32, [c_int64, c_int32, c_int32, c_int32]),
+    "cdb_linear_parts": (
+        c_int32,
+        [
+            _P, c_int64, _P, _P, c_int64,  # x, ldx, w_packed, parts, parts_elems
+            c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, dtype, stream
         ],
     ),
 }

@@ -41,6 +41,7 @@ struct LinearParams {
   const bf16_t* x;  // [M, K], row stride ldx elements
   const bf16_t* w;  // packed [N, K] (gated: [2N, K], gate rows then up rows)
   bf16_t* y;        // [M, N], row stride ldy
+  float* parts;     // split-K form: fp32 partial sums [splits, M, N] instead of y
   int64_t ldx, ldy;
   int32_t M, N, K;
   int32_t steps_per_wave;  // 32-element contraction steps per wave
@@ -182,7 +183,10 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
 //   * workgroups of one column range (different row ranges) sit on one XCD,
 //     so the weights cross HBM once.
 // ---------------------------------------------------------------------------
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS>
+// KSPLIT > 1: K is cut into KSPLIT ranges of KSTEPS steps; each workgroup covers
+// one range and stores fp32 partial sums to p.parts[split], for a consumer that
+// adds them in split order and rounds once (the residual RMSNorm).
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1>
 __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   constexpr int NT = GATED ? 2 * NTW : NTW;
   constexpr int ROWS = 16 * MT;
@@ -196,25 +200,30 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   const int lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
+  // Workgroups that share a (column range, K split) -- all its row ranges -- sit on one XCD.
   const int n_tiles = p.N / (64 * NTW);
   const int m_tiles = (p.M + ROWS - 1) / ROWS;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int mi = q % m_tiles;
-  const int ni = (q / m_tiles) * 8 + xcd;
-  if (ni >= n_tiles) return;  // padding workgroup of the XCD-major order: exits before any barrier
+  const int pair = (q / m_tiles) * 8 + xcd;  // column range + K split
+  if (pair >= n_tiles * KSPLIT) return;     // padding workgroup of the XCD-major order: exits before any barrier
+  const int ni = pair % n_tiles, ks = pair / n_tiles;
   const int m0 = mi * ROWS;
   const int n0 = ni * 64 * NTW;
 
-  // K is a compile-time constant so the chunk loop unrolls completely: the
-  // compiler's wait-count pass then sees every load of the register rings in
+  // The K range is a compile-time constant so the chunk loop unrolls completely:
+  // the compiler's wait-count pass then sees every load of the register rings in
   // order and waits exactly for the chunk it is about to use.
   constexpr int total = KSTEPS;
   constexpr int nchunks = (total + SC - 1) / SC;
+  const int tile_steps = p.K / 32;  // steps of one packed weight tile
+  const int k_first = ks * KSTEPS;
   const bf16_t* wp[NT];
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    wp[j] = p.w + ((int64_t)(n0 / 16 + wave * NTW + j) * total) * 512 + 8 * lane;
-    if constexpr (GATED) wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wave * NTW + j) * total) * 512 + 8 * lane;
+    wp[j] = p.w + ((int64_t)(n0 / 16 + wave * NTW + j) * tile_steps + k_first) * 512 + 8 * lane;
+    if constexpr (GATED)
+      wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wave * NTW + j) * tile_steps + k_first) * 512 + 8 * lane;
   }
   // x staging: thread unit u reads 16 bytes of one row (units of a row are
   // consecutive, so the global reads coalesce) and stores them to that row's
@@ -225,13 +234,13 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   for (int i = 0; i < UPT; ++i) {
     const int u = tid + 256 * i;
     const int row = u / (KC / 8), k8 = u % (KC / 8);
-    xsrc[i] = p.x + (int64_t)min(m0 + row, p.M - 1) * p.ldx;
+    xsrc[i] = p.x + (int64_t)min(m0 + row, p.M - 1) * p.ldx + (int64_t)k_first * 32;
     xk[i] = 8 * k8;
     xdst[i] = (((row >> 4) * SC + (k8 >> 2)) * kWave) + (row & 15) + 16 * (k8 & 3);
   }
   auto load_x = [&](int c, bf16x8_t (&xr)[UPT]) {
 #pragma unroll
-    for (int i = 0; i < UPT; ++i) xr[i] = cdb::load_x(xsrc[i] + min(c * KC + xk[i], p.K - 8));
+    for (int i = 0; i < UPT; ++i) xr[i] = cdb::load_x(xsrc[i] + min(c * KC + xk[i], total * 32 - 8));
   };
   auto store_x = [&](int buf, const bf16x8_t (&xr)[UPT]) {
     bf16x8_t* base = &xs[buf][0][0][0];
@@ -299,6 +308,14 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   for (int mt = 0; mt < MT; ++mt) {
     const int m = m0 + 16 * mt + (lane & 15);
     if (m >= p.M) continue;
+    if constexpr (KSPLIT > 1) {
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        float* dst = p.parts + ((int64_t)ks * p.M + m) * p.N + n0 + 16 * (wave * NTW + j) + 4 * (lane >> 4);
+        *reinterpret_cast<f32x4_t*>(dst) = acc[j][mt];
+      }
+      continue;
+    }
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
       Vec<bf16_t, 4> o;
@@ -317,13 +334,14 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   }
 }
 
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS>
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1>
 int launch_linear_wide(LinearParams prm, hipStream_t stream) {
-  if (prm.N % (64 * NTW) || prm.K != 32 * KSTEPS) return CDB_ERR_SHAPE;
+  if (prm.N % (64 * NTW) || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
   const int n_tiles = prm.N / (64 * NTW);
   const int m_tiles = (prm.M + 16 * MT - 1) / (16 * MT);
-  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS>),
-                     dim3((n_tiles + 7) / 8 * 8 * m_tiles), dim3(256), 0, stream, prm);
+  const int pairs = n_tiles * KSPLIT;
+  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT>),
+                     dim3((pairs + 7) / 8 * 8 * m_tiles), dim3(256), 0, stream, prm);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 
@@ -414,6 +432,31 @@ int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
                : launch_linear_wide<4, 2, 4, 2, false, 64>(prm, stream);
 }
 
+// Split-K form: 2048- and 5632-wide inputs into outputs of a multiple of 64
+// columns (the Ouro O and down projections), fp32 partials per K range. Split
+// counts and tiles from a sweep with cold weights, timed together with the
+// residual RMSNorm that adds the partials: four ranges up to 64 rows; above,
+// two for the 2048-wide input (whose partials would cost more than the
+// parallelism buys) up to 128 rows, four for the 5632-wide one up to 256.
+// Returns 0 for shapes without a split form.
+int parts_splits(int64_t rows, int32_t out_features, int32_t in_features) {
+  if (rows < 1 || out_features < 64 || out_features % 64) return 0;
+  if (in_features == 2048) return rows <= 64 ? 4 : rows <= 128 ? 2 : 0;
+  if (in_features == 5632) return rows <= kLinearWideMaxRows ? 4 : 0;
+  return 0;
+}
+
+int dispatch_parts(const LinearParams& prm, hipStream_t stream) {
+  if (prm.K == 2048) {
+    if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 16, 4>(prm, stream);
+    if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 16, 4>(prm, stream);
+    return launch_linear_wide<2, 1, 4, 4, false, 32, 2>(prm, stream);
+  }
+  if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 44, 4>(prm, stream);
+  if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 44, 4>(prm, stream);
+  return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
+}
+
 int dispatch_linear(const LinearParams& prm, bool gated, hipStream_t stream) {
   if (wide_path(prm)) return dispatch_wide(prm, gated, stream);
   if (prm.M <= 16) return dispatch_rows<1, 4>(prm, gated, 8, stream);
@@ -452,6 +495,7 @@ extern "C" int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void
   prm.x = static_cast<const bf16_t*>(x);
   prm.w = static_cast<const bf16_t*>(w_packed);
   prm.y = static_cast<bf16_t*>(y);
+  prm.parts = nullptr;
   prm.ldx = ldx;
   prm.ldy = ldy;
   prm.M = rows;
@@ -460,4 +504,33 @@ extern "C" int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void
   prm.steps_per_wave = 0;
   if (rows > kLinearMaxRows && !wide_path(prm)) return CDB_ERR_SHAPE;
   return dispatch_linear(prm, gated != 0, stream);
+}
+
+extern "C" int32_t cdb_linear_parts_splits(int64_t rows, int32_t out_features, int32_t in_features, int32_t dtype) {
+  if (dtype != CDB_DTYPE_BF16) return 0;
+  return parts_splits(rows, out_features, in_features);
+}
+
+extern "C" int cdb_linear_parts(const void* x, int64_t ldx, const void* w_packed, float* parts, int64_t parts_elems,
+                                int32_t rows, int32_t out_features, int32_t in_features, int32_t dtype,
+                                hipStream_t stream) {
+  if (!x || !w_packed || !parts) return CDB_ERR_NULL;
+  if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
+  const int splits = parts_splits(rows, out_features, in_features);
+  if (splits == 0 || ldx < in_features || ldx % 8) return CDB_ERR_SHAPE;
+  if (parts_elems < (int64_t)splits * rows * out_features) return CDB_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)parts & 15)) return CDB_ERR_SHAPE;
+
+  LinearParams prm;
+  prm.x = static_cast<const bf16_t*>(x);
+  prm.w = static_cast<const bf16_t*>(w_packed);
+  prm.y = nullptr;
+  prm.parts = parts;
+  prm.ldx = ldx;
+  prm.ldy = out_features;
+  prm.M = rows;
+  prm.N = out_features;
+  prm.K = in_features;
+  prm.steps_per_wave = 0;
+  return dispatch_parts(prm, stream);
 }

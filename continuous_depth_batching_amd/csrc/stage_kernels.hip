@@ -41,6 +41,8 @@ CDB_DEVICE float block_sum(float v, float* lds) {
 // ---------------------------------------------------------------------------
 struct NormParams {
   const void* x;
+  const float* x_parts;  // when non-null, x is R(sum over x_splits of x_parts[s]) ([x_splits, rows, width] fp32)
+  int32_t x_splits;
   const void* residual;
   const void* w_a;
   const void* w_b;
@@ -75,10 +77,27 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_kernel(NormParams P) {
     const int col = (k * kThreads + threadIdx.x) * V;
     live[k] = col < W;
     if (live[k]) {
-      Vec<T, V> a;
-      a.load(x + col);
+      if (P.x_parts) {
+        // Split-K partials of the producing projection, summed in split order and
+        // rounded once, as the projection's own output would be.
 #pragma unroll
-      for (int i = 0; i < V; ++i) v[k][i] = a.get(i);
+        for (int i = 0; i < V; ++i) v[k][i] = 0.f;
+        for (int sp = 0; sp < P.x_splits; ++sp) {
+          const float* part = P.x_parts + ((int64_t)sp * P.rows + row) * W + col;
+#pragma unroll
+          for (int i = 0; i < V; i += 4) {
+            const float4 q4 = *reinterpret_cast<const float4*>(part + i);
+            v[k][i] += q4.x; v[k][i + 1] += q4.y; v[k][i + 2] += q4.z; v[k][i + 3] += q4.w;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[k][i] = Elem<T>::round(v[k][i]);
+      } else {
+        Vec<T, V> a;
+        a.load(x + col);
+#pragma unroll
+        for (int i = 0; i < V; ++i) v[k][i] = a.get(i);
+      }
       if (r) {
         Vec<T, V> b;
         b.load(r + col);
@@ -593,11 +612,29 @@ int cdb_rmsnorm_fused(const void* x, const void* residual, const void* w_a, cons
   if (mode < 0 || mode > 2 || rows < 0 || width <= 0 || rows > 0x7fffffff) return CDB_ERR_SHAPE;
   if (mode != 0 && !residual) return CDB_ERR_NULL;
   if (w_b && !out_y) return CDB_ERR_NULL;
-  NormParams P{x, residual, w_a, w_b, out_h, out_y, rows, width, mode, eps_a, eps_b};
+  NormParams P{x, nullptr, 0, residual, w_a, w_b, out_h, out_y, rows, width, mode, eps_a, eps_b};
   if (dtype == CDB_DTYPE_F32) {
     if (width % 4) return CDB_ERR_SHAPE;
     return launch_norm<float>(P, stream);
   }
+  if (dtype == CDB_DTYPE_BF16) {
+    if (width % 8) return CDB_ERR_SHAPE;
+    return launch_norm<bf16_t>(P, stream);
+  }
+  return CDB_ERR_UNSUPPORTED;
+}
+
+int cdb_rmsnorm_fused_parts(const float* x_parts, int32_t splits, const void* residual, const void* w_a,
+                            const void* w_b, void* out_h, void* out_y, int64_t rows, int32_t width, int32_t mode,
+                            float eps_a, float eps_b, int32_t dtype, hipStream_t stream) {
+  if (rows == 0) return CDB_OK;
+  if (!x_parts || !w_a || !out_h) return CDB_ERR_NULL;
+  if (mode < 0 || mode > 2 || rows < 0 || width <= 0 || rows > 0x7fffffff || splits < 1 || splits > 64)
+    return CDB_ERR_SHAPE;
+  if (mode != 0 && !residual) return CDB_ERR_NULL;
+  if (w_b && !out_y) return CDB_ERR_NULL;
+  if (((uintptr_t)x_parts & 15)) return CDB_ERR_SHAPE;
+  NormParams P{nullptr, x_parts, splits, residual, w_a, w_b, out_h, out_y, rows, width, mode, eps_a, eps_b};
   if (dtype == CDB_DTYPE_BF16) {
     if (width % 8) return CDB_ERR_SHAPE;
     return launch_norm<bf16_t>(P, stream);

@@ -9,6 +9,7 @@ ops can be captured into HIP graphs.
 
 from __future__ import annotations
 
+import functools
 import math
 from dataclasses import dataclass
 
@@ -441,6 +442,99 @@ def linear(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None, g
 @linear.register_fake
 def _(x, weight, packed, gated):
     return x.new_empty((x.shape[0], weight.shape[0] // 2 if gated else weight.shape[0]))
+
+
+@functools.lru_cache(maxsize=4096)
+def linear_parts_splits(rows: int, out_features: int, in_features: int) -> int:
+    """K ranges of cdb_linear_parts for a bf16 projection of this shape; 0 when it has no split form."""
+
+    return int(_lib.lib().cdb_linear_parts_splits(rows, out_features, in_features, _lib.CDB_DTYPE_BF16))
+
+
+def linear_parts_raw(x: torch.Tensor, packed: torch.Tensor, parts: torch.Tensor) -> None:
+    """parts[s] = fp32 partial x @ W.T over the s-th K range (split-K projection, no allocation)."""
+
+    _require_cuda(x, packed, parts)
+    rows, in_features = x.shape
+    splits, p_rows, out_features = parts.shape
+    if x.dtype != torch.bfloat16 or packed.dtype != x.dtype or parts.dtype != torch.float32:
+        raise TypeError("cdb_linear_parts takes bfloat16 x and weight and float32 parts")
+    if packed.numel() != out_features * in_features or p_rows != rows:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, packed weight of {packed.numel()} elements, "
+                         f"parts {tuple(parts.shape)}")
+    if splits != linear_parts_splits(rows, out_features, in_features):
+        raise ValueError(f"parts must hold linear_parts_splits(...) = "
+                         f"{linear_parts_splits(rows, out_features, in_features)} ranges, not {splits}")
+    if x.stride(1) != 1 or not parts.is_contiguous() or not packed.is_contiguous():
+        raise ValueError("x must have unit stride along its last dimension; parts and the packed weight are dense")
+    _lib.check(_lib.lib().cdb_linear_parts(x.data_ptr(), x.stride(0), packed.data_ptr(), parts.data_ptr(),
+                                           parts.numel(), rows, out_features, in_features, _lib.CDB_DTYPE_BF16,
+                                           _stream()), "cdb_linear_parts")
+
+
+def rmsnorm_fused_parts_raw(parts: torch.Tensor, residual: torch.Tensor | None, w_a: torch.Tensor,
+                            w_b: torch.Tensor | None, out_h: torch.Tensor, out_y: torch.Tensor | None, mode: int,
+                            eps_a: float, eps_b: float) -> None:
+    """cdb_rmsnorm_fused on x = R(sum of the split-K partials `parts` [splits, rows, width]) (no allocation)."""
+
+    splits, rows, width = parts.shape
+    if parts.dtype != torch.float32:
+        raise TypeError("parts must be float32")
+    for name, t in (("residual", residual), ("out_h", out_h), ("out_y", out_y)):
+        if t is not None and (t.shape != (rows, width) or t.dtype != out_h.dtype):
+            raise ValueError(f"{name} must be [{rows}, {width}] of out_h's dtype")
+    for name, w in (("w_a", w_a), ("w_b", w_b)):
+        if w is not None and (w.shape != (width,) or w.dtype != out_h.dtype):
+            raise ValueError(f"{name} must be a [{width}] vector of out_h's dtype")
+    _require_cuda(parts, residual, w_a, w_b, out_h, out_y)
+    _require_contiguous(parts=parts, residual=residual, w_a=w_a, w_b=w_b, out_h=out_h, out_y=out_y)
+    code = _lib.lib().cdb_rmsnorm_fused_parts(
+        parts.data_ptr(), splits, _ptr(residual), w_a.data_ptr(), _ptr(w_b), out_h.data_ptr(), _ptr(out_y),
+        rows, width, mode, eps_a, eps_b, dtype_code(out_h.dtype), _stream())
+    _lib.check(code, "cdb_rmsnorm_fused_parts")
+
+
+def linear_residual_rmsnorm_auto(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None,
+                                 residual: torch.Tensor, w_a: torch.Tensor, w_b: torch.Tensor, eps_a: float,
+                                 eps_b: float, mode: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The body of cdb::linear_residual_rmsnorm, callable without op dispatch."""
+
+    rows, in_features = x.shape
+    out_features = weight.shape[0]
+    splits = 0
+    if (packed is not None and x.dtype == torch.bfloat16 and x.stride(1) == 1 and x.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0 and residual.is_contiguous()):
+        splits = linear_parts_splits(rows, out_features, in_features)
+    h = x.new_empty((rows, out_features))
+    y = x.new_empty((rows, out_features))
+    if splits:
+        parts = torch.empty((splits, rows, out_features), dtype=torch.float32, device=x.device)
+        linear_parts_raw(x, packed, parts)
+        rmsnorm_fused_parts_raw(parts, residual, w_a, w_b, h, y, mode, eps_a, eps_b)
+    else:
+        o = linear_auto(x, weight, packed, False)
+        rmsnorm_fused_raw(o, residual.contiguous(), w_a, w_b, h, y, mode, eps_a, eps_b)
+    return h, y
+
+
+@torch.library.custom_op("cdb::linear_residual_rmsnorm", mutates_args=(), device_types="cuda")
+def linear_residual_rmsnorm(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None,
+                            residual: torch.Tensor, w_a: torch.Tensor, w_b: torch.Tensor, eps_a: float, eps_b: float,
+                            mode: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """residual_rmsnorm(x @ weight.T, residual, ...): a projection into a residual norm.
+
+    Shapes with a split-K form (linear_parts_splits > 0, given the packed weight)
+    write fp32 partials that the norm adds in order and rounds once -- the
+    projection's own bf16 output, never stored; others run cdb::linear then the
+    fused norm."""
+
+    return linear_residual_rmsnorm_auto(x, weight, packed, residual, w_a, w_b, eps_a, eps_b, mode)
+
+
+@linear_residual_rmsnorm.register_fake
+def _(x, weight, packed, residual, w_a, w_b, eps_a, eps_b, mode):
+    shape = (x.shape[0], weight.shape[0])
+    return x.new_empty(shape), x.new_empty(shape)
 
 
 def copy_rows_raw(src: torch.Tensor, src_index: torch.Tensor | None, dst: torch.Tensor,

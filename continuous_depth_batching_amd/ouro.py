@@ -15,10 +15,12 @@ SwiGLU MLP, a final norm after every loop step, and Linear(E, 1) exit gates.
     stream, capturable as one HIP graph per bucket;
   * coda = bank gather, LM head, greedy argmax;
   * prefill = the same stack over prompt tokens with the MFMA varlen attention.
-Dense projections of decode batches up to 64 rows run on the weight-streaming
-``cdb::linear`` kernel (the gated form writes silu(gate) * up directly);
-larger batches (prefill) use torch matmuls (hipBLASLt); the LM head takes the
-same split (its packed copy serves coda batches of up to 32 rows).
+Dense projections of decode batches run on the weight-streaming ``cdb::linear``
+kernels (the gated form writes silu(gate) * up directly); the O and down
+projections write split-K fp32 partials that the residual norm after them
+adds and rounds (``cdb::linear_residual_rmsnorm``); larger batches (prefill)
+use torch matmuls (hipBLASLt); the LM head's packed copy serves coda batches
+of up to 32 rows.
 Everything else is ``torch.ops.cdb.*`` / the C ABI.
 """
 
@@ -289,14 +291,13 @@ class OuroCDBAdapter(CDBModelAdapter):
         for li, w in enumerate(self.layers):
             qkv = ops.linear_auto(x, w["wqkv"], w["pqkv"], False)
             attn = attend(li, qkv)
-            o = ops.linear_auto(attn.view(rows, self.q_width), w["wo"], w["po"], False)
-            residual, x = torch.ops.cdb.residual_rmsnorm(o, residual, w["n_in2"], w["n_post"], self.eps, self.eps,
-                                                         ops.NORM_OURO_SANDWICH)
+            residual, x = ops.linear_residual_rmsnorm_auto(attn.view(rows, self.q_width), w["wo"], w["po"], residual,
+                                                           w["n_in2"], w["n_post"], self.eps, self.eps,
+                                                           ops.NORM_OURO_SANDWICH)
             act = ops.linear_auto(x, w["wgu"], w["pgu"], True)
-            m = ops.linear_auto(act, w["wd"], w["pd"], False)
             nxt = self.layers[li + 1]["n_in"] if li + 1 < num_layers else self.final_norm
-            residual, x = torch.ops.cdb.residual_rmsnorm(m, residual, w["n_post2"], nxt, self.eps, self.eps,
-                                                         ops.NORM_OURO_SANDWICH)
+            residual, x = ops.linear_residual_rmsnorm_auto(act, w["wd"], w["pd"], residual, w["n_post2"], nxt,
+                                                           self.eps, self.eps, ops.NORM_OURO_SANDWICH)
         return x
 
     def recurrent_step(self, launch: RecurrentLaunch) -> None:

@@ -95,6 +95,17 @@ int cdb_rmsnorm_fused(const void* x, const void* residual, const void* w_a, cons
                       void* out_y, int64_t rows, int32_t width, int32_t mode, float eps_a, float eps_b,
                       int32_t dtype, hipStream_t stream);
 
+/* cdb_rmsnorm_fused with x given as the fp32 split-K partials of the projection
+ * that produces it (cdb_linear_parts): x[r, c] = R(sum over s < splits, in
+ * order, of x_parts[s, r, c]), the projection's own rounded output, then the
+ * same modes as cdb_rmsnorm_fused. bf16 only; x_parts [splits, rows, width]
+ * contiguous and 16-byte aligned; 1 <= splits <= 64. Fuses the O and down
+ * projections' outputs into the residual norms that follow them
+ * (ouro/modeling_ouro.py:168,431 into :445-450 and :481-502). */
+int cdb_rmsnorm_fused_parts(const float* x_parts, int32_t splits, const void* residual, const void* w_a,
+                            const void* w_b, void* out_h, void* out_y, int64_t rows, int32_t width, int32_t mode,
+                            float eps_a, float eps_b, int32_t dtype, hipStream_t stream);
+
 /* out[r, :] = R(R(silu(g)) * u) for gate_up[r] = [g | u] of 2*width elements
  * (ouro/modeling_ouro.py:167-169, huginn/modeling_huginn.py:314-316). */
 int cdb_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t width, int32_t dtype, hipStream_t stream);
@@ -198,6 +209,23 @@ int cdb_linear_pack_weight(const void* w, int64_t ldw, void* w_packed, int64_t r
  * in_features a multiple of 32. */
 int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void* y, int64_t ldy, int32_t rows,
                int32_t out_features, int32_t in_features, int32_t gated, int32_t dtype, hipStream_t stream);
+
+/* Number of K ranges cdb_linear_parts splits a projection of this shape into,
+ * or 0 when it has no split form for it (then use cdb_linear or a library GEMM).
+ * Split forms exist for bf16 with in_features 2048 (up to 128 rows) or 5632 (up
+ * to 256 rows) and out_features a multiple of 64 -- the Ouro O and down
+ * projections (ouro/modeling_ouro.py:168,431). */
+int32_t cdb_linear_parts_splits(int64_t rows, int32_t out_features, int32_t in_features, int32_t dtype);
+
+/* Split-K projection: parts[s, r, n] = fp32 sum over k in the s-th of
+ * splits = cdb_linear_parts_splits(...) equal K ranges of x[r, k] * w[n, k],
+ * unrounded, for the consumer to add in order and round once
+ * (cdb_rmsnorm_fused_parts). w packed by cdb_linear_pack_weight; parts holds
+ * parts_elems >= splits * rows * out_features floats, 16-byte aligned; x row
+ * stride ldx a multiple of 8 elements. Shapes without a split form return
+ * CDB_ERR_SHAPE. Same projections as cdb_linear (ouro/modeling_ouro.py:168,431). */
+int cdb_linear_parts(const void* x, int64_t ldx, const void* w_packed, float* parts, int64_t parts_elems,
+                     int32_t rows, int32_t out_features, int32_t in_features, int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -116,3 +116,44 @@ def test_linear_argument_errors_without_gpu() -> None:
     assert pack(rows=2040) == _lib.CDB_ERR_SHAPE
     assert pack(ldw=2000) == _lib.CDB_ERR_SHAPE
     assert pack(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
+
+    bf16 = _lib.CDB_DTYPE_BF16
+    assert lib.cdb_linear_parts_splits(16, 2048, 2048, bf16) == 4
+    assert lib.cdb_linear_parts_splits(65, 2048, 2048, bf16) == 2
+    assert lib.cdb_linear_parts_splits(129, 2048, 2048, bf16) == 0
+    assert lib.cdb_linear_parts_splits(256, 2048, 5632, bf16) == 4
+    assert lib.cdb_linear_parts_splits(257, 2048, 5632, bf16) == 0
+    assert lib.cdb_linear_parts_splits(16, 2048, 4096, bf16) == 0
+    assert lib.cdb_linear_parts_splits(16, 2000, 2048, bf16) == 0
+    assert lib.cdb_linear_parts_splits(16, 2048, 2048, _lib.CDB_DTYPE_F32) == 0
+
+    def parts(**over):
+        args = dict(x=fake, ldx=2048, w=fake, parts=fake, parts_elems=4 * 16 * 2048, rows=16, out_features=2048,
+                    in_features=2048, dtype=bf16, stream=None)
+        args.update(over)
+        return lib.cdb_linear_parts(*args.values())
+
+    assert parts(parts=None) == _lib.CDB_ERR_NULL
+    assert parts(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
+    assert parts(rows=0) == _lib.CDB_ERR_SHAPE
+    assert parts(rows=129, parts_elems=1 << 30) == _lib.CDB_ERR_SHAPE
+    assert parts(in_features=4096, ldx=4096) == _lib.CDB_ERR_SHAPE
+    assert parts(parts_elems=4 * 16 * 2048 - 1) == _lib.CDB_ERR_SHAPE
+    assert parts(ldx=2044) == _lib.CDB_ERR_SHAPE
+    assert parts(parts=ctypes.c_void_p(0x1004)) == _lib.CDB_ERR_SHAPE
+
+    def norm(**over):
+        args = dict(parts=fake, splits=4, residual=fake, w_a=fake, w_b=fake, h=fake, y=fake, rows=16, width=2048,
+                    mode=1, eps_a=1e-6, eps_b=1e-6, dtype=bf16, stream=None)
+        args.update(over)
+        return lib.cdb_rmsnorm_fused_parts(*args.values())
+
+    assert norm(parts=None) == _lib.CDB_ERR_NULL
+    assert norm(residual=None) == _lib.CDB_ERR_NULL
+    assert norm(y=None) == _lib.CDB_ERR_NULL
+    assert norm(splits=0) == _lib.CDB_ERR_SHAPE
+    assert norm(splits=65) == _lib.CDB_ERR_SHAPE
+    assert norm(width=2044) == _lib.CDB_ERR_SHAPE
+    assert norm(parts=ctypes.c_void_p(0x1008)) == _lib.CDB_ERR_SHAPE
+    assert norm(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
+    assert norm(rows=0) == _lib.CDB_OK

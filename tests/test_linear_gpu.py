@@ -154,3 +154,79 @@ def test_pack_layout_is_the_mfma_operand_order(n: int, k: int) -> None:
     torch.cuda.synchronize()
     expected = w.view(n // 16, 16, k // 32, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1)
     assert torch.equal(packed, expected)
+
+
+PARTS_CASES = [(r, k, n) for r in (1, 5, 16, 32, 33, 64, 65, 128) for k, n in ((2048, 2048), (5632, 2048))] + [
+    (r, 5632, n) for r in (129, 200, 256) for n in (2048, 64)] + [(40, 2048, 1024), (3, 5632, 192)]
+
+
+@pytest.mark.parametrize("rows,k,n", PARTS_CASES)
+def test_split_k_partials_sum_to_the_fp32_product(rows: int, k: int, n: int) -> None:
+    from continuous_depth_batching_amd import ops
+
+    splits = ops.linear_parts_splits(rows, n, k)
+    assert splits in (2, 4)
+    x, w = _inputs(rows, k, n, seed=rows * 11 + k + n)
+    parts = torch.full((splits, rows, n), float("nan"), device="cuda")
+    ops.linear_parts_raw(x, ops.pack_linear_weight(w), parts)
+    torch.cuda.synchronize()
+    # Each partial is its K range's fp32 product, up to summation order: both sides
+    # chain a few dozen fp32 additions, so allow 2^-16 * sum |x_k w_k| -- about 1/60 of
+    # one average product term over a 1024-wide range, so a dropped or repeated
+    # K step still fails.
+    width = k // splits
+    for s in range(splits):
+        xs, ws = x[:, s * width:(s + 1) * width], w[:, s * width:(s + 1) * width]
+        ref = xs.float() @ ws.float().t()
+        tol = (xs.float().abs() @ ws.float().abs().t()) * 2.0 ** -16
+        assert ((parts[s] - ref).abs() <= tol).all(), f"split {s}: max excess {((parts[s] - ref).abs() - tol).max()}"
+    total = parts[0].clone()
+    for s in range(1, splits):
+        total += parts[s]
+    _check_rounded(total.bfloat16(), x.float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x, w))
+
+
+@pytest.mark.parametrize("rows,k", [(1, 2048), (16, 5632), (33, 2048), (96, 5632), (128, 2048), (256, 5632)])
+def test_norm_from_partials_is_the_two_step_result(rows: int, k: int) -> None:
+    """Partials added in order and rounded once, then the sandwich norm: bit-identical to
+    running the fused norm on that rounded projection output."""
+
+    from continuous_depth_batching_amd import ops
+
+    n = 2048
+    x, w = _inputs(rows, k, n, seed=rows + 3 * k)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows)
+    residual = torch.randn((rows, n), generator=g, device="cuda").bfloat16()
+    w_a = (1 + 0.1 * torch.randn(n, generator=g, device="cuda")).bfloat16()
+    w_b = (1 + 0.1 * torch.randn(n, generator=g, device="cuda")).bfloat16()
+    packed = ops.pack_linear_weight(w)
+    for mode in (ops.NORM_OURO_SANDWICH, ops.NORM_HUGINN_SANDWICH):
+        h, y = ops.linear_residual_rmsnorm_auto(x, w, packed, residual, w_a, w_b, 1e-6, 1e-5, mode)
+        splits = ops.linear_parts_splits(rows, n, k)
+        parts = torch.empty((splits, rows, n), device="cuda")
+        ops.linear_parts_raw(x, packed, parts)
+        o = parts[0].clone()
+        for s in range(1, splits):
+            o += parts[s]
+        h_ref, y_ref = torch.ops.cdb.residual_rmsnorm(o.bfloat16(), residual, w_a, w_b, 1e-6, 1e-5, mode)
+        torch.cuda.synchronize()
+        assert torch.equal(h, h_ref) and torch.equal(y, y_ref)
+        h2, y2 = ops.linear_residual_rmsnorm_auto(x, w, packed, residual, w_a, w_b, 1e-6, 1e-5, mode)
+        assert torch.equal(h, h2) and torch.equal(y, y2)
+
+
+def test_linear_residual_rmsnorm_falls_back_without_a_split_form() -> None:
+    from continuous_depth_batching_amd import ops
+
+    rows, k, n = 160, 2048, 2048  # a 2048-wide input above 128 rows has no split form
+    assert ops.linear_parts_splits(rows, n, k) == 0
+    x, w = _inputs(rows, k, n, seed=5)
+    residual = torch.randn((rows, n), device="cuda").bfloat16()
+    w_a = torch.ones(n, device="cuda").bfloat16()
+    h, y = torch.ops.cdb.linear_residual_rmsnorm(x, w, ops.pack_linear_weight(w), residual, w_a, w_a, 1e-6, 1e-6,
+                                                 ops.NORM_OURO_SANDWICH)
+    h_ref, y_ref = torch.ops.cdb.residual_rmsnorm(torch.mm(x, w.t()), residual, w_a, w_a, 1e-6, 1e-6,
+                                                  ops.NORM_OURO_SANDWICH)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref) and torch.equal(y, y_ref)

@@ -100,6 +100,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         ],
     ),
     "cdb_linear_parts_splits": (c_int32, [c_int64, c_int32, c_int32, c_int32]),
+    "cdb_linear_argmax_workspace_bytes": (c_int64, [c_int32, c_int32]),
+    "cdb_linear_argmax": (
+        c_int32,
+        [
+            _P, c_int64, _P, _P, _P, c_int64,  # x, ldx, w_packed, out, workspace, workspace_bytes
+            c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, dtype, stream
+        ],
+    ),
     "cdb_linear_parts": (
         c_int32,
         [

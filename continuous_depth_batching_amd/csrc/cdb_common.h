@@ -131,6 +131,14 @@ CDB_DEVICE float row16_max(float v) {
   return v;
 }
 
+// Greedy-argmax order (torch.argmax): a NaN counts as the maximum; among equal
+// values (and among NaNs) the smaller index wins. True when (a, ia) beats (b, ib).
+CDB_DEVICE bool argmax_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
 CDB_DEVICE float shfl_xor_f32(float v, int mask) {
   int lane = __lane_id();
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(v)));

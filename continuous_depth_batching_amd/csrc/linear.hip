@@ -37,11 +37,19 @@ namespace cdb {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 
+// Kept at 64 bytes, which the launch preloads into scalar registers: the
+// output forms share the two output pointers.
 struct LinearParams {
   const bf16_t* x;  // [M, K], row stride ldx elements
   const bf16_t* w;  // packed [N, K] (gated: [2N, K], gate rows then up rows)
-  bf16_t* y;        // [M, N], row stride ldy
-  float* parts;     // split-K form: fp32 partial sums [splits, M, N] instead of y
+  union {
+    bf16_t* y;        // [M, N], row stride ldy
+    float* best_val;  // argmax form: per row and 16-column tile, the largest rounded value ...
+  };
+  union {
+    float* parts;       // split-K form: fp32 partial sums [splits, M, N] instead of y
+    int32_t* best_idx;  // argmax form: ... and its first column ([M, N / 16] each)
+  };
   int64_t ldx, ldy;
   int32_t M, N, K;
   int32_t steps_per_wave;  // 32-element contraction steps per wave
@@ -59,8 +67,11 @@ CDB_DEVICE bf16x8_t load_x(const bf16_t* p) { return *reinterpret_cast<const bf1
 // MT: 16-row tiles of x (1, 2 or 4). NB: 16-column tiles of y per workgroup; every
 // wave computes all of them, so each x vector it loads feeds NB (gated: 2*NB)
 // MFMAs. S: contraction steps loaded per batch. SLOTS: LDS partial tiles (waves
-// w, w + SLOTS, w + 2*SLOTS, ... add into slot w in that order).
-template <int MT, int NB, int S, int SLOTS, bool GATED, int MAXT>
+// w, w + SLOTS, w + 2*SLOTS, ... add into slot w in that order). ARGMAX: instead
+// of y, store each row's greedy-argmax candidate of every 16-column tile (the
+// largest bf16-rounded output and its first column, torch.argmax order), for
+// linear_argmax_merge_kernel.
+template <int MT, int NB, int S, int SLOTS, bool GATED, int MAXT, bool ARGMAX = false>
 __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
   constexpr int NT = GATED ? 2 * NB : NB;  // W row tiles: gate tiles, then up tiles
   __shared__ f32x4_t red[SLOTS][NT][MT][kWave];
@@ -141,8 +152,41 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
   }
   __syncthreads();
 
-  // Epilogue: one thread per (column tile, row tile, lane) of the output.
   const int slots = min(nwaves, SLOTS);
+  if constexpr (ARGMAX) {
+    // One wave per (column tile, row tile): lane l holds row l % 16, columns
+    // 4 (l / 16) .. +3; the four lane groups of a row are then combined.
+    for (int idx = threadIdx.x; idx < NB * MT * kWave; idx += blockDim.x) {
+      const int j = idx / (MT * kWave);
+      const int mt = (idx / kWave) % MT;
+      const int l = idx & (kWave - 1);
+      const int m = mt * 16 + (l & 15);
+      f32x4_t v = red[0][j][mt][l];
+      for (int sl = 1; sl < slots; ++sl) v += red[sl][j][mt][l];
+      const int c0 = n0 + 16 * j + 4 * (l >> 4);
+      float best = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float r = round_bf16(v[i]);
+        if (argmax_better(r, c0 + i, best, bi)) { best = r; bi = c0 + i; }
+      }
+#pragma unroll
+      for (int mask = 16; mask <= 32; mask <<= 1) {
+        const float ov = shfl_xor_f32(best, mask);
+        const int oi = __shfl_xor(bi, mask, 64);
+        if (argmax_better(ov, oi, best, bi)) { best = ov; bi = oi; }
+      }
+      if (l < 16 && m < p.M) {
+        const int64_t e = (int64_t)m * (p.N / 16) + n0 / 16 + j;
+        p.best_val[e] = best;
+        p.best_idx[e] = bi;
+      }
+    }
+    return;
+  }
+
+  // Epilogue: one thread per (column tile, row tile, lane) of the output.
   for (int idx = threadIdx.x; idx < NB * MT * kWave; idx += blockDim.x) {
     const int j = idx / (MT * kWave);
     const int mt = (idx / kWave) % MT;
@@ -359,6 +403,67 @@ __global__ void __launch_bounds__(256) linear_pack_kernel(const bf16_t* w, int64
   }
 }
 
+// Second pass of the argmax form: one workgroup per row combines the row's tile
+// candidates. Each thread loads its share of the candidates up front (16-byte
+// vectors), so the row is one round of loads. The comparison is a total order,
+// so the reduction order does not matter.
+constexpr int kArgmaxMergeThreads = 256;
+constexpr int kArgmaxMergeVecs = 4;  // 16-byte vectors (4 candidates) per thread per batch
+
+__global__ void __launch_bounds__(kArgmaxMergeThreads) linear_argmax_merge_kernel(const float* best_val,
+                                                                                  const int32_t* best_idx,
+                                                                                  int32_t tiles, int64_t* out,
+                                                                                  int32_t rows) {
+  __shared__ float sv[kArgmaxMergeThreads / kWave];
+  __shared__ int si[kArgmaxMergeThreads / kWave];
+  const int row = blockIdx.x;
+  if (row >= rows) return;
+  const float* v = best_val + (int64_t)row * tiles;
+  const int32_t* ix = best_idx + (int64_t)row * tiles;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  // Whole vectors while the row's candidates are 16-byte aligned (tiles % 4 == 0 and
+  // row bases aligned); the remainder one by one.
+  const int nvec = (tiles % 4 == 0) ? tiles / 4 : 0;
+  for (int base = threadIdx.x; base < nvec; base += kArgmaxMergeThreads * kArgmaxMergeVecs) {
+    float4 vv[kArgmaxMergeVecs];
+    int4 iv[kArgmaxMergeVecs];
+#pragma unroll
+    for (int u = 0; u < kArgmaxMergeVecs; ++u) {
+      const int q = min(base + u * kArgmaxMergeThreads, nvec - 1);
+      vv[u] = reinterpret_cast<const float4*>(v)[q];
+      iv[u] = reinterpret_cast<const int4*>(ix)[q];
+    }
+#pragma unroll
+    for (int u = 0; u < kArgmaxMergeVecs; ++u) {
+      if (base + u * kArgmaxMergeThreads >= nvec) continue;
+      if (argmax_better(vv[u].x, iv[u].x, best, bi)) { best = vv[u].x; bi = iv[u].x; }
+      if (argmax_better(vv[u].y, iv[u].y, best, bi)) { best = vv[u].y; bi = iv[u].y; }
+      if (argmax_better(vv[u].z, iv[u].z, best, bi)) { best = vv[u].z; bi = iv[u].z; }
+      if (argmax_better(vv[u].w, iv[u].w, best, bi)) { best = vv[u].w; bi = iv[u].w; }
+    }
+  }
+  for (int e = nvec * 4 + threadIdx.x; e < tiles; e += kArgmaxMergeThreads)
+    if (argmax_better(v[e], ix[e], best, bi)) { best = v[e]; bi = ix[e]; }
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) {
+    const float ov = shfl_xor_f32(best, mask);
+    const int oi = __shfl_xor(bi, mask, 64);
+    if (argmax_better(ov, oi, best, bi)) { best = ov; bi = oi; }
+  }
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kArgmaxMergeThreads / kWave; ++w)
+      if (argmax_better(sv[w], si[w], best, bi)) { best = sv[w]; bi = si[w]; }
+    out[row] = bi;
+  }
+}
+
 // Launch shape of one instantiation: threads per workgroup are capped so the
 // accumulators and a batch of loads fit without spilling, and the LDS partial
 // tiles (SLOTS x NT x MT x 1 KiB) stay within 64 KiB.
@@ -378,15 +483,15 @@ inline int linear_steps_per_wave(int32_t in_features, int batch, int max_waves) 
   return (per_wave + batch - 1) / batch * batch;
 }
 
-template <int MT, int NB, int S, bool GATED>
+template <int MT, int NB, int S, bool GATED, bool ARGMAX = false>
 int launch_linear(LinearParams prm, hipStream_t stream, int max_waves = kLinearMaxWaves) {
   using Shape = LinearShape<MT, NB, S, GATED>;
   if (prm.N % (16 * NB)) return CDB_ERR_SHAPE;
   const int waves_cap = max_waves < Shape::kMaxWaves ? max_waves : Shape::kMaxWaves;
   prm.steps_per_wave = linear_steps_per_wave(prm.K, S, waves_cap);
   const int nwaves = (prm.K / 32 + prm.steps_per_wave - 1) / prm.steps_per_wave;
-  hipLaunchKernelGGL((linear_kernel<MT, NB, S, Shape::kSlots, GATED, Shape::kThreads>), dim3(prm.N / (16 * NB)),
-                     dim3(nwaves * kWave), 0, stream, prm);
+  hipLaunchKernelGGL((linear_kernel<MT, NB, S, Shape::kSlots, GATED, Shape::kThreads, ARGMAX>),
+                     dim3(prm.N / (16 * NB)), dim3(nwaves * kWave), 0, stream, prm);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 
@@ -533,4 +638,48 @@ extern "C" int cdb_linear_parts(const void* x, int64_t ldx, const void* w_packed
   prm.K = in_features;
   prm.steps_per_wave = 0;
   return dispatch_parts(prm, stream);
+}
+
+extern "C" int64_t cdb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_features) {
+  if (rows < 0 || out_features < 16 || out_features % 16) return -1;
+  return (int64_t)rows * (out_features / 16) * 8;
+}
+
+extern "C" int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int64_t* out, void* workspace,
+                                 int64_t workspace_bytes, int32_t rows, int32_t out_features, int32_t in_features,
+                                 int32_t dtype, hipStream_t stream) {
+  if (!x || !w_packed || !out || !workspace) return CDB_ERR_NULL;
+  if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
+  if (rows < 1 || rows > kLinearMaxRows || out_features < 16 || out_features % 16 || in_features < 32 ||
+      in_features % 32 || ldx < in_features || ldx % 8)
+    return CDB_ERR_SHAPE;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_packed & 15) || ((uintptr_t)workspace & 15)) return CDB_ERR_SHAPE;
+  const int tiles = out_features / 16;
+  if (workspace_bytes < (int64_t)rows * tiles * 8) return CDB_ERR_CAPACITY;
+
+  LinearParams prm;
+  prm.x = static_cast<const bf16_t*>(x);
+  prm.w = static_cast<const bf16_t*>(w_packed);
+  prm.best_val = static_cast<float*>(workspace);
+  prm.best_idx = reinterpret_cast<int32_t*>(static_cast<float*>(workspace) + (int64_t)rows * tiles);
+  prm.ldx = ldx;
+  prm.ldy = out_features;
+  prm.M = rows;
+  prm.N = out_features;
+  prm.K = in_features;
+  prm.steps_per_wave = 0;
+  static_assert(sizeof(LinearParams) == 64, "LinearParams is preloaded whole");
+  // The projection kernel's tile choice (two column tiles per workgroup once N is wide).
+  const bool two = out_features >= 4096 && out_features % 32 == 0;
+  int rc;
+  if (rows <= 16)
+    rc = two ? launch_linear<1, 2, 4, false, true>(prm, stream, 8) : launch_linear<1, 1, 4, false, true>(prm, stream, 8);
+  else if (rows <= 32)
+    rc = two ? launch_linear<2, 2, 4, false, true>(prm, stream, 4) : launch_linear<2, 1, 4, false, true>(prm, stream, 4);
+  else
+    rc = two ? launch_linear<4, 2, 2, false, true>(prm, stream, 4) : launch_linear<4, 1, 2, false, true>(prm, stream, 4);
+  if (rc != CDB_OK) return rc;
+  hipLaunchKernelGGL(linear_argmax_merge_kernel, dim3((unsigned)rows), dim3(kArgmaxMergeThreads), 0, stream,
+                     prm.best_val, prm.best_idx, tiles, out, rows);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }

@@ -211,11 +211,6 @@ __global__ void __launch_bounds__(kThreads) copy_rows_kernel(const uint8_t* src,
 // Greedy argmax over the vocabulary (cdb/model_runner.py:1062,1105): first
 // index of the maximum; a NaN counts as the maximum, as torch.argmax does.
 // ---------------------------------------------------------------------------
-CDB_DEVICE bool better(float a, int ia, float b, int ib) {
-  const bool na = a != a, nb = b != b;
-  if (na || nb) return na && (!nb || ia < ib);
-  return a > b || (a == b && ia < ib);
-}
 
 template <typename T>
 __global__ void __launch_bounds__(kThreads) argmax_kernel(const T* logits, int64_t* out, int64_t rows, int32_t vocab) {
@@ -248,26 +243,26 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const T* logits, int64
       for (int e = 0; e < V; ++e) {
         const float v = buf[u].get(e);
         const int j = vi * V + e;
-        if (better(v, j, best, bi)) { best = v; bi = j; }
+        if (argmax_better(v, j, best, bi)) { best = v; bi = j; }
       }
     }
   }
   for (int j = nvec * V + threadIdx.x; j < vocab; j += kThreads) {
     const float v = Elem<T>::load(x + j);
-    if (better(v, j, best, bi)) { best = v; bi = j; }
+    if (argmax_better(v, j, best, bi)) { best = v; bi = j; }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
     const float ov = shfl_xor_f32(best, m);
     const int oi = __shfl_xor(bi, m, 64);
-    if (better(ov, oi, best, bi)) { best = ov; bi = oi; }
+    if (argmax_better(ov, oi, best, bi)) { best = ov; bi = oi; }
   }
   const int wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) { lv[wave] = best; li[wave] = bi; }
   __syncthreads();
   if (threadIdx.x == 0) {
     for (int w = 1; w < kThreads / 64; ++w)
-      if (better(lv[w], li[w], best, bi)) { best = lv[w]; bi = li[w]; }
+      if (argmax_better(lv[w], li[w], best, bi)) { best = lv[w]; bi = li[w]; }
     out[row] = bi == 0x7fffffff ? 0 : bi;
   }
 }

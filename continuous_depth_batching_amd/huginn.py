@@ -471,7 +471,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
         layout = self.kv_cache_layout()
         attend = self._decode_attend(launch, lambda i: (None, layout.coda_layer_index(i)))
         hidden = self._coda_hidden(state, attend)
-        return ops.argmax_rows(ops.linear_auto(hidden, self.lm_head_w, self.lm_head_p, False))
+        return ops.lm_head_argmax(hidden, self.lm_head_w, self.lm_head_p)
 
     def prefill(self, launch: PrefillLaunch) -> torch.Tensor:
         tokens = launch.tokens.numel()
@@ -490,7 +490,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             state, _ = self._blocks(self.core_blocks, h, n1, attend, None)
         hidden = self._coda_hidden(state, self._prefill_attend(launch, layout.coda_layer_index))
         last = torch.ops.cdb.gather_rows(hidden, launch.last_index)
-        return ops.argmax_rows(ops.linear_auto(last, self.lm_head_w, self.lm_head_p, False))
+        return ops.lm_head_argmax(last, self.lm_head_w, self.lm_head_p)
 
 
 __all__ = ["HuginnConfig", "HuginnForCausalLM", "HuginnCDBAdapter", "build_huginn", "init_huginn_weights",

@@ -593,6 +593,43 @@ def argmax_raw(logits: torch.Tensor, out: torch.Tensor) -> None:
                                      _stream()), "cdb_argmax")
 
 
+def linear_argmax_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor) -> None:
+    """out[r] = argmax_n of the bf16 logits x @ W.T (torch.argmax order), the logits never stored."""
+
+    _require_cuda(x, packed, out, workspace)
+    rows, in_features = x.shape
+    out_features = packed.numel() // in_features if in_features else 0
+    if x.dtype != torch.bfloat16 or packed.dtype != x.dtype:
+        raise TypeError("cdb_linear_argmax takes bfloat16 x and weight")
+    if out.dtype != torch.int64 or out.numel() < rows or packed.numel() != out_features * in_features:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)}, packed weight of {packed.numel()} elements, "
+                         f"out of {out.numel()} int64")
+    if x.stride(1) != 1 or not packed.is_contiguous() or not out.is_contiguous() or not workspace.is_contiguous():
+        raise ValueError("x must have unit stride along its last dimension; weight, out and workspace are dense")
+    _lib.check(_lib.lib().cdb_linear_argmax(x.data_ptr(), x.stride(0), packed.data_ptr(), out.data_ptr(),
+                                            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                                            rows, out_features, in_features, _lib.CDB_DTYPE_BF16, _stream()),
+               "cdb_linear_argmax")
+
+
+def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None) -> torch.Tensor:
+    """Greedy tokens of a coda batch: argmax over the vocabulary of x @ weight.T.
+
+    Batches the projection kernel serves (linear_prefers_kernel) run the fused
+    cdb_linear_argmax; others compute the logits (torch.mm) and cdb_argmax them."""
+
+    rows, in_features = x.shape
+    vocab = weight.shape[0]
+    if (packed is not None and x.dtype == torch.bfloat16 and 1 <= rows <= LINEAR_MAX_ROWS
+            and linear_prefers_kernel(rows, vocab, False, in_features) and vocab % 16 == 0
+            and in_features % 32 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
+        out = torch.empty((rows,), dtype=torch.int64, device=x.device)
+        workspace = torch.empty((rows * (vocab // 16) * 2,), dtype=torch.float32, device=x.device)
+        linear_argmax_raw(x, packed, out, workspace)
+        return out
+    return argmax_rows(linear_auto(x, weight, packed, False))
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """Greedy token per row (first index of the max), without op dispatch."""
 

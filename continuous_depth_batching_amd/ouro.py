@@ -13,7 +13,8 @@ SwiGLU MLP, a final norm after every loop step, and Linear(E, 1) exit gates.
     with fused RoPE + KV append, O-projection, fused gate/up GEMM + SiLU, down
     GEMM, the final norm, the bank scatter and the exit gate -- all on the
     stream, capturable as one HIP graph per bucket;
-  * coda = bank gather, LM head, greedy argmax;
+  * coda = bank gather, then the LM head with its greedy argmax fused
+    (cdb_linear_argmax: the logits never reach memory);
   * prefill = the same stack over prompt tokens with the MFMA varlen attention.
 Dense projections of decode batches run on the weight-streaming ``cdb::linear``
 kernels (the gated form writes silu(gate) * up directly); the O and down
@@ -354,8 +355,7 @@ class OuroCDBAdapter(CDBModelAdapter):
         return self.coda_from_hidden(last)
 
     def coda_from_hidden(self, hidden: torch.Tensor) -> torch.Tensor:
-        logits = ops.linear_auto(hidden, self.lm_head_w, self.lm_head_p, False)
-        return ops.argmax_rows(logits)
+        return ops.lm_head_argmax(hidden, self.lm_head_w, self.lm_head_p)
 
     def coda(self, launch: StageLaunch) -> torch.Tensor:
         # Eager, once per coda tick: direct calls rather than op dispatch.

@@ -227,6 +227,24 @@ int32_t cdb_linear_parts_splits(int64_t rows, int32_t out_features, int32_t in_f
 int cdb_linear_parts(const void* x, int64_t ldx, const void* w_packed, float* parts, int64_t parts_elems,
                      int32_t rows, int32_t out_features, int32_t in_features, int32_t dtype, hipStream_t stream);
 
+/* Workspace bytes cdb_linear_argmax needs: rows * (out_features / 16) * 8
+ * (-1 for invalid sizes). */
+int64_t cdb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_features);
+
+/* Greedy coda in one call: out[r] = the first n maximizing R(sum_k x[r, k] *
+ * w[n, k]) over n < out_features, NaN counting as the maximum (torch.argmax over
+ * the bf16 logits). It replaces lm_head followed by argmax
+ * (cdb/model_runner.py:1062,1105; ouro/modeling_ouro.py:755-775). The logits
+ * are never stored. The projection kernel keeps, per row and 16-column tile,
+ * the best rounded value and its column in `workspace`; a second kernel
+ * combines them. bf16, w packed by cdb_linear_pack_weight, 1 <= rows <= 64,
+ * out_features a multiple of 16, in_features a multiple of 32, ldx a multiple
+ * of 8; workspace 16-byte aligned, at least cdb_linear_argmax_workspace_bytes
+ * bytes (CDB_ERR_CAPACITY otherwise). */
+int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int64_t* out, void* workspace,
+                      int64_t workspace_bytes, int32_t rows, int32_t out_features, int32_t in_features,
+                      int32_t dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -157,3 +157,22 @@ def test_linear_argument_errors_without_gpu() -> None:
     assert norm(parts=ctypes.c_void_p(0x1008)) == _lib.CDB_ERR_SHAPE
     assert norm(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
     assert norm(rows=0) == _lib.CDB_OK
+
+    assert lib.cdb_linear_argmax_workspace_bytes(16, 49152) == 16 * 3072 * 8
+    assert lib.cdb_linear_argmax_workspace_bytes(16, 49150) == -1
+
+    def am(**over):
+        args = dict(x=fake, ldx=2048, w=fake, out=fake, ws=fake, ws_bytes=16 * 3072 * 8, rows=16, out_features=49152,
+                    in_features=2048, dtype=bf16, stream=None)
+        args.update(over)
+        return lib.cdb_linear_argmax(*args.values())
+
+    assert am(out=None) == _lib.CDB_ERR_NULL
+    assert am(ws=None) == _lib.CDB_ERR_NULL
+    assert am(dtype=_lib.CDB_DTYPE_F32) == _lib.CDB_ERR_UNSUPPORTED
+    assert am(rows=0) == _lib.CDB_ERR_SHAPE
+    assert am(rows=65) == _lib.CDB_ERR_SHAPE
+    assert am(out_features=49150) == _lib.CDB_ERR_SHAPE
+    assert am(ldx=2044) == _lib.CDB_ERR_SHAPE
+    assert am(ws=ctypes.c_void_p(0x1008)) == _lib.CDB_ERR_SHAPE
+    assert am(ws_bytes=16 * 3072 * 8 - 1) == _lib.CDB_ERR_CAPACITY

@@ -230,3 +230,64 @@ def test_linear_residual_rmsnorm_falls_back_without_a_split_form() -> None:
                                                   ops.NORM_OURO_SANDWICH)
     torch.cuda.synchronize()
     assert torch.equal(h, h_ref) and torch.equal(y, y_ref)
+
+
+@pytest.mark.parametrize("rows", [1, 5, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("k,n", [(2048, 49152), (2048, 1024), (64, 32)])
+def test_fused_lm_head_argmax_equals_argmax_of_the_logits(rows: int, k: int, n: int) -> None:
+    """cdb_linear_argmax picks exactly what torch.argmax picks on the projection kernel's bf16 logits."""
+
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(rows, k, n, seed=rows * 3 + n)
+    packed = ops.pack_linear_weight(w)
+    logits = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, packed, logits)
+    out = torch.full((rows,), -7, dtype=torch.int64, device="cuda")
+    ws = torch.empty((rows * (n // 16) * 2,), dtype=torch.float32, device="cuda")
+    ops.linear_argmax_raw(x, packed, out, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, torch.argmax(logits, dim=-1))
+    assert torch.equal(out, ops.argmax_rows(logits))
+
+
+def test_fused_lm_head_argmax_ties_and_nans_follow_torch() -> None:
+    from continuous_depth_batching_amd import ops
+
+    rows, k, n = 8, 2048, 49152
+    x, w = _inputs(rows, k, n, seed=11)
+    # Columns 100 and 5000 get the same weight row, aligned with every x row: a tie at
+    # the maximum, which the first column wins.
+    w[100] = (x.float().sum(0) * 0.01).bfloat16()
+    w[5000] = w[100]
+    packed = ops.pack_linear_weight(w)
+    out = torch.empty((rows,), dtype=torch.int64, device="cuda")
+    ws = torch.empty((rows * (n // 16) * 2,), dtype=torch.float32, device="cuda")
+    ops.linear_argmax_raw(x, packed, out, ws)
+    logits = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, packed, logits)
+    torch.cuda.synchronize()
+    assert torch.equal(logits[:, 100], logits[:, 5000])
+    assert torch.equal(out, torch.argmax(logits, dim=-1)) and (out == 100).all()
+    # NaN logits count as the maximum; the first NaN column wins.
+    w[30000] = float("nan")
+    w[7001] = float("nan")
+    packed = ops.pack_linear_weight(w)
+    ops.linear_argmax_raw(x, packed, out, ws)
+    torch.cuda.synchronize()
+    assert (out == 7001).all()
+
+
+def test_lm_head_argmax_routes_large_batches_through_the_logits() -> None:
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(48, 2048, 49152, seed=2)
+    packed = ops.pack_linear_weight(w)
+    tokens = ops.lm_head_argmax(x, w, packed)
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, ops.argmax_rows(ops.linear_auto(x, w, packed, False)))
+    small = ops.lm_head_argmax(x[:16], w, packed)
+    logits = torch.empty((16, 49152), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x[:16], packed, logits)
+    torch.cuda.synchronize()
+    assert torch.equal(small, torch.argmax(logits, dim=-1))

@@ -227,6 +227,19 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
 //   * workgroups of one column range (different row ranges) sit on one XCD,
 //     so the weights cross HBM once.
 // ---------------------------------------------------------------------------
+// Slot of x unit (row r of a 16-row tile, step t of the chunk, k group g) within
+// its 64-unit block: the MFMA lane that reads it is r + 16 g, with r swizzled by
+// an XOR of (t, g) so that the eight (SC = 2) or sixteen (SC = 4) units one row
+// contributes to a chunk -- stored by consecutive threads -- land on distinct
+// LDS banks. For each (t, g) the XOR permutes r, so a step's 64 units stay one
+// contiguous block and the reads stay conflict-free.
+template <int SC>
+CDB_DEVICE int x_slot(int r, int t, int g) {
+  static_assert(SC == 2 || SC == 4, "x chunks of 2 or 4 steps");
+  const int sw = SC == 2 ? 2 * (4 * (t & 1) + g) : 4 * (t & 3) + g;
+  return (r ^ sw) + 16 * g;
+}
+
 // KSPLIT > 1: K is cut into KSPLIT ranges of KSTEPS steps; each workgroup covers
 // one range and stores fp32 partial sums to p.parts[split], for a consumer that
 // adds them in split order and rounds once (the residual RMSNorm).
@@ -280,8 +293,12 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     const int row = u / (KC / 8), k8 = u % (KC / 8);
     xsrc[i] = p.x + (int64_t)min(m0 + row, p.M - 1) * p.ldx + (int64_t)k_first * 32;
     xk[i] = 8 * k8;
-    xdst[i] = (((row >> 4) * SC + (k8 >> 2)) * kWave) + (row & 15) + 16 * (k8 & 3);
+    xdst[i] = (((row >> 4) * SC + (k8 >> 2)) * kWave) + x_slot<SC>(row & 15, k8 >> 2, k8 & 3);
   }
+  // This lane's operand unit (row lane % 16, k group lane / 16) of each step.
+  int xrd[SC];
+#pragma unroll
+  for (int t = 0; t < SC; ++t) xrd[t] = x_slot<SC>(lane & 15, t, lane >> 4);
   auto load_x = [&](int c, bf16x8_t (&xr)[UPT]) {
 #pragma unroll
     for (int i = 0; i < UPT; ++i) xr[i] = cdb::load_x(xsrc[i] + min(c * KC + xk[i], total * 32 - 8));
@@ -331,7 +348,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
           const bool valid = c * SC + t < total;
           bf16x8_t b[MT];
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[cur][mt][t][lane] : bf16x8_t{};
+          for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[cur][mt][t][xrd[t]] : bf16x8_t{};
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
             const bf16x8_t a = valid ? ring[st][nt][t] : bf16x8_t{};

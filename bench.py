@@ -184,33 +184,45 @@ def time_prefill_attention(prompt_lens, iters: int) -> dict:
 
 
 def time_decode_projections(rows: int = 16, layers: int = 24, reps: int = 4) -> dict:
-    """The Ouro-1.4B layer's four projections on cdb_linear at `rows` rows, each over
-    `layers` distinct weights (one per layer, so every launch streams cold weights as
-    in a layer stack), timed from a captured graph so launch gaps are the GPU's own."""
+    """The Ouro-1.4B layer's four projections at `rows` rows as a recurrent step runs them
+    (QKV and gate/up + SiLU on cdb_linear; O and down as split-K fp32 partials on
+    cdb_linear_parts, which the residual norm after them adds), each over `layers`
+    distinct weights (one per layer, so every launch streams cold weights as in a layer
+    stack), timed from a captured graph so launch gaps are the GPU's own."""
 
     import torch
 
     from continuous_depth_batching_amd import ops
 
-    shapes = {"qkv": (2048, 6144, False), "o": (2048, 2048, False), "gate_up_silu": (2048, 5632, True),
-              "down": (5632, 2048, False)}
+    shapes = {"qkv": (2048, 6144, False), "o_split_k": (2048, 2048, False), "gate_up_silu": (2048, 5632, True),
+              "down_split_k": (5632, 2048, False)}
     result = {}
     for name, (k, n, gated) in shapes.items():
+        split = name.endswith("split_k")
         gen = torch.Generator(device="cuda")
         gen.manual_seed(3)
         weights = [ops.pack_linear_weight((torch.randn(((2 if gated else 1) * n, k), generator=gen, device="cuda")
                                            * 0.02).bfloat16()) for _ in range(layers)]
         x = torch.randn((rows, k), generator=gen, device="cuda").bfloat16()
-        y = torch.empty((rows, n), dtype=torch.bfloat16, device="cuda")
+        splits = ops.linear_parts_splits(rows, n, k) if split else 0
+        y = (torch.empty((splits, rows, n), dtype=torch.float32, device="cuda") if split
+             else torch.empty((rows, n), dtype=torch.bfloat16, device="cuda"))
+
+        def run(w):
+            if split:
+                ops.linear_parts_raw(x, w, y)
+            else:
+                ops.linear_raw(x, w, y, gated=gated)
+
         stream = torch.cuda.Stream()
         with torch.cuda.stream(stream):
             for w in weights[:2]:
-                ops.linear_raw(x, w, y, gated=gated)
+                run(w)
             stream.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 for w in weights:
-                    ops.linear_raw(x, w, y, gated=gated)
+                    run(w)
             graph.replay()
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record(stream)
@@ -219,7 +231,7 @@ def time_decode_projections(rows: int = 16, layers: int = 24, reps: int = 4) -> 
             end.record(stream)
         end.synchronize()
         us = start.elapsed_time(end) / (reps * layers) * 1e3
-        nbytes = weights[0].numel() * 2 + rows * (k + n) * 2
+        nbytes = weights[0].numel() * 2 + rows * k * 2 + y.numel() * y.element_size()
         result[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
         del weights

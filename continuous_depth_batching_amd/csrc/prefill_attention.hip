@@ -96,9 +96,11 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
   __shared__ __attribute__((aligned(16))) T vt_lds[2][D][kKeys + kVtPad];
   __shared__ int page_lds[kLdsPages];
 
-  const int tile = blockIdx.x;
-  const int h = blockIdx.y;
-  if (tile >= P.num_tiles || h >= P.num_heads) return;
+  // One workgroup per (tile, head), heads fastest: the host lists the tiles
+  // longest prefix first, so the heaviest workgroups of every head start first.
+  const int tile = blockIdx.x / P.num_heads;
+  const int h = blockIdx.x - tile * P.num_heads;
+  if (tile >= P.num_tiles) return;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -245,6 +247,9 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
         }
       }
       // Scale, causal mask, online softmax over this lane's 8 keys and its 3 peers.
+      // Only blocks that reach past the wave's first query or the last key need
+      // the mask (wave-uniform test).
+      const bool masked = kb + kKeys - 1 > past + tile_q0 + wave * 16 || kb + kKeys > key_end;
       float sv[2][4];
       float mloc = -INFINITY;
 #pragma unroll
@@ -252,21 +257,25 @@ __global__ void __launch_bounds__(256) prefill_attention_kernel(PrefillParams P)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kp = kb + t * 16 + grp * 4 + i;
-          const float x = (kp <= q_pos && kp < key_end) ? st[t][i] * P.scale_log2 : -INFINITY;
-          sv[t][i] = x;
-          mloc = fmaxf(mloc, x);
+          const float x = st[t][i] * P.scale_log2;
+          sv[t][i] = !masked || (kp <= q_pos && kp < key_end) ? x : -INFINITY;
+          mloc = fmaxf(mloc, sv[t][i]);
         }
       mloc = fmaxf(mloc, shfl_xor_f32(mloc, 16));
       mloc = fmaxf(mloc, shfl_xor_f32(mloc, 32));
+      // Key 0 is visible to every query (its position is >= 0 and key_end > 0), so
+      // from the first block on m_new is finite: exp2(-inf) = 0 covers the first
+      // rescale and every masked key without special cases. v_exp_f32 (exp2 with
+      // results below 2^-126 flushed to 0) is enough for softmax weights.
       const float m_new = fmaxf(m, mloc);
-      const float alpha = m_new == -INFINITY ? 1.f : exp2f(m - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
       float psum = 0.f;
       float p[2][4];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[t][i] = m_new == -INFINITY ? 0.f : exp2f(sv[t][i] - m_new);
+          p[t][i] = __builtin_amdgcn_exp2f(sv[t][i] - m_new);
           psum += p[t][i];
         }
       l = l * alpha + psum;
@@ -350,7 +359,8 @@ int cdb_prefill_attention(const void* q, const void* k_pool, const void* v_pool,
   PrefillParams P{q, k_pool, v_pool, layer_stride, layer, block_table, table_row, cu_q, past, tile_seq, tile_q0, out,
                   pool_blocks, num_tiles, num_seqs, num_heads, num_kv_heads, table_width, bs_log2,
                   scale * 1.4426950408889634f};
-  const dim3 grid((unsigned)num_tiles, (unsigned)num_heads);
+  if ((int64_t)num_tiles * num_heads > 0x7fffffff) return CDB_ERR_SHAPE;
+  const dim3 grid((unsigned)(num_tiles * num_heads));
   auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, P);
     return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;

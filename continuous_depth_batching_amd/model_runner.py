@@ -474,7 +474,7 @@ class ModelRunner:
         cache = self.cache
         meta = self.prefill_metadata(requests)
         last_index = meta.last_index
-        tile_seq, tile_q0 = ops.prefill_tiles(meta.lens)
+        tile_seq, tile_q0 = ops.prefill_tiles(meta.lens, meta.past)
         with self._on_stream():
             cache.flush_table_updates()
             launch = PrefillLaunch(

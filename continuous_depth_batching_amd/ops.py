@@ -757,8 +757,11 @@ def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: 
 PREFILL_TILE = 64
 
 
-def prefill_tiles(query_lens: "list[int] | np.ndarray") -> tuple["np.ndarray", "np.ndarray"]:
-    """Tile -> (sequence, first query) arrays for cdb_prefill_attention (64 queries per tile)."""
+def prefill_tiles(query_lens: "list[int] | np.ndarray",
+                  past: "list[int] | np.ndarray | None" = None) -> tuple["np.ndarray", "np.ndarray"]:
+    """Tile -> (sequence, first query) arrays for cdb_prefill_attention (64 queries per tile),
+    longest causal prefix (past + last query of the tile) first, so the heaviest workgroups
+    start first and the launch ends on short ones. Any order computes the same outputs."""
 
     import numpy as np
 
@@ -767,7 +770,10 @@ def prefill_tiles(query_lens: "list[int] | np.ndarray") -> tuple["np.ndarray", "
     seq = np.repeat(np.arange(lens.size, dtype=np.int32), counts)
     starts = np.concatenate([[0], np.cumsum(counts)[:-1]]) if lens.size else np.zeros(0, np.int64)
     q0 = (np.arange(int(counts.sum())) - np.repeat(starts, counts)) * PREFILL_TILE
-    return seq.astype(np.int32), q0.astype(np.int32)
+    base = np.zeros(lens.size, np.int64) if past is None else np.asarray(past, dtype=np.int64)
+    key_end = base[seq] + np.minimum(q0 + PREFILL_TILE, lens[seq])
+    order = np.argsort(-key_end, kind="stable")
+    return seq[order].astype(np.int32), q0[order].astype(np.int32)
 
 
 def prefill_attention_raw(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor,

@@ -121,3 +121,21 @@ def test_slot_resolution_rules() -> None:
     with pytest.raises(ValueError):
         resolve_kv_slots_per_layer("first_then_shared", total_recurrent_steps=4, requested_slots=5)
     assert [kv_slot_for_step(s, policy="first_then_shared", slots_per_layer=3) for s in range(5)] == [0, 1, 2, 2, 2]
+
+
+def test_prefill_tiles_cover_every_query_tile_once_longest_prefix_first() -> None:
+    import numpy as np
+
+    from continuous_depth_batching_amd import ops
+
+    lens = np.array([130, 1, 64, 65, 0, 300])
+    past = np.array([0, 500, 10, 0, 7, 64])
+    seq, q0 = ops.prefill_tiles(lens, past)
+    tiles = sorted(zip(seq.tolist(), q0.tolist()))
+    want = sorted((s, t) for s, n in enumerate(lens.tolist()) for t in range(0, n, ops.PREFILL_TILE))
+    assert tiles == want
+    key_end = past[seq] + np.minimum(q0 + ops.PREFILL_TILE, lens[seq])
+    assert (np.diff(key_end) <= 0).all()
+    # Without past lengths the prefixes are the query positions alone.
+    seq0, q00 = ops.prefill_tiles(lens)
+    assert sorted(zip(seq0.tolist(), q00.tolist())) == want

@@ -248,7 +248,7 @@ def test_rope_kv_write_and_prefill_attention(dtype: str, head_dim: int, heads: i
                           dev(positions), dev(cos), dev(sin), style, None, None)
     np.testing.assert_array_equal(host(qo), q_rot)
     np.testing.assert_array_equal(host(pt), want_pool)
-    tile_seq, tile_q0 = ops.prefill_tiles(lens)
+    tile_seq, tile_q0 = ops.prefill_tiles(lens, pasts)
     out = torch.empty_like(qo)
     ops.prefill_attention_raw(qo, view, layer, dev(table), dev(np.arange(4, dtype=np.int32)), dev(cu),
                               dev(pasts.astype(np.int32)), dev(tile_seq), dev(tile_q0), out, head_dim ** -0.5)

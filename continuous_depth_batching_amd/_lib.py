@@ -79,7 +79,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_int64, c_int32, _P, c_int64,  # layer_stride, layer, rows, pool_rows
             _P, _P, _P, c_int32, c_int32,  # positions, rope_cos, rope_sin, rope_style, max_positions
             _P, _P, c_int64,  # q_bias, k_bias, tokens
-            c_int32, c_int32, c_int32, c_int32, _P,  # H, Hkv, D, dtype, stream
+            c_int32, c_int32, c_int32, c_int64, c_int64,  # H, Hkv, D, q_stride, kv_stride
+            c_int32, _P,  # dtype, stream
         ],
     ),
     "cdb_prefill_attention": (

@@ -462,6 +462,7 @@ struct RopeWriteParams {
   const void* k_bias;
   int64_t tokens;
   int64_t pool_rows;
+  int64_t q_stride, kv_stride;  // elements between consecutive tokens of q and of k / v
   int32_t layer;
   int32_t num_heads, num_kv_heads, rope_style, max_positions;
 };
@@ -532,7 +533,7 @@ __global__ void __launch_bounds__(kThreads) rope_kv_write_kernel(RopeWriteParams
   if (hh < P.num_heads) {
     const int h = hh;
     float o[C];
-    const T* src = static_cast<const T*>(P.q) + (t * P.num_heads + h) * D;
+    const T* src = static_cast<const T*>(P.q) + t * P.q_stride + (int64_t)h * D;
     T* dst = static_cast<T*>(P.q_out) + (t * P.num_heads + h) * D + chunk * C;
     Vec<T, C> ov;
     if (rope_ok) {
@@ -550,7 +551,7 @@ __global__ void __launch_bounds__(kThreads) rope_kv_write_kernel(RopeWriteParams
   const int64_t row = P.rows[t];
   if (row < 0 || row >= P.pool_rows || !rope_ok) return;
   float o[C];
-  rotate_chunk<T, D>(P, static_cast<const T*>(P.k) + (t * P.num_kv_heads + kvh) * D,
+  rotate_chunk<T, D>(P, static_cast<const T*>(P.k) + t * P.kv_stride + (int64_t)kvh * D,
                      P.k_bias ? static_cast<const T*>(P.k_bias) + (int64_t)kvh * D : nullptr, pos, chunk, o);
   const int64_t off = (int64_t)P.layer * P.layer_stride + (row * P.num_kv_heads + kvh) * D + chunk * C;
   Vec<T, C> kw;
@@ -558,7 +559,7 @@ __global__ void __launch_bounds__(kThreads) rope_kv_write_kernel(RopeWriteParams
   for (int i = 0; i < C; ++i) kw.set(i, o[i]);
   kw.store(static_cast<T*>(P.k_pool) + off);
   Vec<T, C> vv;
-  vv.load(static_cast<const T*>(P.v) + (t * P.num_kv_heads + kvh) * D + chunk * C);
+  vv.load(static_cast<const T*>(P.v) + t * P.kv_stride + (int64_t)kvh * D + chunk * C);
   vv.store(static_cast<T*>(P.v_pool) + off);
 }
 
@@ -743,14 +744,19 @@ int cdb_rope_kv_write(const void* q, const void* k, const void* v, void* q_out, 
                       int64_t layer_stride, int32_t layer, const int64_t* rows, int64_t pool_rows,
                       const int32_t* positions, const float* rope_cos, const float* rope_sin, int32_t rope_style,
                       int32_t max_positions, const void* q_bias, const void* k_bias, int64_t tokens,
-                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype, hipStream_t stream) {
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_stride, int64_t kv_stride,
+                      int32_t dtype, hipStream_t stream) {
   if (tokens == 0) return CDB_OK;
   if (!q || !k || !v || !q_out || !k_pool || !v_pool || !rows || !positions) return CDB_ERR_NULL;
   if (rope_style < 0 || rope_style > 2) return CDB_ERR_SHAPE;
   if (rope_style && (!rope_cos || !rope_sin)) return CDB_ERR_NULL;
   if (tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || layer < 0 || pool_rows <= 0) return CDB_ERR_SHAPE;
+  if (q_stride <= 0) q_stride = (int64_t)num_heads * head_dim;
+  if (kv_stride <= 0) kv_stride = (int64_t)num_kv_heads * head_dim;
+  if (q_stride < (int64_t)num_heads * head_dim || kv_stride < (int64_t)num_kv_heads * head_dim) return CDB_ERR_SHAPE;
   RopeWriteParams P{q, k, v, q_out, k_pool, v_pool, layer_stride, rows, positions, rope_cos, rope_sin, q_bias,
-                    k_bias, tokens, pool_rows, layer, num_heads, num_kv_heads, rope_style, max_positions};
+                    k_bias, tokens, pool_rows, q_stride, kv_stride, layer, num_heads, num_kv_heads, rope_style,
+                    max_positions};
   auto by_dim = [&](auto tag) -> int {
     using T = decltype(tag);
     switch (head_dim) {

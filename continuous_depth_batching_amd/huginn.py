@@ -379,8 +379,8 @@ class HuginnCDBAdapter(CDBModelAdapter):
 
         def attend(i: int, w: dict, qkv: torch.Tensor) -> torch.Tensor:
             layer = layer_of(i)
-            q, k, v = self._split_qkv(qkv, contiguous=True)
-            q_rot = torch.empty_like(q)
+            q, k, v = self._split_qkv(qkv)  # strided column slices: the kernel reads them in place
+            q_rot = torch.empty(q.shape, dtype=q.dtype, device=q.device)
             ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
                                   self.rope_cos, self.rope_sin, ROPE_INTERLEAVED, w["q_bias"], w["k_bias"])
             out = torch.empty_like(q_rot)

@@ -734,7 +734,10 @@ def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: 
                       layer: int, rows: torch.Tensor, positions: torch.Tensor, rope_cos: torch.Tensor | None,
                       rope_sin: torch.Tensor | None, rope_style: int, q_bias: torch.Tensor | None,
                       k_bias: torch.Tensor | None) -> None:
-    """Rotate q/k of T tokens, write k/v to pool rows of cache layer ``layer`` (no allocation)."""
+    """Rotate q/k of T tokens, write k/v to pool rows of cache layer ``layer`` (no allocation).
+
+    q, k and v may be token-strided views (e.g. column slices of a fused QKV output)
+    whose [heads, head_dim] part is dense; k and v must share one token stride."""
 
     tokens, num_heads, head_dim = q.shape
     num_kv_heads = k.shape[1]
@@ -744,13 +747,18 @@ def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: 
         raise TypeError("rows int64 and positions int32 with a slot per token expected")
     if not 0 <= layer < view.num_cache_layers:
         raise ValueError("layer out of range")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.stride(2) != 1 or t.stride(1) != head_dim:
+            raise ValueError(f"{name} must be dense within a token ([heads, head_dim] contiguous)")
+    if k.stride(0) != v.stride(0):
+        raise ValueError("k and v must share one token stride")
     _require_cuda(q, k, v, q_out, rows, positions, rope_cos, rope_sin)
-    _require_contiguous(q=q, k=k, v=v, q_out=q_out, rows=rows, positions=positions)
+    _require_contiguous(q_out=q_out, rows=rows, positions=positions)
     code = _lib.lib().cdb_rope_kv_write(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), q_out.data_ptr(), view.k_ptr, view.v_ptr, view.layer_stride,
         layer, rows.data_ptr(), view.pool_rows, positions.data_ptr(), _ptr(rope_cos), _ptr(rope_sin), rope_style,
         0 if rope_cos is None else rope_cos.shape[0], _ptr(q_bias), _ptr(k_bias), tokens, num_heads,
-        num_kv_heads, head_dim, dtype_code(q.dtype), _stream())
+        num_kv_heads, head_dim, q.stride(0), k.stride(0), dtype_code(q.dtype), _stream())
     _lib.check(code, "cdb_rope_kv_write")
 
 

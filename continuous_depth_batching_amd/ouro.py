@@ -339,10 +339,11 @@ class OuroCDBAdapter(CDBModelAdapter):
 
             def attend(li: int, qkv: torch.Tensor, ut: int = ut) -> torch.Tensor:
                 layer = layout.core_layer_index(li, ut)
-                q = qkv[:, :q_w].contiguous().view(tokens, self.num_heads, hd)
-                k = qkv[:, q_w:q_w + kv_w].contiguous().view(tokens, self.num_kv_heads, hd)
-                v = qkv[:, q_w + kv_w:].contiguous().view(tokens, self.num_kv_heads, hd)
-                q_rot = torch.empty_like(q)
+                # Strided column slices of the fused QKV output: no split copies.
+                q = qkv[:, :q_w].view(tokens, self.num_heads, hd)
+                k = qkv[:, q_w:q_w + kv_w].view(tokens, self.num_kv_heads, hd)
+                v = qkv[:, q_w + kv_w:].view(tokens, self.num_kv_heads, hd)
+                q_rot = torch.empty((tokens, self.num_heads, hd), dtype=qkv.dtype, device=qkv.device)
                 ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
                                       self.rope_cos, self.rope_sin, 1, None, None)
                 out = torch.empty_like(q_rot)

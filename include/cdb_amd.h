@@ -162,12 +162,15 @@ int cdb_exit_kv_copy(void* k_pool, void* v_pool, int64_t layer_stride, int64_t p
  * rotate(k [+ k_bias]) and v are written to cache layer `layer` at pool rows
  * rows[t] (negative rows write nothing). Replaces the write half of
  * PagedAttentionCache.update (continuous_batching/cache.py:284-318) and the
- * RoPE before it. */
+ * RoPE before it. q, k and v may be column slices of one fused QKV output:
+ * q_stride / kv_stride are the elements between consecutive tokens (0: dense
+ * [T, H, D] / [T, Hkv, D]); q_out is dense. */
 int cdb_rope_kv_write(const void* q, const void* k, const void* v, void* q_out, void* k_pool, void* v_pool,
                       int64_t layer_stride, int32_t layer, const int64_t* rows, int64_t pool_rows,
                       const int32_t* positions, const float* rope_cos, const float* rope_sin, int32_t rope_style,
                       int32_t max_positions, const void* q_bias, const void* k_bias, int64_t tokens,
-                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype, hipStream_t stream);
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int64_t q_stride, int64_t kv_stride,
+                      int32_t dtype, hipStream_t stream);
 
 /* Varlen causal prefill attention over the paged pool on MFMA tiles.
  * Replaces flash_attn_varlen_func as the reference's prefill calls it after

@@ -248,6 +248,18 @@ def test_rope_kv_write_and_prefill_attention(dtype: str, head_dim: int, heads: i
                           dev(positions), dev(cos), dev(sin), style, None, None)
     np.testing.assert_array_equal(host(qo), q_rot)
     np.testing.assert_array_equal(host(pt), want_pool)
+    # The same write from column slices of one fused [T, (H + 2 Hkv) * D] QKV buffer (the
+    # models' layout) reads the tokens in place and must give the same bits.
+    fused = torch.cat([dev(q, DT[dtype]).reshape(T, -1), dev(k, DT[dtype]).reshape(T, -1),
+                       dev(v, DT[dtype]).reshape(T, -1)], dim=1)
+    qw, kw = heads * head_dim, kv_heads * head_dim
+    pt2 = dev(pool, DT[dtype]).contiguous()
+    qo2 = torch.empty_like(qo)
+    ops.rope_kv_write_raw(fused[:, :qw].view(T, heads, head_dim), fused[:, qw:qw + kw].view(T, kv_heads, head_dim),
+                          fused[:, qw + kw:].view(T, kv_heads, head_dim), qo2, ops.KVPoolView(pt2, bs), layer,
+                          dev(wrows), dev(positions), dev(cos), dev(sin), style, None, None)
+    torch.cuda.synchronize()
+    assert torch.equal(qo2, qo) and torch.equal(pt2, pt)
     tile_seq, tile_q0 = ops.prefill_tiles(lens, pasts)
     out = torch.empty_like(qo)
     ops.prefill_attention_raw(qo, view, layer, dev(table), dev(np.arange(4, dtype=np.int32)), dev(cu),

@@ -547,11 +547,11 @@ int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
                  : launch_linear_wide<2, 1, 4, 4, false, 64>(prm, stream);
   }
   if (prm.M <= 128) {
-    return gated ? launch_linear_wide<4, 1, 4, 2, true, 64>(prm, stream)
-                 : launch_linear_wide<2, 2, 4, 4, false, 64>(prm, stream);
+    return gated ? launch_linear_wide<4, 1, 2, 4, true, 64>(prm, stream)
+                 : launch_linear_wide<4, 1, 2, 4, false, 64>(prm, stream);
   }
-  return gated ? launch_linear_wide<4, 2, 2, 4, true, 64>(prm, stream)
-               : launch_linear_wide<4, 2, 4, 2, false, 64>(prm, stream);
+  return gated ? launch_linear_wide<8, 1, 2, 4, true, 64>(prm, stream)
+               : launch_linear_wide<4, 2, 2, 4, false, 64>(prm, stream);
 }
 
 // Split-K form: 2048- and 5632-wide inputs into outputs of a multiple of 64

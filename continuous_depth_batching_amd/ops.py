@@ -539,21 +539,31 @@ def _(x, weight, packed, residual, w_a, w_b, eps_a, eps_b, mode):
 
 def copy_rows_raw(src: torch.Tensor, src_index: torch.Tensor | None, dst: torch.Tensor,
                   dst_index: torch.Tensor | None, rows: int) -> None:
-    """dst[dst_index[i]] = src[src_index[i]] over whole rows of the first dimension (no allocation)."""
+    """dst[dst_index[i]] = src[src_index[i]] over whole rows of the first dimension (no allocation).
 
-    if src.dtype != dst.dtype or src.shape[1:] != dst.shape[1:]:
+    Called several times per scheduler tick, so the checks touch each tensor
+    property once (dtypes are singletons, compared by identity)."""
+
+    shape = src.shape
+    n_src, n_dst = shape[0], dst.shape[0]
+    if src.dtype is not dst.dtype or shape[1:] != dst.shape[1:]:
         raise ValueError("src and dst rows must have the same shape and dtype")
-    for name, idx in (("src_index", src_index), ("dst_index", dst_index)):
-        if idx is not None and (idx.dtype != torch.int64 or idx.numel() < rows):
-            raise ValueError(f"{name} must be int64 with at least {rows} entries")
-    if src_index is None and src.shape[0] < rows or dst_index is None and dst.shape[0] < rows:
-        raise ValueError("identity index needs at least `rows` rows")
-    _require_cuda(src, dst, src_index, dst_index)
-    _require_contiguous(src=src, dst=dst, src_index=src_index, dst_index=dst_index)
-    row_bytes = src[0].numel() * src.element_size() if src.shape[0] else 0
-    _lib.check(_lib.lib().cdb_copy_rows(src.data_ptr(), _ptr(src_index), src.shape[0], dst.data_ptr(),
-                                        _ptr(dst_index), dst.shape[0], rows, row_bytes, _stream()),
-               "cdb_copy_rows")
+    for name, idx, n in (("src_index", src_index, n_src), ("dst_index", dst_index, n_dst)):
+        if idx is None:
+            if n < rows:
+                raise ValueError("identity index needs at least `rows` rows")
+        elif idx.dtype is not torch.int64 or idx.numel() < rows or not idx.is_contiguous() or not idx.is_cuda:
+            raise ValueError(f"{name} must be a contiguous CUDA int64 tensor with at least {rows} entries")
+    if not (src.is_cuda and dst.is_cuda):
+        raise RuntimeError("CDB kernels run on the GPU only; got a tensor on the CPU")
+    if not (src.is_contiguous() and dst.is_contiguous()):
+        raise ValueError("src and dst must be contiguous")
+    row_bytes = src.numel() // n_src * src.element_size() if n_src else 0
+    code = _lib.lib().cdb_copy_rows(src.data_ptr(), None if src_index is None else src_index.data_ptr(), n_src,
+                                    dst.data_ptr(), None if dst_index is None else dst_index.data_ptr(), n_dst, rows,
+                                    row_bytes, _stream())
+    if code:
+        _lib.check(code, "cdb_copy_rows")
 
 
 def gather_rows_raw(src: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
@@ -620,13 +630,21 @@ def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor |
 
     rows, in_features = x.shape
     vocab = weight.shape[0]
-    if (packed is not None and x.dtype == torch.bfloat16 and 1 <= rows <= LINEAR_MAX_ROWS
+    if (packed is not None and x.dtype is torch.bfloat16 and 1 <= rows <= LINEAR_MAX_ROWS
             and linear_prefers_kernel(rows, vocab, False, in_features) and vocab % 16 == 0
-            and in_features % 32 == 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0):
-        out = torch.empty((rows,), dtype=torch.int64, device=x.device)
-        workspace = torch.empty((rows * (vocab // 16) * 2,), dtype=torch.float32, device=x.device)
-        linear_argmax_raw(x, packed, out, workspace)
-        return out
+            and in_features % 32 == 0 and packed.numel() == vocab * in_features and packed.dtype is torch.bfloat16
+            and x.is_cuda and packed.is_cuda and packed.is_contiguous()):
+        stride = x.stride()
+        ptr = x.data_ptr()
+        if stride[1] == 1 and stride[0] % 8 == 0 and ptr % 16 == 0:
+            out = torch.empty((rows,), dtype=torch.int64, device=x.device)
+            workspace = torch.empty((rows * (vocab // 16) * 2,), dtype=torch.float32, device=x.device)
+            code = _lib.lib().cdb_linear_argmax(ptr, stride[0], packed.data_ptr(), out.data_ptr(),
+                                                workspace.data_ptr(), workspace.numel() * 4, rows, vocab,
+                                                in_features, _lib.CDB_DTYPE_BF16, _stream())
+            if code:
+                _lib.check(code, "cdb_linear_argmax")
+            return out
     return argmax_rows(linear_auto(x, weight, packed, False))
 
 

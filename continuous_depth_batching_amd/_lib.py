@@ -106,7 +106,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int32,
         [
             _P, c_int64, _P, _P, _P, c_int64,  # x, ldx, w_packed, out, workspace, workspace_bytes
-            c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, dtype, stream
+            c_int32, c_int32, c_int32,  # rows, out_features, in_features
+            _P, _P, c_int64, _P, c_int32,  # embed, bank, bank_rows, bank_slots, width
+            c_int32, _P,  # dtype, stream
         ],
     ),
     "cdb_linear_parts": (

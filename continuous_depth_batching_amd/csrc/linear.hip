@@ -427,12 +427,24 @@ __global__ void __launch_bounds__(256) linear_pack_kernel(const bf16_t* w, int64
 constexpr int kArgmaxMergeThreads = 256;
 constexpr int kArgmaxMergeVecs = 4;  // 16-byte vectors (4 candidates) per thread per batch
 
+// With an embedding table, a row whose bank_slots entry is >= 0 also has the
+// embedding row of its token copied to that hidden-bank row: the next token's
+// prelude (an embedding lookup) fused into the coda.
+struct ArgmaxEmbed {
+  const bf16_t* embed;       // [embed_rows, width] or null
+  bf16_t* bank;              // [bank_rows, width]
+  const int64_t* bank_slots; // [rows]; < 0: no successor
+  int64_t embed_rows, bank_rows;
+  int32_t width;
+};
+
 __global__ void __launch_bounds__(kArgmaxMergeThreads) linear_argmax_merge_kernel(const float* best_val,
                                                                                   const int32_t* best_idx,
                                                                                   int32_t tiles, int64_t* out,
-                                                                                  int32_t rows) {
+                                                                                  int32_t rows, ArgmaxEmbed E) {
   __shared__ float sv[kArgmaxMergeThreads / kWave];
   __shared__ int si[kArgmaxMergeThreads / kWave];
+  __shared__ int token_lds;
   const int row = blockIdx.x;
   if (row >= rows) return;
   const float* v = best_val + (int64_t)row * tiles;
@@ -478,7 +490,17 @@ __global__ void __launch_bounds__(kArgmaxMergeThreads) linear_argmax_merge_kerne
     for (int w = 1; w < kArgmaxMergeThreads / kWave; ++w)
       if (argmax_better(sv[w], si[w], best, bi)) { best = sv[w]; bi = si[w]; }
     out[row] = bi;
+    token_lds = bi;
   }
+  if (E.embed == nullptr) return;
+  const int64_t slot = E.bank_slots[row];
+  if (slot < 0 || slot >= E.bank_rows) return;  // block-uniform
+  __syncthreads();
+  const int64_t token = token_lds;
+  if (token < 0 || token >= E.embed_rows) return;
+  const uint4* src = reinterpret_cast<const uint4*>(E.embed + token * E.width);
+  uint4* dst = reinterpret_cast<uint4*>(E.bank + slot * E.width);
+  for (int v = threadIdx.x; v < E.width / 8; v += kArgmaxMergeThreads) dst[v] = src[v];
 }
 
 // Launch shape of one instantiation: threads per workgroup are capped so the
@@ -664,8 +686,12 @@ extern "C" int64_t cdb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_f
 
 extern "C" int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int64_t* out, void* workspace,
                                  int64_t workspace_bytes, int32_t rows, int32_t out_features, int32_t in_features,
-                                 int32_t dtype, hipStream_t stream) {
+                                 const void* embed, void* bank, int64_t bank_rows, const int64_t* bank_slots,
+                                 int32_t width, int32_t dtype, hipStream_t stream) {
   if (!x || !w_packed || !out || !workspace) return CDB_ERR_NULL;
+  if (embed && (!bank || !bank_slots)) return CDB_ERR_NULL;
+  if (embed && (width <= 0 || width % 8 || bank_rows <= 0 || ((uintptr_t)embed & 15) || ((uintptr_t)bank & 15)))
+    return CDB_ERR_SHAPE;
   if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
   if (rows < 1 || rows > kLinearMaxRows || out_features < 16 || out_features % 16 || in_features < 32 ||
       in_features % 32 || ldx < in_features || ldx % 8)
@@ -696,7 +722,9 @@ extern "C" int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packe
   else
     rc = two ? launch_linear<4, 2, 2, false, true>(prm, stream, 4) : launch_linear<4, 1, 2, false, true>(prm, stream, 4);
   if (rc != CDB_OK) return rc;
+  ArgmaxEmbed emb{static_cast<const bf16_t*>(embed), static_cast<bf16_t*>(bank), bank_slots, out_features,
+                  bank_rows, width};
   hipLaunchKernelGGL(linear_argmax_merge_kernel, dim3((unsigned)rows), dim3(kArgmaxMergeThreads), 0, stream,
-                     prm.best_val, prm.best_idx, tiles, out, rows);
+                     prm.best_val, prm.best_idx, tiles, out, rows, emb);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }

@@ -429,25 +429,40 @@ class ContinuousDepthBatchingEngine:
         items = self._drop_cancelled_items(items)
         if not items:
             return
-        pending = self.runner.stage_coda_batch(items, allow_async=self.cdb_config.use_async_batching)
+        use_async = self.cdb_config.use_async_batching
+        selected: list[tuple[list[DepthWorkItem], list[int], list[bool]]] = []
+
+        def successors(coda_items: list[DepthWorkItem]) -> tuple[list[DepthWorkItem], list[int]]:
+            # Runs once the coda's tokens count as in flight, before the coda launch,
+            # so the runner can fuse the successors' prelude into it.
+            eager_items, eager_rows, flags = self._select_eager_reentries(coda_items)
+            selected.append((eager_items, eager_rows, flags))
+            if eager_items:
+                self._record_prelude("after_coda_eager", len(eager_items), gathered=len(eager_items))
+            return eager_items, eager_rows
+
+        pending = self.runner.stage_coda_batch(items, allow_async=use_async,
+                                               successors=successors if use_async else None)
         if self.record_launches:
             self.launch_log.append(LaunchRecord("coda", [i.state.request_id for i in items],
                                                 [i.token_position for i in items]))
-        if self.cdb_config.use_async_batching:
-            eager_items, eager_rows = self._select_eager_reentries(pending)
-            if eager_items:
-                self._record_prelude("after_coda_eager", len(eager_items), gathered=len(eager_items))
-                self.runner.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
+        if use_async:
+            eager_items, _, flags = selected[0]
+            pending.eager_reentries = flags
             self._enqueue_prelude_items(eager_items, front=True)
         self.pending_coda_results.append(pending)
         self.last_stats.max_pending_coda_results = max(self.last_stats.max_pending_coda_results,
                                                        len(self.pending_coda_results))
 
-    def _select_eager_reentries(self, pending: PendingCodaResult) -> tuple[list[DepthWorkItem], list[int]]:
-        flags = [False] * len(pending.items)
+    def _select_eager_reentries(self, coda_items: list[DepthWorkItem]
+                                ) -> tuple[list[DepthWorkItem], list[int], list[bool]]:
+        """Successors staged ahead of their token (cdb/continuous_api.py:1304-1327): every coda
+        row whose request will not finish on the pending token and gets a KV slot."""
+
+        flags = [False] * len(coda_items)
         items: list[DepthWorkItem] = []
         rows: list[int] = []
-        for idx, item in enumerate(pending.items):
+        for idx, item in enumerate(coda_items):
             state = item.state
             if state.will_finish_on_pending_token():
                 continue
@@ -458,8 +473,7 @@ class ContinuousDepthBatchingEngine:
             flags[idx] = True
             items.append(self._build_decode_item(state, token_id=TMP_TOKEN_ID))
             rows.append(idx)
-        pending.eager_reentries = flags
-        return items, rows
+        return items, rows, flags
 
     def _consume_ready_coda_results(self, *, block: bool) -> None:
         while self.pending_coda_results:

@@ -72,6 +72,9 @@ class StageLaunch:
     cache: PagedKVCache | None = None
     workspace: torch.Tensor | None = None      # decode-attention workspace
     split_pages: int = 0
+    # Coda only, with coda_writes_successor_prelude: [n] int64 bank slots of the rows'
+    # eager successors (-1: none), whose prelude the coda runs on its greedy token.
+    successor_slots: torch.Tensor | None = None
 
 
 @dataclass
@@ -94,6 +97,10 @@ class CDBModelAdapter(ABC):
     """Model-specific stage kernels used by the CDB runner."""
 
     stages_use_attention: bool = False
+    # The coda can also run the prelude of the rows' next tokens (an embedding lookup of
+    # the greedy token into launch.successor_slots), so eager re-entries need no prelude
+    # launch of their own (cdb/model_runner.py:439-457 gathers those tokens on device).
+    coda_writes_successor_prelude: bool = False
 
     @property
     @abstractmethod

@@ -21,7 +21,7 @@ from __future__ import annotations
 import gc
 from contextlib import contextmanager, nullcontext
 from dataclasses import dataclass, field
-from typing import Any, Iterator, Sequence
+from typing import Any, Callable, Iterator, Sequence
 
 import numpy as np
 import torch
@@ -442,23 +442,51 @@ class ModelRunner:
         self.recurrent_graph_captures += 1
 
     # -- coda --------------------------------------------------------------------------------------------------
-    def stage_coda_batch(self, items: list[DepthWorkItem], *, allow_async: bool = True) -> PendingCodaResult:
+    def stage_coda_batch(self, items: list[DepthWorkItem], *, allow_async: bool = True,
+                         successors: Callable[[list[DepthWorkItem]], tuple[list[DepthWorkItem], list[int]]] | None = None
+                         ) -> PendingCodaResult:
+        """Greedy next tokens of ``items`` (cdb/model_runner.py:1036-1125).
+
+        ``successors``, once the items' tokens count as in flight, names the eager
+        re-entries: (successor items with placeholder tokens, the coda rows they follow).
+        Their prelude runs on the device tokens -- inside the coda launch when the
+        adapter can fuse it, else as a prelude gathering from this result."""
+
         if not items:
             return PendingCodaResult(items=[], host_tokens=torch.empty(0, dtype=torch.int64))
         for item in items:
             item.state.tokens_in_flight += 1
         n = len(items)
+        eager_items, eager_rows = successors(items) if successors is not None else ([], [])
+        fused = bool(eager_items) and self.adapter.coda_writes_successor_prelude
+        upload = np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n)
+        if fused:
+            new_slots = self.allocate_hidden_slots(len(eager_items))
+            successor = np.full(n, -1, dtype=np.int64)
+            successor[eager_rows] = new_slots
+            # One upload: [coda rows' slots | each row's successor slot or -1 | the successors' slots].
+            upload = np.concatenate([upload, successor, np.asarray(new_slots, dtype=np.int64)])
         with self._on_stream():
-            slots = self._to_device(np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n),
-                                    torch.int64)
-            tokens = self.adapter.coda(self._stage_launch(items, slots))
+            dev = self._to_device(upload, torch.int64)
+            launch = self._stage_launch(items, dev[:n])
+            if fused:
+                launch.successor_slots = dev[n:2 * n]
+            tokens = self.adapter.coda(launch)
             host = self._pinned((n,), torch.int64)
             host.copy_(tokens, non_blocking=True)
             event = torch.cuda.Event()
             event.record()
+            if fused:
+                self.gate_state.reset(dev[2 * n:], len(eager_items))
+        pending = PendingCodaResult(items=items, host_tokens=host, device_tokens=tokens, ready_event=event)
+        if fused:
+            for item, slot in zip(eager_items, new_slots):
+                item.hidden_slot = slot
+        elif eager_items:
+            self.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
         if not allow_async:
             event.synchronize()
-        return PendingCodaResult(items=items, host_tokens=host, device_tokens=tokens, ready_event=event)
+        return pending
 
     def consume_coda_result(self, pending: PendingCodaResult) -> list[int]:
         if pending.ready_event is not None:

@@ -603,8 +603,31 @@ def argmax_raw(logits: torch.Tensor, out: torch.Tensor) -> None:
                                      _stream()), "cdb_argmax")
 
 
-def linear_argmax_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor) -> None:
-    """out[r] = argmax_n of the bf16 logits x @ W.T (torch.argmax order), the logits never stored."""
+def _successor_embed_args(embed: torch.Tensor | None, bank: torch.Tensor | None, bank_slots: torch.Tensor | None,
+                          rows: int) -> tuple:
+    """(embed, bank, bank_rows, bank_slots, width) arguments of cdb_linear_argmax's fused prelude."""
+
+    if embed is None:
+        return None, None, 0, None, 0
+    if bank is None or bank_slots is None:
+        raise ValueError("the fused prelude needs the bank and the successors' bank slots")
+    width = embed.shape[1]
+    if (embed.dtype is not torch.bfloat16 or bank.dtype is not torch.bfloat16 or bank.dim() != 2
+            or bank.shape[1] != width or not embed.is_contiguous() or not bank.is_contiguous()):
+        raise ValueError("embed and bank must be contiguous bf16 [rows, width] tables of one width")
+    if bank_slots.dtype is not torch.int64 or bank_slots.numel() < rows or not bank_slots.is_contiguous():
+        raise ValueError(f"bank_slots must be a contiguous int64 tensor with at least {rows} entries")
+    _require_cuda(embed, bank, bank_slots)
+    return embed.data_ptr(), bank.data_ptr(), bank.shape[0], bank_slots.data_ptr(), width
+
+
+def linear_argmax_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, workspace: torch.Tensor,
+                      embed: torch.Tensor | None = None, bank: torch.Tensor | None = None,
+                      bank_slots: torch.Tensor | None = None) -> None:
+    """out[r] = argmax_n of the bf16 logits x @ W.T (torch.argmax order), the logits never stored.
+
+    With ``embed``: bank[bank_slots[r]] = embed[out[r]] for rows whose slot is >= 0
+    (the successor's prelude fused into the coda)."""
 
     _require_cuda(x, packed, out, workspace)
     rows, in_features = x.shape
@@ -616,17 +639,23 @@ def linear_argmax_raw(x: torch.Tensor, packed: torch.Tensor, out: torch.Tensor, 
                          f"out of {out.numel()} int64")
     if x.stride(1) != 1 or not packed.is_contiguous() or not out.is_contiguous() or not workspace.is_contiguous():
         raise ValueError("x must have unit stride along its last dimension; weight, out and workspace are dense")
+    emb = _successor_embed_args(embed, bank, bank_slots, rows)
     _lib.check(_lib.lib().cdb_linear_argmax(x.data_ptr(), x.stride(0), packed.data_ptr(), out.data_ptr(),
                                             workspace.data_ptr(), workspace.numel() * workspace.element_size(),
-                                            rows, out_features, in_features, _lib.CDB_DTYPE_BF16, _stream()),
+                                            rows, out_features, in_features, *emb, _lib.CDB_DTYPE_BF16, _stream()),
                "cdb_linear_argmax")
 
 
-def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None) -> torch.Tensor:
+def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None,
+                   embed: torch.Tensor | None = None, bank: torch.Tensor | None = None,
+                   bank_slots: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy tokens of a coda batch: argmax over the vocabulary of x @ weight.T.
 
     Batches the projection kernel serves (linear_prefers_kernel) run the fused
-    cdb_linear_argmax; others compute the logits (torch.mm) and cdb_argmax them."""
+    cdb_linear_argmax; others compute the logits (torch.mm) and cdb_argmax them.
+    With ``embed``, rows whose ``bank_slots`` entry is >= 0 also get the embedding
+    of their token written to that bank row (the next token's prelude): inside the
+    fused call, or as one row copy after the unfused one."""
 
     rows, in_features = x.shape
     vocab = weight.shape[0]
@@ -639,13 +668,17 @@ def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor |
         if stride[1] == 1 and stride[0] % 8 == 0 and ptr % 16 == 0:
             out = torch.empty((rows,), dtype=torch.int64, device=x.device)
             workspace = torch.empty((rows * (vocab // 16) * 2,), dtype=torch.float32, device=x.device)
+            emb = _successor_embed_args(embed, bank, bank_slots, rows)
             code = _lib.lib().cdb_linear_argmax(ptr, stride[0], packed.data_ptr(), out.data_ptr(),
                                                 workspace.data_ptr(), workspace.numel() * 4, rows, vocab,
-                                                in_features, _lib.CDB_DTYPE_BF16, _stream())
+                                                in_features, *emb, _lib.CDB_DTYPE_BF16, _stream())
             if code:
                 _lib.check(code, "cdb_linear_argmax")
             return out
-    return argmax_rows(linear_auto(x, weight, packed, False))
+    tokens = argmax_rows(linear_auto(x, weight, packed, False))
+    if embed is not None:
+        copy_rows_raw(embed, tokens, bank, bank_slots, rows)
+    return tokens
 
 
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:

@@ -182,6 +182,8 @@ def rope_tables(head_dim: int, theta: float, max_positions: int, dtype: torch.dt
 class OuroCDBAdapter(CDBModelAdapter):
     """Stage kernels for Ouro; weights are packed once (fused QKV and gate/up)."""
 
+    coda_writes_successor_prelude = True  # the prelude is the embedding lookup the coda can fuse
+
     def __init__(self, model: nn.Module, *, max_positions: int | None = None) -> None:
         self.model = model
         self.decoder = model.get_decoder() if hasattr(model, "get_decoder") else model.model
@@ -359,9 +361,14 @@ class OuroCDBAdapter(CDBModelAdapter):
         return ops.lm_head_argmax(hidden, self.lm_head_w, self.lm_head_p)
 
     def coda(self, launch: StageLaunch) -> torch.Tensor:
-        # Eager, once per coda tick: direct calls rather than op dispatch.
+        # Eager, once per coda tick: direct calls rather than op dispatch. Rows with an
+        # eager successor also get its prelude -- the embedding of the greedy token in
+        # the successor's bank slot -- from the same launch.
         hidden = ops.gather_rows_raw(launch.bank, launch.slots[:launch.n])
-        return self.coda_from_hidden(hidden)
+        if launch.successor_slots is None:
+            return self.coda_from_hidden(hidden)
+        return ops.lm_head_argmax(hidden, self.lm_head_w, self.lm_head_p, embed=self.embed, bank=launch.bank,
+                                  bank_slots=launch.successor_slots)
 
 
 __all__ = ["OuroConfig", "OuroForCausalLM", "OuroCDBAdapter", "build_ouro", "init_ouro_weights", "rope_tables",

@@ -243,9 +243,16 @@ int64_t cdb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_features);
  * combines them. bf16, w packed by cdb_linear_pack_weight, 1 <= rows <= 64,
  * out_features a multiple of 16, in_features a multiple of 32, ldx a multiple
  * of 8; workspace 16-byte aligned, at least cdb_linear_argmax_workspace_bytes
- * bytes (CDB_ERR_CAPACITY otherwise). */
+ * bytes (CDB_ERR_CAPACITY otherwise).
+ * With embed non-null ([out_features, width] bf16, the token embedding) the
+ * same call also runs the next token's prelude for rows with a successor:
+ * bank[bank_slots[r]] = embed[out[r]] when 0 <= bank_slots[r] < bank_rows --
+ * the eager re-entry's embedding lookup (cdb/model_runner.py:439-457,
+ * cdb/adapters/ouro.py:199-212) fused into the coda. embed and bank 16-byte
+ * aligned, width a multiple of 8. */
 int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int64_t* out, void* workspace,
                       int64_t workspace_bytes, int32_t rows, int32_t out_features, int32_t in_features,
+                      const void* embed, void* bank, int64_t bank_rows, const int64_t* bank_slots, int32_t width,
                       int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus

@@ -185,14 +185,18 @@ class HostLoopRunner(ModelRunner):
             return can_exit and state[0] >= p.threshold
         return can_exit and signal < p.threshold
 
-    def stage_coda_batch(self, items, *, allow_async: bool = True) -> PendingCodaResult:
+    def stage_coda_batch(self, items, *, allow_async: bool = True, successors=None) -> PendingCodaResult:
         if not items:
             return PendingCodaResult(items=[], host_tokens=torch.empty(0, dtype=torch.int64))
         for item in items:
             item.state.tokens_in_flight += 1
+        eager_items, eager_rows = successors(items) if successors is not None else ([], [])
         tokens = torch.tensor([round(self.hidden[item.hidden_slot]) % self.vocab for item in items],
                               dtype=torch.int64)
-        return PendingCodaResult(items=items, host_tokens=tokens, device_tokens=tokens.clone())
+        pending = PendingCodaResult(items=items, host_tokens=tokens, device_tokens=tokens.clone())
+        if eager_items:
+            self.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
+        return pending
 
     def stage_prefill_batch(self, requests, *, allow_async: bool = True) -> PendingPrefillResult:
         meta = self.prefill_metadata(requests)

@@ -163,7 +163,8 @@ def test_linear_argument_errors_without_gpu() -> None:
 
     def am(**over):
         args = dict(x=fake, ldx=2048, w=fake, out=fake, ws=fake, ws_bytes=16 * 3072 * 8, rows=16, out_features=49152,
-                    in_features=2048, dtype=bf16, stream=None)
+                    in_features=2048, embed=None, bank=None, bank_rows=0, bank_slots=None, width=0, dtype=bf16,
+                    stream=None)
         args.update(over)
         return lib.cdb_linear_argmax(*args.values())
 
@@ -176,3 +177,6 @@ def test_linear_argument_errors_without_gpu() -> None:
     assert am(ldx=2044) == _lib.CDB_ERR_SHAPE
     assert am(ws=ctypes.c_void_p(0x1008)) == _lib.CDB_ERR_SHAPE
     assert am(ws_bytes=16 * 3072 * 8 - 1) == _lib.CDB_ERR_CAPACITY
+    assert am(embed=fake) == _lib.CDB_ERR_NULL                       # the fused prelude needs bank and slots
+    assert am(embed=fake, bank=fake, bank_slots=fake, bank_rows=512, width=2044) == _lib.CDB_ERR_SHAPE
+    assert am(embed=fake, bank=fake, bank_slots=fake, bank_rows=0, width=2048) == _lib.CDB_ERR_SHAPE

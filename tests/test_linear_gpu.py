@@ -291,3 +291,31 @@ def test_lm_head_argmax_routes_large_batches_through_the_logits() -> None:
     ops.linear_raw(x[:16], packed, logits)
     torch.cuda.synchronize()
     assert torch.equal(small, torch.argmax(logits, dim=-1))
+
+
+@pytest.mark.parametrize("rows", [1, 7, 16, 32, 48])
+def test_coda_writes_the_successors_prelude(rows: int) -> None:
+    """With an embedding table, rows with a successor slot get embed[token] in that bank row
+    (fused into the argmax pass up to 32 rows, a row copy above); other bank rows keep their bits."""
+
+    from continuous_depth_batching_amd import ops
+
+    vocab, width = 49152, 2048
+    x, w = _inputs(rows, width, vocab, seed=rows + 17)
+    packed = ops.pack_linear_weight(w)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(rows)
+    embed = torch.randn((vocab, width), generator=g, device="cuda").bfloat16()
+    bank = torch.randn((4 * rows + 8, width), generator=g, device="cuda").bfloat16()
+    before = bank.clone()
+    slots = torch.full((rows,), -1, dtype=torch.int64, device="cuda")
+    with_successor = torch.arange(0, rows, 2, device="cuda")
+    targets = 2 * rows + 3 + with_successor   # distinct rows away from anything else
+    slots[with_successor] = targets
+    tokens = ops.lm_head_argmax(x, w, packed, embed=embed, bank=bank, bank_slots=slots)
+    plain = ops.lm_head_argmax(x, w, packed)
+    torch.cuda.synchronize()
+    assert torch.equal(tokens, plain)
+    want = before.clone()
+    want[targets] = embed[tokens[with_successor]]
+    assert torch.equal(bank, want)

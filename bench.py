@@ -47,8 +47,11 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=1)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--num-seqs", type=int, default=256)
-    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention"), default="ouro-cdb",
-                   help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings")
+    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention", "kv-pressure"), default="ouro-cdb",
+                   help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings; "
+                        "kv-pressure: KV swap timings and the engine on a cache too small for the batch")
+    p.add_argument("--pressure-fraction", type=float, default=0.6,
+                   help="kv-pressure: cache size as a fraction of what the batch needs without preemption")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-microbench", action="store_true")
     p.add_argument("--cpu-sample-tokens", type=int, default=160)
@@ -274,6 +277,99 @@ def copy_calibration(nbytes: int = 1 << 30, iters: int = 5) -> dict:
             "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
 
 
+def time_kv_swap(blocks: int = 256, iters: int = 5) -> dict:
+    """Swap one 4096-token Ouro-1.4B request (kv single: 24 cache layers, 16 heads x 128, bf16,
+    256 blocks of 16 tokens, 3 MiB each) out to the pinned host pool and back, its device
+    blocks scattered as after allocator churn. The yardstick is a plain pinned copy of the
+    same bytes in one DMA; the gather kernel's HBM rate is timed on its own."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+    from continuous_depth_batching_amd.cache import PagedKVCache
+    from continuous_depth_batching_amd.kv_cache_policy import LoopedKvLayout
+    from continuous_depth_batching_amd.offloading import KvSwapPool
+
+    layout = LoopedKvLayout.build(num_prelude_layers=0, num_core_layers=24, num_coda_layers=0,
+                                  total_recurrent_steps=4, policy="single")
+    cache = PagedKVCache(layout=layout, num_blocks=2 * blocks + 8, block_size=16, num_kv_heads=16, head_dim=128,
+                         max_model_len=16 * blocks, max_num_batched_tokens=8192, max_requests=4,
+                         dtype=torch.bfloat16, device=torch.device("cuda"))
+    stream = torch.cuda.Stream()
+    pool = KvSwapPool(cache, num_host_blocks=blocks, stream=stream)
+    device_blocks = np.random.default_rng(0).permutation(cache.num_blocks)[:blocks].tolist()
+    host_blocks = list(range(blocks))
+    nbytes = blocks * pool.slabs * pool.block_elems * 2
+
+    def timed(fn, n: int) -> float:
+        fn()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record()
+            for _ in range(n):
+                fn()
+            end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / n
+
+    out_ms = timed(lambda: pool.swap_out(device_blocks, host_blocks), iters)
+    in_ms = timed(lambda: pool.swap_in(host_blocks, device_blocks), iters)
+    flat_dev = torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda")
+    flat_host = pool.host.view(-1)
+    with torch.cuda.stream(stream):
+        d2h_ms = timed(lambda: flat_host.copy_(flat_dev, non_blocking=True), iters)
+        h2d_ms = timed(lambda: flat_dev.copy_(flat_host, non_blocking=True), iters)
+    rows = pool.chunk_blocks * pool.slabs
+    with torch.cuda.stream(stream):
+        index = pool._upload_index(device_blocks[: pool.chunk_blocks])
+        gather_ms = timed(lambda: ops.copy_rows_raw(pool.device_rows, index, pool.staging, None, rows), 20)
+    gather_bytes = 2 * rows * pool.block_elems * 2
+
+    def gbps(b: int, ms: float) -> float:
+        return round(b / (ms * 1e-3) / 1e9, 1)
+
+    return {"request": f"{16 * blocks} tokens, {blocks} blocks, {nbytes} bytes", "chunk_blocks": pool.chunk_blocks,
+            "swap_out_ms": round(out_ms, 3), "swap_out_GBps": gbps(nbytes, out_ms),
+            "swap_in_ms": round(in_ms, 3), "swap_in_GBps": gbps(nbytes, in_ms),
+            "plain_d2h_GBps": gbps(nbytes, d2h_ms), "plain_h2d_GBps": gbps(nbytes, h2d_ms),
+            "swap_out_frac_of_plain": round(d2h_ms / out_ms, 3), "swap_in_frac_of_plain": round(h2d_ms / in_ms, 3),
+            "gather_kernel_us": round(gather_ms * 1e3, 2), "gather_kernel_GBps": gbps(gather_bytes, gather_ms)}
+
+
+def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpressured_blocks: int) -> dict:
+    """The end-to-end workload on a cache of ``num_blocks`` under each preempting pressure mode,
+    beside the same run (no warmup either) on a cache that needs no preemption."""
+
+    import torch
+
+    from continuous_depth_batching_amd.config import ContinuousDepthBatchingConfig
+    from continuous_depth_batching_amd.engine import ContinuousDepthBatchingEngine
+
+    results = {}
+    for mode, blocks, space in (("none", unpressured_blocks, None), ("recompute", num_blocks, None),
+                                ("offload", num_blocks, 16.0)):
+        cfg = ContinuousDepthBatchingConfig(
+            max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False, kv_policy="single",
+            refill=True, block_size=16, max_num_seqs=256, num_blocks=blocks, max_model_len=4096,
+            kv_pressure_mode=mode, cpu_offload_space=space)
+        engine = ContinuousDepthBatchingEngine.from_model(model, cfg)
+        engine.runner.capture_all_buckets()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        generated = sum(len(o.generated_tokens) for o in outs)
+        results[mode] = {"tok_per_s": round(generated / elapsed, 1), "seconds": round(elapsed, 2),
+                         "generated_tokens": generated, **engine.offloading_manager.preemption_stats(),
+                         "prefill_batches": engine.last_stats.prefill_batches}
+        print(json.dumps({"pressure_mode_done": mode, **results[mode]}), flush=True)
+        del engine
+        torch.cuda.empty_cache()
+    return results
+
+
 def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     """Numpy oracle decoding a bounded sample of the workload on the host cores."""
 
@@ -320,6 +416,19 @@ def main() -> int:
     cfg = ouro_1p4b_config()
     prompts, outputs, depths = c2_workload(args.num_seqs, cfg.vocab_size)
     result: dict = {}
+    blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs)) * 1.05) + 64
+
+    if args.workload == "kv-pressure":
+        swap = time_kv_swap()
+        print(json.dumps({"kv_swap": swap}), flush=True)
+        model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
+        pressured = int(blocks * args.pressure_fraction)
+        modes = run_pressure_modes(model, prompts, outputs, depths, pressured, blocks)
+        print(json.dumps({"metric": "KV swap-out host-link GB/s (4096-token Ouro-1.4B request)",
+                          "value": swap["swap_out_GBps"], "unit": "GB/s", "n_gpus": 1, "kv_swap": swap,
+                          "pressure": {"num_blocks": pressured, "unpressured_num_blocks": blocks,
+                                       "fraction": args.pressure_fraction, "modes": modes}}))
+        return 0
 
     attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device),
                                       split_pages=0, iters=args.attention_iters)
@@ -352,7 +461,6 @@ def main() -> int:
         return 0
 
     model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
-    blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs)) * 1.05) + 64
     engine_cfg = ContinuousDepthBatchingConfig(
         max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False, kv_policy="single",
         refill=True, block_size=16, max_num_seqs=256, num_blocks=blocks, max_model_len=4096,

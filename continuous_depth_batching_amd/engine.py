@@ -31,6 +31,7 @@ from typing import Any, Callable
 import torch
 
 from .cache import CacheFullError, PagedKVCache
+from .offloading import OffloadingManager
 from .config import ContinuousDepthBatchingConfig
 from .exit_policy import ExitPolicy
 from .kv_cache_policy import LoopedKvLayout, copies_exit_kv, resolve_kv_slots_per_layer
@@ -130,6 +131,7 @@ class ContinuousDepthBatchingEngine:
     model_adapter: CDBModelAdapter
     exit_policy: ExitPolicy
     exit_kv_layout: LoopedKvLayout | None = None
+    offloading_manager: OffloadingManager | None = None
     last_stats: ContinuousDepthBatchingStats = field(default_factory=ContinuousDepthBatchingStats)
     pending_coda_results: deque = field(default_factory=deque)
     pending_prefill_results: deque = field(default_factory=deque)
@@ -180,8 +182,12 @@ class ContinuousDepthBatchingEngine:
                                  max_num_seqs=cfg.max_num_seqs, min_free_slots=cfg.min_free_slots,
                                  min_coda_batch_size=cfg.min_coda_batch_size)
         exit_kv_layout = layout if copies_exit_kv(cfg.kv_policy) else None
+        offloading_manager = OffloadingManager(cache, scheduler, cfg.cpu_offload_space,
+                                               allow_recompute_fallback=not copies_exit_kv(cfg.kv_policy),
+                                               swap_factory=runner.make_kv_swap_pool)
         return cls(model=model, cdb_config=cfg, cache=cache, scheduler=scheduler, runner=runner,
-                   model_adapter=adapter, exit_policy=exit_policy, exit_kv_layout=exit_kv_layout)
+                   model_adapter=adapter, exit_policy=exit_policy, exit_kv_layout=exit_kv_layout,
+                   offloading_manager=offloading_manager)
 
     # -- public API (continuous_api.py:378-452) -----------------------------------------------------------------
     @torch.no_grad()
@@ -222,10 +228,12 @@ class ContinuousDepthBatchingEngine:
         return outputs
 
     def reset(self) -> None:
+        self.offloading_manager.free_all_waiting_cpu_caches()
         self.scheduler.reset()
         self.cache.free_all_requests()
         self.cache.reset_peak_usage()
         self.runner.reset_cdb_runtime_counters()
+        self.offloading_manager.reset()
         self.last_stats = ContinuousDepthBatchingStats()
         self.pending_coda_results.clear()
         self.pending_prefill_results.clear()
@@ -238,13 +246,16 @@ class ContinuousDepthBatchingEngine:
     # -- refill loop (continuous_api.py:503-606) ----------------------------------------------------------------
     def _run_scheduler_loop(self) -> None:
         sched = self.scheduler
-        cfg = self.cdb_config
         while sched.has_pending_work() or self.pending_coda_results or self.pending_prefill_results:
             self._consume_ready_prefill_results(block=not sched.has_pending_work())
             self._consume_ready_coda_results(block=not sched.has_pending_work())
             if not sched.has_pending_work():
                 continue
-            resumed = self._restage_stalled_decoders()
+            # Restores go first, so the prefill gate below sees them; they already hold a block for
+            # their pending token. Restored and restaged decoders share one prelude launch.
+            restored = self._restore_offloaded_requests()
+            resumed = [item for state in restored if (item := self._stage_decode_token(state)) is not None]
+            resumed += self._restage_stalled_decoders()
             self._prelude_and_enqueue_depth(resumed, site="resumed", front=True)
             stats = self.last_stats
             stats.scheduler_ticks += 1
@@ -265,8 +276,9 @@ class ContinuousDepthBatchingEngine:
                     self._consume_ready_coda_results(block=True)
                     continue
                 if self.stalled_decoders:
-                    raise CacheFullError("KV cache full: stalled decoders cannot allocate and preemption "
-                                         f"(kv_pressure_mode={cfg.kv_pressure_mode!r}) is not served by this engine")
+                    # Nothing else can run and no stalled decoder can allocate: yield one request's KV.
+                    self._preempt_stalled_decoder()
+                    continue
                 self._raise_scheduler_stall()
             if scheduled.kind == "prefill":
                 self._run_prefill_batch(scheduled)
@@ -567,9 +579,15 @@ class ContinuousDepthBatchingEngine:
         if self._try_allocate_one_decode_token(state):
             self.stalled_decoders.pop(state.request_id, None)
             return self._build_decode_item(state)
-        if self.cdb_config.kv_pressure_mode in ("none", "reserve"):
-            raise CacheFullError(f"KV cache full staging a decode block for request {state.request_id} "
-                                 f"(kv_pressure_mode={self.cdb_config.kv_pressure_mode!r})")
+        if self.cdb_config.kv_pressure_mode == "none":
+            raise CacheFullError(
+                f"KV cache full staging a decode block for request {state.request_id} and "
+                "kv_pressure_mode='none' does no preemption. Increase num_blocks, reduce load, or select "
+                "kv_pressure_mode='reserve'/'recompute'/'offload'.")
+        if self.cdb_config.kv_pressure_mode == "reserve":
+            raise CacheFullError(
+                f"Reserve admission over-committed the KV cache: request {state.request_id} could not "
+                "allocate a decode block. This is a bug in reservation accounting.")
         self.stalled_decoders[state.request_id] = state
         return None
 
@@ -581,6 +599,33 @@ class ContinuousDepthBatchingEngine:
                 break
             items.append(item)
         return items
+
+    def _preempt_stalled_decoder(self) -> None:
+        """Yield one stalled decoder's KV so the rest of the batch drains (continuous_api.py:1625-1652).
+
+        Only a stalled request sits at a clean token boundary. The victim is the one with the
+        fewest computed tokens, ties going to the most recent staller."""
+
+        if len(self.scheduler.active_requests) <= 1:
+            request_id = next(iter(self.stalled_decoders))
+            raise CacheFullError(
+                f"A single request's KV cache does not fit: request {request_id} could not allocate "
+                "a decode block and no other request can be preempted (increase num_blocks or reduce "
+                "max_model_len).")
+        request_id = min(reversed(self.stalled_decoders), key=lambda r: self.stalled_decoders[r].current_len())
+        state = self.stalled_decoders.pop(request_id)
+        self.offloading_manager.preempt_request(request_id, state)
+
+    def _restore_offloaded_requests(self) -> list[RequestState]:
+        """Re-admit swapped-out requests and copy their KV back before any launch reads it
+        (continuous_api.py:1490-1505)."""
+
+        if not self.offloading_manager.offloading_enabled:
+            return []
+        restored = self.scheduler.admit_offloaded_restores()
+        if restored:
+            self.offloading_manager.restore_scheduled_requests(restored)
+        return restored
 
     def _try_allocate_one_decode_token(self, state: RequestState) -> bool:
         current = state.current_len()
@@ -611,6 +656,8 @@ class ContinuousDepthBatchingEngine:
         sched = self.scheduler
         max_steps = self.cdb_config.max_recurrent_steps or 0
         while sched.has_pending_work():
+            # Restored requests decode again, so they join this wave's cohort scan.
+            self._restore_offloaded_requests()
             sched.record_resident_sample()
             did_prefill = False
             while sched.admit_prefill(sched.has_decode_work()):
@@ -625,8 +672,14 @@ class ContinuousDepthBatchingEngine:
             cohort = cohort[: self.cdb_config.max_num_seqs]
             items = [item for s in cohort if (item := self._stage_decode_token(s)) is not None]
             if not items:
-                if not did_prefill and sched.has_pending_work():
-                    raise CacheFullError("No-refill loop stalled with pending work")
+                if not did_prefill:
+                    if self.stalled_decoders:
+                        # No wave can run and no stalled decoder can allocate: yield one request's KV.
+                        self._preempt_stalled_decoder()
+                        continue
+                    if sched.has_pending_work():
+                        raise CacheFullError("No-refill loop stalled with pending work: the KV cache cannot "
+                                             "admit any waiting request and no decode work is ready")
                 continue
             self._record_prelude("wave_cohort", len(items))
             self.runner.compute_prelude_batch(items)

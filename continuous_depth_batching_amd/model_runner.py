@@ -31,6 +31,7 @@ from .cache import PagedKVCache
 from .config import ContinuousDepthBatchingConfig
 from .exit_policy import ExitDecisionRule, ExitPolicy
 from .model_adapter import CDBModelAdapter, GateLaunch, PrefillLaunch, RecurrentLaunch, StageLaunch
+from .offloading import KvSwapPool
 from .requests import TMP_TOKEN_ID, DepthWorkItem, FutureRequestState
 
 CODA_PIPELINE_DEPTH = 2
@@ -582,6 +583,12 @@ class ModelRunner:
                                  self._to_device(np.asarray(slots, dtype=np.int32), torch.int32), len(rows),
                                  layer_base=self.layout.core_base, core_layers=self.layout.num_core_layers,
                                  num_slots=self.layout.slots_per_layer)
+
+    # -- KV swap (offload pressure mode) -------------------------------------------------------------------------
+    def make_kv_swap_pool(self, num_host_blocks: int) -> KvSwapPool:
+        """The pinned host pool that swapped-out KV blocks move to, on the compute stream."""
+
+        return KvSwapPool(self.cache, num_host_blocks, stream=self.stream)
 
     def synchronize(self) -> None:
         self.stream.synchronize()

@@ -156,6 +156,44 @@ class RequestState:
         self._synthetic_exit_cursor += 1
         return depth
 
+    def prepare_for_offload_requeue(self) -> None:
+        """Reset a request whose KV was just swapped out, so it resumes from the restored KV
+        (continuous_batching/requests.py:275-288, cdb/requests.py:82-94).
+
+        The block allocation is dropped (the blocks come back on restore); a decoder keeps its
+        pending token and re-runs it through the recurrent path from step 0. The synthetic
+        exit-depth cursor is untouched, so the pending token replays its own recorded depth."""
+
+        self.allocated_blocks = 0
+        if self._status == RequestStatus.DECODING:
+            self.remaining_prefill_tokens = []
+        self.reset_depth_state_for_next_token()
+
+    def create_equivalent_initial_request(self) -> "RequestState":
+        """Rebuild this request as a fresh prefill for soft-reset preemption
+        (continuous_batching/requests.py:290-315, cdb/requests.py:111-126).
+
+        The generated tokens, the pending one included, are folded onto the prompt and the
+        length budget shrinks by as many. The re-prefill computes the pending token at full
+        depth, so its recorded exit depth is spent: the replay resumes at ``cursor + 1``.
+        Timing and the exit depths of the tokens already decoded carry over."""
+
+        new_state = RequestState(
+            request_id=self.request_id,
+            initial_tokens=self.initial_tokens + self.generated_tokens,
+            max_new_tokens=None if self.max_new_tokens is None else self.max_new_tokens - len(self.generated_tokens),
+            eos_token_id=self.eos_token_id,
+            stop_sequences=[list(s) for s in self.stop_sequences],
+            synthetic_exit_depths=self.synthetic_exit_depths[self._synthetic_exit_cursor + 1:],
+            replay_eos_finishes=self.replay_eos_finishes,
+        )
+        new_state._true_initial_tokens = self._true_initial_tokens or len(self.initial_tokens)
+        new_state.exit_depths = list(self.exit_depths)
+        new_state.created_time = self.created_time
+        new_state.lifespan = self.lifespan
+        new_state.first_token_time = self.first_token_time
+        return new_state
+
     def to_generation_output(self) -> GenerationOutput:
         return GenerationOutput(
             request_id=self.request_id,

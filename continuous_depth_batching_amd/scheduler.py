@@ -143,6 +143,28 @@ class CDBScheduler:
     def free_residency_slots(self) -> int:
         return max(0, self.max_num_seqs - len(self.active_requests))
 
+    def admit_offloaded_restores(self) -> list[RequestState]:
+        """Move swapped-out waiting requests back to the active set with blocks for their restored
+        length plus one token (scheduler_base.py:434-460).
+
+        Restores go before fresh prompts, are held while draining after a preemption, are bounded
+        by the open resident slots and stop at the first request whose blocks do not fit."""
+
+        if self.block_new_requests or self.kv_pressure_mode != "offload":
+            return []
+        admitted: list[RequestState] = []
+        for request_id in list(self.waiting_requests_order):
+            state = self.waiting_requests[request_id]
+            if not state.is_cpu_offloaded:
+                continue
+            if self.free_residency_slots() == 0 or not self._allocate_blocks_if_needed(state, 1):
+                break
+            self.active_requests[request_id] = state
+            del self.waiting_requests[request_id]
+            self.waiting_requests_order.remove(request_id)
+            admitted.append(state)
+        return admitted
+
     def admit_prefill_batch(self, candidates: list[RequestState]) -> bool:
         if not candidates:
             return False

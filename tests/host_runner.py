@@ -212,11 +212,46 @@ class HostLoopRunner(ModelRunner):
     def capture_all_buckets(self, buckets=None) -> int:
         return 0
 
+    def make_kv_swap_pool(self, num_host_blocks: int) -> "HostKvSwap":
+        return HostKvSwap(self.cache, num_host_blocks)
+
     def synchronize(self) -> None:
         pass
 
     def stream_scope(self):
         return nullcontext()
+
+
+class HostKvSwap:
+    """KvSwapPool's block moves on a host cache: the same host-pool layout (one pool block holds
+    a device block's slabs over every cache layer, K and V), moved with tensor indexing."""
+
+    def __init__(self, cache, num_host_blocks: int) -> None:
+        self.cache = cache
+        self.slabs = 2 * cache.num_layers
+        self.plane_blocks = cache.pool.shape[2] // cache.block_size
+        self.block_elems = cache.block_size * cache.num_key_value_heads * cache.head_dim
+        self.device_rows = cache.pool.view(self.slabs * self.plane_blocks, self.block_elems)
+        self.host = torch.zeros((num_host_blocks, self.slabs, self.block_elems), dtype=cache.dtype)
+        self.moves: list[tuple[str, list[int], list[int]]] = []
+
+    def _rows(self, device_blocks: list[int]) -> torch.Tensor:
+        blocks = torch.tensor(device_blocks, dtype=torch.int64)
+        return (torch.arange(self.slabs)[None, :] * self.plane_blocks + blocks[:, None]).reshape(-1)
+
+    def swap_out(self, device_blocks: list[int], host_blocks: list[int]) -> None:
+        assert len(device_blocks) == len(host_blocks)
+        self.moves.append(("out", list(device_blocks), list(host_blocks)))
+        if device_blocks:
+            slabs = self.device_rows[self._rows(device_blocks)].view(len(device_blocks), self.slabs, -1)
+            self.host[torch.tensor(host_blocks)] = slabs
+
+    def swap_in(self, host_blocks: list[int], device_blocks: list[int]) -> None:
+        assert len(device_blocks) == len(host_blocks)
+        self.moves.append(("in", list(device_blocks), list(host_blocks)))
+        if device_blocks:
+            self.device_rows[self._rows(device_blocks)] = self.host[torch.tensor(host_blocks)].reshape(
+                -1, self.block_elems)
 
 
 def make_engine(**cfg_over):

@@ -52,6 +52,10 @@ def parse_args() -> argparse.Namespace:
                         "kv-pressure: KV swap timings and the engine on a cache too small for the batch")
     p.add_argument("--pressure-fraction", type=float, default=0.6,
                    help="kv-pressure: cache size as a fraction of what the batch needs without preemption")
+    p.add_argument("--pressure-safety-margin", type=float, default=0.0,
+                   help="kv-pressure: prefill admission margin of the pressured runs (0 admits greedily, so "
+                        "decode growth reaches the preemption path instead of being throttled at admission)")
+    p.add_argument("--swap-only", action="store_true", help="kv-pressure: only the swap timings")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-microbench", action="store_true")
     p.add_argument("--cpu-sample-tokens", type=int, default=160)
@@ -337,7 +341,8 @@ def time_kv_swap(blocks: int = 256, iters: int = 5) -> dict:
             "gather_kernel_us": round(gather_ms * 1e3, 2), "gather_kernel_GBps": gbps(gather_bytes, gather_ms)}
 
 
-def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpressured_blocks: int) -> dict:
+def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpressured_blocks: int,
+                       safety_margin: float) -> dict:
     """The end-to-end workload on a cache of ``num_blocks`` under each preempting pressure mode,
     beside the same run (no warmup either) on a cache that needs no preemption."""
 
@@ -349,21 +354,31 @@ def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpress
     results = {}
     for mode, blocks, space in (("none", unpressured_blocks, None), ("recompute", num_blocks, None),
                                 ("offload", num_blocks, 16.0)):
+        margin = 0.2 if mode == "none" else safety_margin
         cfg = ContinuousDepthBatchingConfig(
             max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False, kv_policy="single",
             refill=True, block_size=16, max_num_seqs=256, num_blocks=blocks, max_model_len=4096,
-            kv_pressure_mode=mode, cpu_offload_space=space)
+            kv_pressure_mode=mode, cpu_offload_space=space, safety_margin=margin)
         engine = ContinuousDepthBatchingEngine.from_model(model, cfg)
         engine.runner.capture_all_buckets()
+        swap = engine.offloading_manager.swap
+        if swap is not None:
+            swap.record_timings = True
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
         generated = sum(len(o.generated_tokens) for o in outs)
+        stats = engine.last_stats
         results[mode] = {"tok_per_s": round(generated / elapsed, 1), "seconds": round(elapsed, 2),
                          "generated_tokens": generated, **engine.offloading_manager.preemption_stats(),
-                         "prefill_batches": engine.last_stats.prefill_batches}
+                         "prefill_batches": stats.prefill_batches, "prefill_tokens_recomputed":
+                             sum(length for _, _, length in engine.offloading_manager.recompute_events),
+                         "recurrent_batches": stats.recurrent_batches,
+                         "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),
+                         "coda_batches": stats.coda_batches, "scheduler_ticks": stats.scheduler_ticks,
+                         "swap": swap.transfer_summary() if swap is not None else None}
         print(json.dumps({"pressure_mode_done": mode, **results[mode]}), flush=True)
         del engine
         torch.cuda.empty_cache()
@@ -420,14 +435,18 @@ def main() -> int:
 
     if args.workload == "kv-pressure":
         swap = time_kv_swap()
-        print(json.dumps({"kv_swap": swap}), flush=True)
-        model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
-        pressured = int(blocks * args.pressure_fraction)
-        modes = run_pressure_modes(model, prompts, outputs, depths, pressured, blocks)
-        print(json.dumps({"metric": "KV swap-out host-link GB/s (4096-token Ouro-1.4B request)",
-                          "value": swap["swap_out_GBps"], "unit": "GB/s", "n_gpus": 1, "kv_swap": swap,
-                          "pressure": {"num_blocks": pressured, "unpressured_num_blocks": blocks,
-                                       "fraction": args.pressure_fraction, "modes": modes}}))
+        line = {"metric": "KV swap-out host-link GB/s (4096-token Ouro-1.4B request)",
+                "value": swap["swap_out_GBps"], "unit": "GB/s", "n_gpus": 1, "kv_swap": swap}
+        if not args.swap_only:
+            print(json.dumps({"kv_swap": swap}), flush=True)
+            model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
+            pressured = int(blocks * args.pressure_fraction)
+            modes = run_pressure_modes(model, prompts, outputs, depths, pressured, blocks,
+                                       args.pressure_safety_margin)
+            line["pressure"] = {"num_blocks": pressured, "unpressured_num_blocks": blocks,
+                                "fraction": args.pressure_fraction, "safety_margin": args.pressure_safety_margin,
+                                "modes": modes}
+        print(json.dumps(line))
         return 0
 
     attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device),

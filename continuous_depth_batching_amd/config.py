@@ -9,6 +9,7 @@ kernels, plus ``paged|cdb_hip``.
 
 from __future__ import annotations
 
+import math
 from copy import deepcopy
 from dataclasses import dataclass
 from typing import Any, Literal
@@ -31,6 +32,18 @@ def is_supported_attention_implementation(config: Any) -> bool:
     if backend in ("flash_attention", "cdb_hip"):
         return True
     return backend.startswith("flash_attention_") and backend[len("flash_attention_"):].isdigit()
+
+
+def validate_cache_size_request(num_blocks: int | None, mem_fraction_static: float | None) -> None:
+    """Explicit block count or a static memory fraction, not both (kv_cache_sizing.py:25-31)."""
+
+    if num_blocks is not None and num_blocks <= 0:
+        raise ValueError(f"num_blocks must be positive, but got {num_blocks}")
+    if mem_fraction_static is not None and (not math.isfinite(mem_fraction_static)
+                                            or not 0 < mem_fraction_static < 1):
+        raise ValueError(f"mem_fraction_static must be finite and in (0, 1), but got {mem_fraction_static}")
+    if num_blocks is not None and mem_fraction_static is not None:
+        raise ValueError("Set either num_blocks or mem_fraction_static, not both")
 
 
 def validate_kv_pressure_config(mode: str, cpu_offload_space: float | None) -> None:
@@ -104,12 +117,7 @@ class ContinuousDepthBatchingConfig:
             raise ValueError(f"block_size must be positive, but got {self.block_size}")
         if self.block_size & (self.block_size - 1):
             raise ValueError(f"block_size must be a power of two for the paged kernels, got {self.block_size}")
-        if self.num_blocks is not None and self.num_blocks <= 0:
-            raise ValueError(f"num_blocks must be positive when set, but got {self.num_blocks}")
-        if self.num_blocks is not None and self.mem_fraction_static is not None:
-            raise ValueError("set at most one of num_blocks and mem_fraction_static")
-        if self.mem_fraction_static is not None and not 0 < self.mem_fraction_static <= 1:
-            raise ValueError(f"mem_fraction_static must be in (0, 1], got {self.mem_fraction_static}")
+        validate_cache_size_request(self.num_blocks, self.mem_fraction_static)
         if self.max_num_batched_tokens <= 0:
             raise ValueError(f"max_num_batched_tokens must be positive, but got {self.max_num_batched_tokens}")
         if self.max_model_len <= 0:

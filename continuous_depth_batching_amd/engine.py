@@ -23,6 +23,7 @@ item's previous launch, which have long landed.
 
 from __future__ import annotations
 
+import gc
 import time
 from collections import Counter, deque
 from dataclasses import dataclass, field
@@ -32,7 +33,7 @@ import torch
 
 from .cache import CacheFullError, PagedKVCache
 from .offloading import OffloadingManager
-from .config import ContinuousDepthBatchingConfig
+from .config import ContinuousDepthBatchingConfig, validate_cache_size_request
 from .exit_policy import ExitPolicy
 from .kv_cache_policy import LoopedKvLayout, copies_exit_kv, resolve_kv_slots_per_layer
 from .model_adapter import CDBModelAdapter, resolve_cdb_model_adapter
@@ -106,18 +107,35 @@ class LaunchRecord:
     exits: list[bool] = field(default_factory=list)
 
 
-def resolve_num_blocks(num_blocks: int | None, mem_fraction: float | None, bytes_per_block: int,
-                       device: torch.device) -> int:
-    """Explicit num_blocks, or size the pool from free device memory (kv_cache_sizing.py:34-80)."""
+DEFAULT_MEM_FRACTION_STATIC = 0.8
 
+
+def resolve_num_blocks(num_blocks: int | None, mem_fraction: float | None, bytes_per_block: int,
+                       device: torch.device | str) -> int:
+    """Explicit num_blocks, or the usable blocks of the post-load budget
+    ``free - total * (1 - fraction)`` (kv_cache_sizing.py:34-80, paged_cache_geometry.py:143-144).
+
+    The model is loaded before the engine is built, so the reserve ``total * (1 - fraction)``
+    covers graph captures, activations and every allocation outside the KV pool. On a 288 GB
+    MI355X the default fraction leaves about 58 GB of that reserve."""
+
+    validate_cache_size_request(num_blocks, mem_fraction)
     if num_blocks is not None:
         return num_blocks
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("Automatic KV cache sizing requires CUDA (torch's device for the GPU); set num_blocks "
+                         "explicitly for other devices")
+    gc.collect()
+    torch.cuda.empty_cache()
     free, total = torch.cuda.mem_get_info(device)
-    fraction = 0.8 if mem_fraction is None else mem_fraction
-    budget = int(free - (1.0 - fraction) * total)
+    fraction = DEFAULT_MEM_FRACTION_STATIC if mem_fraction is None else mem_fraction
+    budget = int(free - total * (1 - fraction))
     blocks = budget // bytes_per_block - PagedKVCache.EXTRA_BLOCKS
     if blocks <= 0:
-        raise CacheFullError("not enough free device memory for the paged KV cache")
+        raise ValueError(f"No usable KV blocks fit: free={free} bytes, total={total} bytes, "
+                         f"mem_fraction_static={fraction}, bytes_per_block={bytes_per_block}. "
+                         "Increase mem_fraction_static or reduce the model/cache size.")
     return blocks
 
 

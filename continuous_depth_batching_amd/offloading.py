@@ -77,9 +77,31 @@ class KvSwapPool:
         self._index_dev = torch.empty(cap, dtype=torch.int64, device=cache.device)
         self._index_event: torch.cuda.Event | None = None
         self.stream = stream
+        # Optional HIP-event timing of every move: (direction, bytes, start, end).
+        self.record_timings = False
+        self._timings: list[tuple[str, int, torch.cuda.Event, torch.cuda.Event]] = []
 
     def _scope(self):
         return torch.cuda.stream(self.stream) if self.stream is not None else nullcontext()
+
+    def _timed(self, direction: str, blocks: int):
+        if not self.record_timings:
+            return None
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        self._timings.append((direction, blocks * self.slabs * self.block_elems * self.host.element_size(),
+                              start, end))
+        return end
+
+    def transfer_summary(self) -> dict[str, float]:
+        """Moves, bytes and device milliseconds per direction (call after a synchronize)."""
+
+        out: dict[str, float] = {}
+        for direction, nbytes, start, end in self._timings:
+            out[f"{direction}_moves"] = out.get(f"{direction}_moves", 0) + 1
+            out[f"{direction}_bytes"] = out.get(f"{direction}_bytes", 0) + nbytes
+            out[f"{direction}_ms"] = round(out.get(f"{direction}_ms", 0.0) + start.elapsed_time(end), 3)
+        return out
 
     def _upload_index(self, device_blocks: list[int]) -> torch.Tensor:
         """Device rows of every slab of ``device_blocks``, block-major, on the compute stream."""
@@ -113,6 +135,7 @@ class KvSwapPool:
             return
         s, step = self.slabs, self.chunk_blocks
         with self._scope():
+            end = self._timed("out", len(device_blocks))
             index = self._upload_index(device_blocks)
             for c0 in range(0, len(device_blocks), step):
                 c1 = min(len(device_blocks), c0 + step)
@@ -120,6 +143,8 @@ class KvSwapPool:
                 for h0, k0, r in host_block_runs(host_blocks[c0:c1]):
                     self.host[h0:h0 + r].view(r * s, self.block_elems).copy_(
                         self.staging[k0 * s:(k0 + r) * s], non_blocking=True)
+            if end is not None:
+                end.record()
 
     def swap_in(self, host_blocks: list[int], device_blocks: list[int]) -> None:
         """Device block device_blocks[j] = host[host_blocks[j]], over every cache layer, K and V."""
@@ -129,6 +154,7 @@ class KvSwapPool:
             return
         s, step = self.slabs, self.chunk_blocks
         with self._scope():
+            end = self._timed("in", len(device_blocks))
             index = self._upload_index(device_blocks)
             for c0 in range(0, len(device_blocks), step):
                 c1 = min(len(device_blocks), c0 + step)
@@ -136,6 +162,8 @@ class KvSwapPool:
                     self.staging[k0 * s:(k0 + r) * s].copy_(
                         self.host[h0:h0 + r].view(r * s, self.block_elems), non_blocking=True)
                 ops.copy_rows_raw(self.staging, None, self.device_rows, index[c0 * s:c1 * s], (c1 - c0) * s)
+            if end is not None:
+                end.record()
 
 
 class OffloadingManager:

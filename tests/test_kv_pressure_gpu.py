@@ -118,3 +118,27 @@ def test_recompute_preemption_matches_the_composed_oracle(use_async: bool) -> No
         assert out.generated_tokens == tokens, f"request {i}, cuts {cuts.get(i)}"
         assert out.exit_depths == exits
     assert engine.cache.get_num_free_blocks() == engine.cache.num_blocks
+
+
+def test_auto_sized_cache_serves_a_batch() -> None:
+    """num_blocks=None sizes the pool from free device memory after the model is loaded
+    (kv_cache_sizing.py:34-80); the fraction leaves about 512 MiB for the KV pool."""
+
+    import gc
+
+    from tests.test_engine_gpu import workload
+
+    model, weights = build_model(seed=0)
+    gc.collect()
+    torch.cuda.empty_cache()
+    free, total = torch.cuda.mem_get_info()
+    fraction = (total - free + 512 * 1024**2) / total
+    engine = make_engine(model, num_blocks=None, mem_fraction_static=fraction, max_num_seqs=4)
+    cache = engine.cache
+    assert cache.num_blocks > 0 and engine.cdb_config.num_blocks == cache.num_blocks
+    pool_bytes = cache.pool.numel() * cache.pool.element_size()
+    assert 256 * 1024**2 < pool_bytes <= 576 * 1024**2  # 512 MiB, plus whatever a late free returned
+    prompts, mnt = workload(seed=4, n=4, new_tokens=8)
+    outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=None)
+    want = run_oracle(weights, prompts, mnt)
+    assert [o.generated_tokens for o in outs] == [w.tokens for w in want]

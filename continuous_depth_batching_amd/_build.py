@@ -1,4 +1,5 @@
-"""Compile the HIP kernels under ``csrc/`` into ``libcdb_amd.so`` for gfx950.
+"""Compile the HIP kernels under ``csrc/`` into ``libcdb_amd.so`` for gfx950, and the
+host tick core ``csrc/tick.cpp`` into the ``_tick`` extension module.
 
 The library is built in-tree next to this file so that it travels with the
 source tree; object files go to ``_build/`` at the repository root. Every call
@@ -10,6 +11,7 @@ from __future__ import annotations
 import os
 import shutil
 import subprocess
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -84,5 +86,31 @@ def build_library(*, force: bool = False, jobs: int | None = None) -> Path:
     return LIBRARY_PATH
 
 
+TICK_SOURCE = CSRC_DIR / "tick.cpp"
+TICK_PATH = PACKAGE_DIR / ("_tick" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_tick(*, force: bool = False) -> Path:
+    """Compile the host tick core (``csrc/tick.cpp``, a CPython extension) with g++."""
+
+    if not force and TICK_PATH.exists() and TICK_PATH.stat().st_mtime >= TICK_SOURCE.stat().st_mtime:
+        return TICK_PATH
+    cxx = shutil.which(os.environ.get("CXX", "g++")) or shutil.which("g++")
+    if not cxx:
+        raise RuntimeError("g++ not found; the host tick core needs a C++ compiler")
+    tmp = TICK_PATH.with_name(TICK_PATH.name + ".tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(TICK_SOURCE), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed for {TICK_SOURCE.name}:\n{proc.stderr}")
+    os.replace(tmp, TICK_PATH)
+    return TICK_PATH
+
+
+def build_all(*, force: bool = False) -> tuple[Path, Path]:
+    return build_library(force=force), build_tick(force=force)
+
+
 if __name__ == "__main__":
-    print(build_library())
+    print(build_all())

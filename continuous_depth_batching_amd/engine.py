@@ -46,6 +46,7 @@ from .model_runner import (
 )
 from .requests import TMP_TOKEN_ID, DepthWorkItem, GenerationOutput, RequestState, RequestStatus
 from .scheduler import CDBScheduler, ScheduledCDBBatch
+from . import _tick
 
 
 @dataclass
@@ -404,21 +405,30 @@ class ContinuousDepthBatchingEngine:
         stats.recurrent_batches += 1
         stats.recurrent_steps += len(items)
         max_steps = self.cdb_config.max_recurrent_steps
-        delayed = self.exit_policy.delayed()
-        refills: list[DepthWorkItem] = []
-        exits: list[bool] = []
+        if not self.exit_policy.delayed():
+            # Synchronous horizon: this launch's flags route its rows (the host tick core does
+            # the per-row work: exit bookkeeping, coda list, step advance of the refills).
+            coda_items, refills, exits = _tick.route_sync(
+                items, flags.wait(), max_steps, stats.exit_depth_histogram,
+                self._exit_kv_backlog if self.exit_kv_layout is not None else None)
+            self.scheduler.enqueue_coda_items(coda_items)
+            if refills:
+                self.scheduler.enqueue_depth_front(refills)
+            self._flush_exit_kv_copies()
+            if self.record_launches:
+                self.launch_log.append(LaunchRecord("recurrent", [i.state.request_id for i in items],
+                                                    [i.token_position for i in items], launch_steps, exits))
+            return
+        refills = []
+        exits = []
         for idx, item in enumerate(items):
+            # Delayed horizon: a launch's decisions route the item after its next launch.
             step = item.recurrent_step
-            if delayed:
-                previous = self._pending_flags.pop(id(item), None)
-                should_exit = step == max_steps - 1 or (
-                    item.apply_exit_gate and previous is not None and previous[0].get(previous[1]))
-                if not should_exit:
-                    self._pending_flags[id(item)] = (flags, idx)
-            elif not item.apply_exit_gate:
-                should_exit = step == max_steps - 1
-            else:
-                should_exit = flags.get(idx)
+            previous = self._pending_flags.pop(id(item), None)
+            should_exit = step == max_steps - 1 or (
+                item.apply_exit_gate and previous is not None and previous[0].get(previous[1]))
+            if not should_exit:
+                self._pending_flags[id(item)] = (flags, idx)
             exits.append(should_exit)
             if should_exit:
                 self._record_exit(item, step)

@@ -32,6 +32,7 @@ from .config import ContinuousDepthBatchingConfig
 from .exit_policy import ExitDecisionRule, ExitPolicy
 from .model_adapter import CDBModelAdapter, GateLaunch, PrefillLaunch, RecurrentLaunch, StageLaunch
 from .offloading import KvSwapPool
+from . import _tick
 from .requests import TMP_TOKEN_ID, DepthWorkItem, FutureRequestState
 
 CODA_PIPELINE_DEPTH = 2
@@ -100,6 +101,14 @@ class PendingFlags:
     event: Any | None
     _values: list[int] | None = None
 
+    def wait(self) -> np.ndarray:
+        """The decision bytes, once the launch has written them (one per row, then padding)."""
+
+        if self.event is not None:
+            self.event.synchronize()
+            self.event = None
+        return self.host.numpy()
+
     def get(self, index: int) -> bool:
         values = self._values
         if values is None:
@@ -141,9 +150,18 @@ class _RecurrentBucket:
     flag_events: list[Any] = field(default_factory=list)
 
 
+@dataclass
+class _CodaTurn:
+    host_upload: torch.Tensor  # pinned int64: coda slots | successor slots | successors' own slots
+    dev_upload: torch.Tensor
+    host_tokens: torch.Tensor  # pinned int64 greedy tokens
+    event: Any
+
+
 class ModelRunner:
     META_POSITIONS, META_TABLE_ROWS, META_LAYER_OFFSET, META_STEPS, META_SYNTHETIC = range(5)
     FLAG_TURNS = 4
+    CODA_TURNS = 4
 
     def __init__(self, *, engine_config: ContinuousDepthBatchingConfig, cache: PagedKVCache,
                  model_adapter: CDBModelAdapter, exit_policy: ExitPolicy) -> None:
@@ -185,6 +203,9 @@ class ModelRunner:
         self.recurrent_graph_captures = 0
         self.stage_graph_hits = 0
         self.stage_graph_captures = 0
+        self._slot_of_step: tuple[int, ...] | None = None
+        self._coda_turns: list[_CodaTurn | None] = [None] * self.CODA_TURNS
+        self._coda_turn_index = 0
 
     # -- hidden slots (cdb/model_runner.py:1193-1203, 1359-1363) ------------------------------------------------
     def reset_cdb_runtime_counters(self) -> None:
@@ -356,9 +377,10 @@ class ModelRunner:
             self._run_recurrent(b)
             host_flags = b.host_flags[turn]
             host_flags[:n].copy_(b.launch.gate.flags[:n], non_blocking=True)
-            event = torch.cuda.Event()
+            event = b.flag_events[turn]
+            if event is None:
+                event = b.flag_events[turn] = torch.cuda.Event()
             event.record()
-            b.flag_events[turn] = event
         return PendingFlags(host=host_flags, event=event)
 
     def fill_recurrent_metadata(self, items: list[DepthWorkItem], i64: np.ndarray, i32: np.ndarray) -> None:
@@ -370,25 +392,12 @@ class ModelRunner:
         slot -1 and position -1 make every kernel skip them
         (cdb/model_runner.py:704-754 assembles the same per-row facts)."""
 
-        n = len(items)
-        base = self.layout.core_base
-        core = self.layout.num_core_layers
-        slot_for = self.layout.slot_for_step
-        i64[:n] = [item.hidden_slot for item in items]
-        i32[self.META_POSITIONS, :n] = [item.token_position for item in items]
-        row_of = self.cache.table_row_of
-        i32[self.META_TABLE_ROWS, :n] = [row_of[item.state.request_id] for item in items]
-        steps = [item.recurrent_step for item in items]
-        i32[self.META_STEPS, :n] = steps
-        i32[self.META_LAYER_OFFSET, :n] = [base + slot_for(s) * core for s in steps]
-        i32[self.META_SYNTHETIC, :n] = [-1 if (d := item.synthetic_exit_depth) is None or not item.apply_exit_gate
-                                        else d for item in items]
-        i64[n:] = -1
-        i32[self.META_POSITIONS, n:] = -1
-        i32[self.META_TABLE_ROWS, n:] = 0
-        i32[self.META_LAYER_OFFSET, n:] = base
-        i32[self.META_STEPS, n:] = 0
-        i32[self.META_SYNTHETIC, n:] = -1
+        slot_of_step = self._slot_of_step
+        if slot_of_step is None:
+            steps = self.engine_config.max_recurrent_steps or 0
+            slot_of_step = self._slot_of_step = tuple(self.layout.slot_for_step(s) for s in range(steps))
+        _tick.fill_recurrent(items, i64, i32, self.cache.table_row_of, self.layout.core_base,
+                             self.layout.num_core_layers, slot_of_step)
 
     def capture_all_buckets(self, buckets: Sequence[int] | None = None) -> int:
         """Capture the recurrent-stage graph of every bucket ahead of time.
@@ -460,22 +469,27 @@ class ModelRunner:
         n = len(items)
         eager_items, eager_rows = successors(items) if successors is not None else ([], [])
         fused = bool(eager_items) and self.adapter.coda_writes_successor_prelude
-        upload = np.fromiter((it.hidden_slot for it in items), dtype=np.int64, count=n)
+        m = n + n + len(eager_items) if fused else n
+        turn = self._coda_turn(m, n)
+        upload = turn.host_upload.numpy()
+        upload[:n] = [it.hidden_slot for it in items]
         if fused:
             new_slots = self.allocate_hidden_slots(len(eager_items))
-            successor = np.full(n, -1, dtype=np.int64)
-            successor[eager_rows] = new_slots
             # One upload: [coda rows' slots | each row's successor slot or -1 | the successors' slots].
-            upload = np.concatenate([upload, successor, np.asarray(new_slots, dtype=np.int64)])
+            successor = upload[n:2 * n]
+            successor[:] = -1
+            successor[eager_rows] = new_slots
+            upload[2 * n:m] = new_slots
         with self._on_stream():
-            dev = self._to_device(upload, torch.int64)
+            dev = turn.dev_upload[:m]
+            dev.copy_(turn.host_upload[:m], non_blocking=True)
             launch = self._stage_launch(items, dev[:n])
             if fused:
                 launch.successor_slots = dev[n:2 * n]
             tokens = self.adapter.coda(launch)
-            host = self._pinned((n,), torch.int64)
+            host = turn.host_tokens[:n]
             host.copy_(tokens, non_blocking=True)
-            event = torch.cuda.Event()
+            event = turn.event
             event.record()
             if fused:
                 self.gate_state.reset(dev[2 * n:], len(eager_items))
@@ -488,6 +502,25 @@ class ModelRunner:
         if not allow_async:
             event.synchronize()
         return pending
+
+    def _coda_turn(self, upload: int, rows: int) -> _CodaTurn:
+        """The next of CODA_TURNS rotating coda buffers. At most CODA_PIPELINE_DEPTH codas are
+        unconsumed at once, so a turn comes round again only after its result was read; its
+        event is still waited on first."""
+
+        k = self._coda_turn_index
+        self._coda_turn_index = (k + 1) % self.CODA_TURNS
+        turn = self._coda_turns[k]
+        if turn is not None:
+            turn.event.synchronize()
+        if turn is None or turn.host_upload.numel() < upload or turn.host_tokens.numel() < rows:
+            cap = max(upload, 3 * self.max_num_seqs)
+            turn = self._coda_turns[k] = _CodaTurn(
+                host_upload=self._pinned((cap,), torch.int64),
+                dev_upload=torch.empty(cap, dtype=torch.int64, device=self.device),
+                host_tokens=self._pinned((max(rows, self.max_num_seqs),), torch.int64),
+                event=torch.cuda.Event())
+        return turn
 
     def consume_coda_result(self, pending: PendingCodaResult) -> list[int]:
         if pending.ready_event is not None:

@@ -275,6 +275,21 @@ class CDBScheduler:
         self._mark_request_in_flight(item.state.request_id)
         self.coda_queue.append(item)
 
+    def enqueue_coda_items(self, items: list[DepthWorkItem]) -> None:
+        """enqueue_coda over ``items`` in order, with the in-flight peaks updated once."""
+
+        if not items:
+            return
+        in_flight = self.in_flight_request_ids
+        for item in items:
+            in_flight.add(item.state.request_id)
+        if len(in_flight) > self.max_in_flight_requests:
+            self.max_in_flight_requests = len(in_flight)
+        live = len(self.active_requests) + len(self.waiting_requests)
+        if live > self.max_live_requests:
+            self.max_live_requests = live
+        self.coda_queue.extend(items)
+
     def schedule_prefill_batch(self, token_budget: int, cache_budget: int) -> ScheduledCDBBatch | None:
         candidates = self.get_prefill_candidates()
         if not candidates:

@@ -47,9 +47,11 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=1)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--num-seqs", type=int, default=256)
-    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention", "kv-pressure"), default="ouro-cdb",
+    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention", "kv-pressure", "ouro-2p6b"),
+                   default="ouro-cdb",
                    help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings; "
-                        "kv-pressure: KV swap timings and the engine on a cache too small for the batch")
+                        "kv-pressure: KV swap timings and the engine on a cache too small for the batch; "
+                        "ouro-2p6b: the 48-layer shape at 512 sequences, single vs per-step KV")
     p.add_argument("--pressure-fraction", type=float, default=0.6,
                    help="kv-pressure: cache size as a fraction of what the batch needs without preemption")
     p.add_argument("--pressure-safety-margin", type=float, default=0.0,
@@ -385,6 +387,63 @@ def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpress
     return results
 
 
+def run_ouro_2p6b(num_seqs: int = 512) -> dict:
+    """Ouro-2.6B shape (48 layers looped 4 steps), 512 sequences with the headline prompt, output
+    and exit-depth distributions, timed with shared (``single``) and per-step KV.
+
+    Single KV gets a pool sized for the whole batch. Per-step KV (``last_exited``: 192 cache
+    layers, 1.5 MiB per token) needs about 2.5x this GPU's HBM for the batch, so its pool is
+    sized from free device memory after the model is loaded (``mem_fraction_static`` 0.8) and
+    KV pressure swaps decoders to a 64 GiB pinned host pool (``offload``; a soft reset would
+    replace exit-step KV). Each engine captures its graphs and runs a short warmup first."""
+
+    import torch
+
+    from continuous_depth_batching_amd.config import ContinuousDepthBatchingConfig
+    from continuous_depth_batching_amd.engine import ContinuousDepthBatchingEngine
+    from continuous_depth_batching_amd.ouro import OuroConfig, build_ouro
+
+    cfg = OuroConfig(vocab_size=49152, hidden_size=2048, intermediate_size=5632, num_hidden_layers=48,
+                     num_attention_heads=16, num_key_value_heads=16, head_dim=128, total_ut_steps=4,
+                     max_position_embeddings=4096)
+    model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device="cuda")
+    prompts, outputs, depths = c2_workload(num_seqs, cfg.vocab_size)
+    need = sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs))
+    runs = {}
+    for policy in ("single", "last_exited"):
+        common = dict(max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False,
+                      kv_policy=policy, refill=True, block_size=16, max_num_seqs=num_seqs, max_model_len=4096)
+        if policy == "single":
+            extra = dict(num_blocks=int(need * 1.05) + 64, kv_pressure_mode="none")
+        else:
+            extra = dict(num_blocks=None, kv_pressure_mode="offload", cpu_offload_space=64.0)
+        engine = ContinuousDepthBatchingEngine.from_model(model, ContinuousDepthBatchingConfig(**common, **extra))
+        engine.runner.capture_all_buckets()
+        k = 32
+        engine.generate_batch(prompts[:k], max_new_tokens=[min(o, 24) for o in outputs[:k]], eos_token_id=None,
+                              exit_depths=[d[: min(o, 24) - 1] for d, o in zip(depths[:k], outputs[:k])])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        generated = sum(len(o.generated_tokens) for o in outs)
+        stats = engine.last_stats
+        om = engine.offloading_manager
+        runs[policy] = {
+            "tok_per_s": round(generated / elapsed, 1), "seconds": round(elapsed, 2), "generated_tokens": generated,
+            "num_blocks": engine.cache.num_blocks, "blocks_for_whole_batch": need,
+            "kv_bytes_per_block": om.bytes_per_block(), "cache_layers": engine.cache.num_layers,
+            "recurrent_batches": stats.recurrent_batches,
+            "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1), "coda_batches": stats.coda_batches,
+            "prefill_batches": stats.prefill_batches, "exit_kv_copies": stats.exit_kv_copies,
+            **om.preemption_stats()}
+        print(json.dumps({"ouro_2p6b_done": policy, **runs[policy]}), flush=True)
+        del engine, om
+        torch.cuda.empty_cache()
+    return runs
+
+
 def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     """Numpy oracle decoding a bounded sample of the workload on the host cores."""
 
@@ -432,6 +491,13 @@ def main() -> int:
     prompts, outputs, depths = c2_workload(args.num_seqs, cfg.vocab_size)
     result: dict = {}
     blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs)) * 1.05) + 64
+
+    if args.workload == "ouro-2p6b":
+        runs = run_ouro_2p6b()
+        print(json.dumps({"metric": "output tok/s, Ouro-2.6B-shape CDB decode bs=512, single vs per-step KV",
+                          "value": runs["single"]["tok_per_s"], "unit": "output tok/s", "n_gpus": 1,
+                          "dtype": "bf16", "data": "synthetic", "runs": runs}))
+        return 0
 
     if args.workload == "kv-pressure":
         swap = time_kv_swap()

@@ -47,11 +47,12 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=1)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--num-seqs", type=int, default=256)
-    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention", "kv-pressure", "ouro-2p6b"),
+    p.add_argument("--workload", choices=("ouro-cdb", "decode-attention", "kv-pressure", "ouro-2p6b", "huginn"),
                    default="ouro-cdb",
                    help="ouro-cdb: the end-to-end engine; decode-attention: only the kernel timings; "
                         "kv-pressure: KV swap timings and the engine on a cache too small for the batch; "
-                        "ouro-2p6b: the 48-layer shape at 512 sequences, single vs per-step KV")
+                        "ouro-2p6b: the 48-layer shape at 512 sequences, single vs per-step KV; "
+                        "huginn: the Huginn-0125 shape at 128 sequences, 32 loop steps")
     p.add_argument("--pressure-fraction", type=float, default=0.6,
                    help="kv-pressure: cache size as a fraction of what the batch needs without preemption")
     p.add_argument("--pressure-safety-margin", type=float, default=0.0,
@@ -444,6 +445,50 @@ def run_ouro_2p6b(num_seqs: int = 512) -> dict:
     return runs
 
 
+def run_huginn_0125(num_seqs: int = 128, new_tokens: int = 256) -> dict:
+    """Huginn-0125 shape (hidden 5280, 55 heads x 96, prelude 2 + core 4 + coda 2 layers, MLP 17920,
+    vocab 65536), random-init bf16, seed 1. 128 sequences: prompts lognormal(5.0, 0.9) in [8, 1024]
+    with uniform ids, 256 new tokens each; per-token exit steps replayed from Poisson(12)
+    truncated to [1, 32]; kv single; refill. The latent state starts from the reference's
+    state_init="random" (truncated normal, seeded)."""
+
+    import torch
+
+    from continuous_depth_batching_amd.config import ContinuousDepthBatchingConfig
+    from continuous_depth_batching_amd.engine import ContinuousDepthBatchingEngine
+    from continuous_depth_batching_amd.huginn import HuginnConfig, build_huginn
+    from continuous_depth_batching_amd.workloads import lognormal_requests, poisson_exit_trace
+
+    cfg = HuginnConfig(block_size=2048, state_init="random", state_seed=1)
+    model = build_huginn(cfg, seed=1, dtype=torch.bfloat16, device="cuda", qk_bias_std=0.02)
+    prompts, _ = lognormal_requests(num_requests=num_seqs, vocab_size=cfg.vocab_size, prompt_mu=5.0,
+                                    prompt_sigma=0.9, prompt_range=(8, 1024), output_mu=5.0, output_sigma=0.8,
+                                    output_range=(16, 1024), seed=3)
+    outputs = [new_tokens] * num_seqs
+    depths = poisson_exit_trace(outputs, mean=12.0, max_steps=32, seed=4)
+    need = sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs))
+    engine = ContinuousDepthBatchingEngine.from_model(model, ContinuousDepthBatchingConfig(
+        max_recurrent_steps=32, synthetic_exit_replay=True, delay_gate_consumption=False, kv_policy="single",
+        refill=True, block_size=16, max_num_seqs=num_seqs, num_blocks=int(need * 1.05) + 64, max_model_len=2048,
+        kv_pressure_mode="none"))
+    engine.runner.capture_all_buckets()
+    k = 16
+    engine.generate_batch(prompts[:k], max_new_tokens=[16] * k, eos_token_id=None,
+                          exit_depths=[d[:15] for d in depths[:k]])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    generated = sum(len(o.generated_tokens) for o in outs)
+    stats = engine.last_stats
+    return {"tok_per_s": round(generated / elapsed, 1), "seconds": round(elapsed, 2), "generated_tokens": generated,
+            "recurrent_batches": stats.recurrent_batches, "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),
+            "recurrent_steps": stats.recurrent_steps, "coda_batches": stats.coda_batches,
+            "prefill_batches": stats.prefill_batches, "mean_exit_depth":
+                round(sum(d + 1 for ds in depths for d in ds) / sum(len(ds) for ds in depths), 2)}
+
+
 def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     """Numpy oracle decoding a bounded sample of the workload on the host cores."""
 
@@ -491,6 +536,13 @@ def main() -> int:
     prompts, outputs, depths = c2_workload(args.num_seqs, cfg.vocab_size)
     result: dict = {}
     blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs)) * 1.05) + 64
+
+    if args.workload == "huginn":
+        run = run_huginn_0125()
+        print(json.dumps({"metric": "output tok/s, Huginn-0125-shape CDB decode bs=128, 32 loop steps",
+                          "value": run["tok_per_s"], "unit": "output tok/s", "n_gpus": 1, "dtype": "bf16",
+                          "data": "synthetic", "run": run}))
+        return 0
 
     if args.workload == "ouro-2p6b":
         runs = run_ouro_2p6b()

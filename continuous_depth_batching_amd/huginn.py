@@ -64,6 +64,9 @@ class HuginnConfig:
     bias: bool = False
     tie_embeddings: bool = True
     state_init: str = "zero"
+    # Seed of the generator behind state_init="random" (None: torch's default generator, as the
+    # reference draws it).
+    state_seed: int | None = None
     bos_token_id: int = 65504
     eos_token_id: int = 65505
     pad_token_id: int = 65509
@@ -226,12 +229,16 @@ class HuginnCDBAdapter(CDBModelAdapter):
         if not self.supports(model):
             raise TypeError(f"HuginnCDBAdapter does not support model type {type(model)!r}")
         cfg = model.config
-        if cfg.state_init != "zero":
-            raise NotImplementedError("only state_init='zero' is served (the reference's reproducible default)")
+        if cfg.state_init not in ("zero", "random"):
+            raise ValueError(f"state_init must be 'zero' or 'random', got {cfg.state_init!r}")
         self.model = model
         self.config = cfg
         p = next(model.parameters())
         self._dtype, self._device = p.dtype, p.device
+        self._state_generator: torch.Generator | None = None
+        if cfg.state_init == "random" and cfg.state_seed is not None:
+            self._state_generator = torch.Generator(device=self._device)
+            self._state_generator.manual_seed(cfg.state_seed)
         self.E = cfg.n_embd
         self.num_heads = cfg.n_heads
         self.num_kv_heads = cfg.num_key_value_heads
@@ -423,6 +430,18 @@ class HuginnCDBAdapter(CDBModelAdapter):
             self.injection_bank = torch.zeros_like(bank)
         return self.injection_bank
 
+    def _initial_state(self, injection: torch.Tensor) -> torch.Tensor:
+        """The recurrent state a token starts from (modeling_huginn.py:418-427): zeros, or a
+        normal of std sqrt(2 / (5E)) clamped at 3 std and scaled by sqrt(E)."""
+
+        if self.config.state_init == "zero":
+            return torch.zeros_like(injection)
+        std = self.config.state_init_std
+        state = torch.empty_like(injection)
+        state.normal_(mean=0.0, std=std, generator=self._state_generator)
+        state.clamp_(min=-3 * std, max=3 * std)
+        return state.mul_(self.config.embed_scale)
+
     # -- stages --------------------------------------------------------------------------------------------------
     def prelude(self, launch: StageLaunch) -> None:
         n = launch.n
@@ -434,6 +453,9 @@ class HuginnCDBAdapter(CDBModelAdapter):
             attend = self._decode_attend(launch, lambda i: (None, layout.prelude_layer_index(i)))
             x, _ = self._blocks(self.prelude_blocks, x, n1, attend, None)
         torch.ops.cdb.scatter_rows_(inj_bank, launch.slots[:n], x)
+        if self.config.state_init == "random":
+            torch.ops.cdb.scatter_rows_(launch.bank, launch.slots[:n], self._initial_state(x))
+            return
         # Zero initial state (configuration_huginn.py:31-37, modeling_huginn.py:414-427): a negative
         # source index makes the row copy write zeros.
         minus = torch.full((n,), -1, dtype=torch.int64, device=self._device)
@@ -482,7 +504,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             x, _ = self._blocks(self.prelude_blocks, x, n1,
                                 self._prefill_attend(launch, layout.prelude_layer_index), None)
         injection = x
-        state = torch.zeros_like(injection)
+        state = self._initial_state(injection)
         for step in range(self.total_recurrent_steps):
             h = self._core_input(state, injection, None, tokens)
             n1, _ = self._norm(h, self.core_blocks[0]["n1"])

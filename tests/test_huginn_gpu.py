@@ -107,3 +107,52 @@ def test_huginn_bf16_runs_and_tracks_oracle() -> None:
             for p, m, d in zip(prompts, mnt, depths)]
     assert np.mean([o.generated_tokens[0] == w.tokens[0] for o, w in zip(outs, want)]) >= 0.75
     assert all(len(o.generated_tokens) == m for o, m in zip(outs, mnt))
+
+
+def test_random_state_init_is_the_references_truncated_normal() -> None:
+    """state_init="random" (huginn/modeling_huginn.py:418-427): N(0, s) with s = sqrt(2 / (5E)),
+    clamped at 3 s, times sqrt(E). Clamping (not truncating) puts 2 (1 - Phi(3)) = 0.26998% of
+    the draws exactly on the bounds and leaves a standard deviation of 0.99750 s
+    (variance 1 - 6 phi(3) - (1 - 9) 2 (1 - Phi(3)) = 0.995007), so the rows must show
+    sqrt(E) * s * 0.99750, that mass at +-3 s sqrt(E), and nothing beyond."""
+
+    import math
+
+    from continuous_depth_batching_amd.huginn import HuginnCDBAdapter, HuginnForCausalLM
+
+    cfg = tiny_huginn_config(state_init="random", state_seed=3)
+    with torch.device("cuda"):
+        model = HuginnForCausalLM(cfg).float().eval()
+    adapter = HuginnCDBAdapter(model)
+    e = cfg.n_embd
+    s = math.sqrt(2 / (5 * e))
+    x = adapter._initial_state(torch.zeros((8192, e), device="cuda")).double()
+    bound = 3 * s * math.sqrt(e)
+    assert x.abs().max().item() <= bound * (1 + 1e-6)
+    assert abs(x.mean().item()) < 0.01 * s * math.sqrt(e)
+    assert abs(x.std().item() / (s * math.sqrt(e)) - 0.99750) < 0.002
+    at_bound = (x.abs() >= bound * (1 - 1e-6)).double().mean().item()
+    assert abs(at_bound / 0.0026998 - 1) < 0.1
+    # Seeded: a second adapter over the same config draws the same rows.
+    again = HuginnCDBAdapter(model)._initial_state(torch.zeros((8192, e), device="cuda")).double()
+    assert torch.equal(x, again)
+
+
+def test_random_state_init_engine_is_reproducible_under_a_seed() -> None:
+    from continuous_depth_batching_amd.huginn import HuginnForCausalLM
+
+    weights = tiny_huginn_weights(4)
+    prompts, mnt = workload(seed=4, n=4, new_tokens=6)
+    runs = []
+    for seed in (9, 9, 10):
+        with torch.device("cuda"):
+            model = HuginnForCausalLM(tiny_huginn_config(state_init="random", state_seed=seed))
+        model.load_state_dict({k: torch.from_numpy(v) for k, v in weights.items()})
+        engine = make_engine(model.float().eval(), synthetic_exit_replay=True, kv_policy="single",
+                             delay_gate_consumption=False)
+        depths = [[1] * (m - 1) for m in mnt]
+        outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=None, exit_depths=depths)
+        runs.append([o.generated_tokens for o in outs])
+    assert runs[0] == runs[1]
+    assert all(0 <= t < T["vocab"] for ts in runs[0] for t in ts)
+    assert runs[2] != runs[0]  # another seed starts every token from another state

@@ -104,15 +104,20 @@ class KvSwapPool:
         return out
 
     def _upload_index(self, device_blocks: list[int]) -> torch.Tensor:
-        """Device rows of every slab of ``device_blocks``, block-major, on the compute stream."""
+        """Device rows of every slab of ``device_blocks``, block-major, on the compute stream.
 
-        n = len(device_blocks)
+        A restore moves every request restored in a tick at once, so the index buffers grow
+        past one request's blocks when needed."""
+
         blocks = np.asarray(device_blocks, dtype=np.int64)
-        if n > self.cache.max_blocks_per_request or blocks.min() < 0 or blocks.max() >= self.cache.num_blocks:
+        if blocks.min() < 0 or blocks.max() >= self.cache.num_blocks:
             raise ValueError(f"device blocks out of range for the KV pool: {device_blocks}")
         rows = (np.arange(self.slabs, dtype=np.int64)[None, :] * self.plane_blocks + blocks[:, None]).reshape(-1)
         if self._index_event is not None:
             self._index_event.synchronize()  # the previous upload has left the pinned buffer
+        if rows.size > self._index_host.numel():
+            self._index_host = torch.empty(rows.size, dtype=torch.int64, pin_memory=True)
+            self._index_dev = torch.empty(rows.size, dtype=torch.int64, device=self.cache.device)
         self._index_host.numpy()[: rows.size] = rows
         dev = self._index_dev[: rows.size]
         dev.copy_(self._index_host[: rows.size], non_blocking=True)

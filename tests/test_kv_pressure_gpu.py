@@ -63,6 +63,28 @@ def test_swap_pool_round_trip_is_bit_exact(monkeypatch) -> None:
     assert not back[:, :, untouched].any()
 
 
+def test_swap_pool_moves_more_blocks_than_one_request_holds() -> None:
+    """A restore batches every request restored in a tick: 100 blocks through a pool whose
+    requests hold at most 64."""
+
+    cache = _cache(num_blocks=240, block_size=16, policy="single")
+    assert cache.max_blocks_per_request == 64
+    pool = KvSwapPool(cache, num_host_blocks=120)
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    cache.pool.copy_(torch.randn(cache.pool.shape, generator=gen, device="cuda").to(torch.bfloat16))
+    before = cache.pool.clone()
+    src = list(range(0, 200, 2))                 # 100 scattered device blocks
+    host = list(range(10, 110))
+    pool.swap_out(src[:50], host[:50])           # two requests' swap-outs
+    pool.swap_out(src[50:], host[50:])
+    dst = list(range(1, 201, 2))
+    pool.swap_in(host, dst)                      # one batched restore of both
+    torch.cuda.synchronize()
+    pages = lambda t: t.view(cache.num_layers, 2, -1, 16, 2, 64)
+    assert torch.equal(pages(cache.pool)[:, :, dst], pages(before)[:, :, src])
+    assert torch.equal(pages(cache.pool)[:, :, src], pages(before)[:, :, src])  # sources untouched
+
+
 def test_swap_pool_rejects_out_of_range_blocks() -> None:
     cache = _cache(num_blocks=8, block_size=16, policy="single")
     pool = KvSwapPool(cache, num_host_blocks=4)

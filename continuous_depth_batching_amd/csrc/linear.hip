@@ -258,7 +258,9 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
   // Workgroups that share a (column range, K split) -- all its row ranges -- sit on one XCD.
-  const int n_tiles = p.N / (64 * NTW);
+  // N is a multiple of 16; the last column range may cover fewer than 4 * NTW 16-column
+  // tiles, and the waves past N load the last tile (in bounds) and store nothing.
+  const int n_tiles = (p.N / 16 + 4 * NTW - 1) / (4 * NTW);
   const int m_tiles = (p.M + ROWS - 1) / ROWS;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int mi = q % m_tiles;
@@ -276,11 +278,13 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   const int tile_steps = p.K / 32;  // steps of one packed weight tile
   const int k_first = ks * KSTEPS;
   const bf16_t* wp[NT];
+  const int last_tile = p.N / 16 - 1;
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    wp[j] = p.w + ((int64_t)(n0 / 16 + wave * NTW + j) * tile_steps + k_first) * 512 + 8 * lane;
+    const int tile = min(n0 / 16 + wave * NTW + j, last_tile);
+    wp[j] = p.w + ((int64_t)tile * tile_steps + k_first) * 512 + 8 * lane;
     if constexpr (GATED)
-      wp[NTW + j] = p.w + ((int64_t)((p.N + n0) / 16 + wave * NTW + j) * tile_steps + k_first) * 512 + 8 * lane;
+      wp[NTW + j] = p.w + ((int64_t)(p.N / 16 + tile) * tile_steps + k_first) * 512 + 8 * lane;
   }
   // x staging: thread unit u reads 16 bytes of one row (units of a row are
   // consecutive, so the global reads coalesce) and stores them to that row's
@@ -372,6 +376,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     if constexpr (KSPLIT > 1) {
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
+        if (n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
         float* dst = p.parts + ((int64_t)ks * p.M + m) * p.N + n0 + 16 * (wave * NTW + j) + 4 * (lane >> 4);
         *reinterpret_cast<f32x4_t*>(dst) = acc[j][mt];
       }
@@ -379,6 +384,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     }
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
+      if (n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
       Vec<bf16_t, 4> o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -397,8 +403,8 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
 
 template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1>
 int launch_linear_wide(LinearParams prm, hipStream_t stream) {
-  if (prm.N % (64 * NTW) || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
-  const int n_tiles = prm.N / (64 * NTW);
+  if (prm.N % 16 || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
+  const int n_tiles = (prm.N / 16 + 4 * NTW - 1) / (4 * NTW);  // as the kernel counts column ranges
   const int m_tiles = (prm.M + 16 * MT - 1) / (16 * MT);
   const int pairs = n_tiles * KSPLIT;
   hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT>),
@@ -584,9 +590,17 @@ int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
 // parallelism buys) up to 128 rows, four for the 5632-wide one up to 256.
 // Returns 0 for shapes without a split form.
 int parts_splits(int64_t rows, int32_t out_features, int32_t in_features) {
-  if (rows < 1 || out_features < 64 || out_features % 64) return 0;
-  if (in_features == 2048) return rows <= 64 ? 4 : rows <= 128 ? 2 : 0;
-  if (in_features == 5632) return rows <= kLinearWideMaxRows ? 4 : 0;
+  if (rows < 1 || rows > kLinearWideMaxRows || out_features < 64 || out_features % 16) return 0;
+  if (out_features % 64 == 0) {
+    if (in_features == 2048) return rows <= 64 ? 4 : rows <= 128 ? 2 : 0;
+    if (in_features == 5632) return 4;
+  }
+  // The Huginn O (5280 -> 5280) and down (17920 -> 5280) projections: 5280 columns are
+  // 82.5 column ranges of 64, so the last range is half full. Split counts from the same
+  // cold-weight sweep: three ranges for the 5280-wide input; eight for the 17920-wide one
+  // up to 64 rows, four above.
+  if (in_features == 5280) return 3;
+  if (in_features == 17920) return rows <= 64 ? 8 : 4;
   return 0;
 }
 
@@ -596,9 +610,21 @@ int dispatch_parts(const LinearParams& prm, hipStream_t stream) {
     if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 16, 4>(prm, stream);
     return launch_linear_wide<2, 1, 4, 4, false, 32, 2>(prm, stream);
   }
-  if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 44, 4>(prm, stream);
-  if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 44, 4>(prm, stream);
-  return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
+  if (prm.K == 5632) {
+    if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 44, 4>(prm, stream);
+    if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 44, 4>(prm, stream);
+    return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
+  }
+  if (prm.K == 5280) {
+    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 55, 3>(prm, stream);
+    return launch_linear_wide<4, 1, 2, 4, false, 55, 3>(prm, stream);
+  }
+  if (prm.K == 17920) {
+    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 70, 8>(prm, stream);
+    if (prm.M <= 64) return launch_linear_wide<4, 1, 2, 4, false, 70, 8>(prm, stream);
+    return launch_linear_wide<4, 1, 2, 4, false, 140, 4>(prm, stream);
+  }
+  return CDB_ERR_SHAPE;
 }
 
 int dispatch_linear(const LinearParams& prm, bool gated, hipStream_t stream) {

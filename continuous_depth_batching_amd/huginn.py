@@ -347,12 +347,14 @@ class HuginnCDBAdapter(CDBModelAdapter):
         for i, w in enumerate(blocks):
             qkv = ops.linear_auto(n1, w["wqkv"], w["pqkv"], False)
             a = attend(i, w, qkv)
-            o = ops.linear_auto(a.view(rows, self.q_width), w["wo"], w["po"], False)
-            x1, y = self._norm(o, w["n2"], w["n3"], residual=x)
+            # O and down feed the sandwich norms; shapes with a split-K form hand the norm fp32
+            # partials instead of a stored projection.
+            x1, y = ops.linear_residual_rmsnorm_auto(a.view(rows, self.q_width), w["wo"], w["po"], x, w["n2"],
+                                                     w["n3"], self.eps, self.eps, ops.NORM_HUGINN_SANDWICH)
             act = ops.linear_auto(y, w["wgu"], w["pgu"], True)
-            m = ops.linear_auto(act, w["wd"], w["pd"], False)
             nxt = blocks[i + 1]["n1"] if i + 1 < len(blocks) else final_norm
-            x, n1 = self._norm(m, w["n4"], nxt, residual=x1)
+            x, n1 = ops.linear_residual_rmsnorm_auto(act, w["wd"], w["pd"], x1, w["n4"], nxt, self.eps, self.eps,
+                                                     ops.NORM_HUGINN_SANDWICH)
             y_last = n1
         return x, y_last
 

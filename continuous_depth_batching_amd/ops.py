@@ -495,9 +495,10 @@ def rmsnorm_fused_parts_raw(parts: torch.Tensor, residual: torch.Tensor | None, 
 
 
 def linear_residual_rmsnorm_auto(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor | None,
-                                 residual: torch.Tensor, w_a: torch.Tensor, w_b: torch.Tensor, eps_a: float,
-                                 eps_b: float, mode: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """The body of cdb::linear_residual_rmsnorm, callable without op dispatch."""
+                                 residual: torch.Tensor, w_a: torch.Tensor, w_b: torch.Tensor | None, eps_a: float,
+                                 eps_b: float, mode: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """The body of cdb::linear_residual_rmsnorm, callable without op dispatch; without ``w_b``
+    the second norm is skipped and y is None."""
 
     rows, in_features = x.shape
     out_features = weight.shape[0]
@@ -506,7 +507,7 @@ def linear_residual_rmsnorm_auto(x: torch.Tensor, weight: torch.Tensor, packed: 
             and x.data_ptr() % 16 == 0 and residual.is_contiguous()):
         splits = linear_parts_splits(rows, out_features, in_features)
     h = x.new_empty((rows, out_features))
-    y = x.new_empty((rows, out_features))
+    y = x.new_empty((rows, out_features)) if w_b is not None else None
     if splits:
         parts = torch.empty((splits, rows, out_features), dtype=torch.float32, device=x.device)
         linear_parts_raw(x, packed, parts)

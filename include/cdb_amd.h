@@ -217,7 +217,9 @@ int cdb_linear(const void* x, int64_t ldx, const void* w_packed, void* y, int64_
  * or 0 when it has no split form for it (then use cdb_linear or a library GEMM).
  * Split forms exist for bf16 with in_features 2048 (up to 128 rows) or 5632 (up
  * to 256 rows) and out_features a multiple of 64 -- the Ouro O and down
- * projections (ouro/modeling_ouro.py:168,431). */
+ * projections (ouro/modeling_ouro.py:168,431) -- and with in_features 5280 or
+ * 17920 (up to 256 rows) and out_features a multiple of 16 -- the Huginn O and
+ * down projections (huginn/modeling_huginn.py:242,302,311,316). */
 int32_t cdb_linear_parts_splits(int64_t rows, int32_t out_features, int32_t in_features, int32_t dtype);
 
 /* Split-K projection: parts[s, r, n] = fp32 sum over k in the s-th of

@@ -157,7 +157,11 @@ def test_pack_layout_is_the_mfma_operand_order(n: int, k: int) -> None:
 
 
 PARTS_CASES = [(r, k, n) for r in (1, 5, 16, 32, 33, 64, 65, 128) for k, n in ((2048, 2048), (5632, 2048))] + [
-    (r, 5632, n) for r in (129, 200, 256) for n in (2048, 64)] + [(40, 2048, 1024), (3, 5632, 192)]
+    (r, 5632, n) for r in (129, 200, 256) for n in (2048, 64)] + [(40, 2048, 1024), (3, 5632, 192)] + [
+    # Huginn O and down: 5280 output columns end in a half-full 64-column range; 80 columns
+    # leave the last range one 16-column tile wide.
+    (r, 5280, 5280) for r in (1, 16, 40, 64, 100, 128, 256)] + [
+    (r, 17920, 5280) for r in (1, 33, 128, 256)] + [(20, 5280, 80), (70, 17920, 112)]
 
 
 @pytest.mark.parametrize("rows,k,n", PARTS_CASES)
@@ -165,7 +169,7 @@ def test_split_k_partials_sum_to_the_fp32_product(rows: int, k: int, n: int) -> 
     from continuous_depth_batching_amd import ops
 
     splits = ops.linear_parts_splits(rows, n, k)
-    assert splits in (2, 4)
+    assert splits in (2, 3, 4, 8)
     x, w = _inputs(rows, k, n, seed=rows * 11 + k + n)
     parts = torch.full((splits, rows, n), float("nan"), device="cuda")
     ops.linear_parts_raw(x, ops.pack_linear_weight(w), parts)
@@ -186,14 +190,14 @@ def test_split_k_partials_sum_to_the_fp32_product(rows: int, k: int, n: int) -> 
     _check_rounded(total.bfloat16(), x.float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x, w))
 
 
-@pytest.mark.parametrize("rows,k", [(1, 2048), (16, 5632), (33, 2048), (96, 5632), (128, 2048), (256, 5632)])
-def test_norm_from_partials_is_the_two_step_result(rows: int, k: int) -> None:
+@pytest.mark.parametrize("rows,k,n", [(1, 2048, 2048), (16, 5632, 2048), (33, 2048, 2048), (96, 5632, 2048),
+                                      (128, 2048, 2048), (256, 5632, 2048), (7, 5280, 5280), (128, 17920, 5280)])
+def test_norm_from_partials_is_the_two_step_result(rows: int, k: int, n: int) -> None:
     """Partials added in order and rounded once, then the sandwich norm: bit-identical to
     running the fused norm on that rounded projection output."""
 
     from continuous_depth_batching_amd import ops
 
-    n = 2048
     x, w = _inputs(rows, k, n, seed=rows + 3 * k)
     g = torch.Generator(device="cuda")
     g.manual_seed(rows)
@@ -214,6 +218,9 @@ def test_norm_from_partials_is_the_two_step_result(rows: int, k: int) -> None:
         assert torch.equal(h, h_ref) and torch.equal(y, y_ref)
         h2, y2 = ops.linear_residual_rmsnorm_auto(x, w, packed, residual, w_a, w_b, 1e-6, 1e-5, mode)
         assert torch.equal(h, h2) and torch.equal(y, y2)
+        h3, y3 = ops.linear_residual_rmsnorm_auto(x, w, packed, residual, w_a, None, 1e-6, 1e-5, mode)
+        torch.cuda.synchronize()
+        assert y3 is None and torch.equal(h3, h_ref)
 
 
 def test_linear_residual_rmsnorm_falls_back_without_a_split_form() -> None:

@@ -243,7 +243,9 @@ CDB_DEVICE int x_slot(int r, int t, int g) {
 // KSPLIT > 1: K is cut into KSPLIT ranges of KSTEPS steps; each workgroup covers
 // one range and stores fp32 partial sums to p.parts[split], for a consumer that
 // adds them in split order and rounds once (the residual RMSNorm).
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1>
+// NTAIL: N is a multiple of 16 but not of 64 * NTW, so the last column range is
+// narrower; without it N must be a multiple of 64 * NTW.
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false>
 __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   constexpr int NT = GATED ? 2 * NTW : NTW;
   constexpr int ROWS = 16 * MT;
@@ -258,9 +260,9 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
 
   // Workgroups that share a (column range, K split) -- all its row ranges -- sit on one XCD.
-  // N is a multiple of 16; the last column range may cover fewer than 4 * NTW 16-column
-  // tiles, and the waves past N load the last tile (in bounds) and store nothing.
-  const int n_tiles = (p.N / 16 + 4 * NTW - 1) / (4 * NTW);
+  // With NTAIL the last column range may cover fewer than 4 * NTW 16-column tiles, and
+  // the waves past N load the last tile (in bounds) and store nothing.
+  const int n_tiles = NTAIL ? (p.N / 16 + 4 * NTW - 1) / (4 * NTW) : p.N / (64 * NTW);
   const int m_tiles = (p.M + ROWS - 1) / ROWS;
   const int xcd = blockIdx.x & 7, q = blockIdx.x >> 3;
   const int mi = q % m_tiles;
@@ -278,13 +280,13 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   const int tile_steps = p.K / 32;  // steps of one packed weight tile
   const int k_first = ks * KSTEPS;
   const bf16_t* wp[NT];
-  const int last_tile = p.N / 16 - 1;
 #pragma unroll
   for (int j = 0; j < NTW; ++j) {
-    const int tile = min(n0 / 16 + wave * NTW + j, last_tile);
+    const int tile = NTAIL ? min(n0 / 16 + wave * NTW + j, p.N / 16 - 1) : n0 / 16 + wave * NTW + j;
     wp[j] = p.w + ((int64_t)tile * tile_steps + k_first) * 512 + 8 * lane;
     if constexpr (GATED)
-      wp[NTW + j] = p.w + ((int64_t)(p.N / 16 + tile) * tile_steps + k_first) * 512 + 8 * lane;
+      wp[NTW + j] = p.w + ((int64_t)(NTAIL ? p.N / 16 + tile : (p.N + n0) / 16 + wave * NTW + j) * tile_steps +
+                           k_first) * 512 + 8 * lane;
   }
   // x staging: thread unit u reads 16 bytes of one row (units of a row are
   // consecutive, so the global reads coalesce) and stores them to that row's
@@ -376,7 +378,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     if constexpr (KSPLIT > 1) {
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
-        if (n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
+        if (NTAIL && n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
         float* dst = p.parts + ((int64_t)ks * p.M + m) * p.N + n0 + 16 * (wave * NTW + j) + 4 * (lane >> 4);
         *reinterpret_cast<f32x4_t*>(dst) = acc[j][mt];
       }
@@ -384,7 +386,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     }
 #pragma unroll
     for (int j = 0; j < NTW; ++j) {
-      if (n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
+      if (NTAIL && n0 + 16 * (wave * NTW + j) >= p.N) continue;  // wave-uniform: a tile past N
       Vec<bf16_t, 4> o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -401,13 +403,13 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   }
 }
 
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1>
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false>
 int launch_linear_wide(LinearParams prm, hipStream_t stream) {
-  if (prm.N % 16 || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
-  const int n_tiles = (prm.N / 16 + 4 * NTW - 1) / (4 * NTW);  // as the kernel counts column ranges
+  if ((NTAIL ? prm.N % 16 : prm.N % (64 * NTW)) || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
+  const int n_tiles = NTAIL ? (prm.N / 16 + 4 * NTW - 1) / (4 * NTW) : prm.N / (64 * NTW);  // as the kernel counts
   const int m_tiles = (prm.M + 16 * MT - 1) / (16 * MT);
   const int pairs = n_tiles * KSPLIT;
-  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT>),
+  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT, NTAIL>),
                      dim3((pairs + 7) / 8 * 8 * m_tiles), dim3(256), 0, stream, prm);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
@@ -616,13 +618,13 @@ int dispatch_parts(const LinearParams& prm, hipStream_t stream) {
     return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
   }
   if (prm.K == 5280) {
-    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 55, 3>(prm, stream);
-    return launch_linear_wide<4, 1, 2, 4, false, 55, 3>(prm, stream);
+    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 55, 3, true>(prm, stream);
+    return launch_linear_wide<4, 1, 2, 4, false, 55, 3, true>(prm, stream);
   }
   if (prm.K == 17920) {
-    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 70, 8>(prm, stream);
-    if (prm.M <= 64) return launch_linear_wide<4, 1, 2, 4, false, 70, 8>(prm, stream);
-    return launch_linear_wide<4, 1, 2, 4, false, 140, 4>(prm, stream);
+    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 70, 8, true>(prm, stream);
+    if (prm.M <= 64) return launch_linear_wide<4, 1, 2, 4, false, 70, 8, true>(prm, stream);
+    return launch_linear_wide<4, 1, 2, 4, false, 140, 4, true>(prm, stream);
   }
   return CDB_ERR_SHAPE;
 }

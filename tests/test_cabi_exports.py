@@ -180,3 +180,23 @@ def test_linear_argument_errors_without_gpu() -> None:
     assert am(embed=fake) == _lib.CDB_ERR_NULL                       # the fused prelude needs bank and slots
     assert am(embed=fake, bank=fake, bank_slots=fake, bank_rows=512, width=2044) == _lib.CDB_ERR_SHAPE
     assert am(embed=fake, bank=fake, bank_slots=fake, bank_rows=0, width=2048) == _lib.CDB_ERR_SHAPE
+
+
+def test_split_k_table_without_gpu() -> None:
+    """cdb_linear_parts_splits is host arithmetic: the split forms of the Ouro O/down
+    (2048 and 5632 inputs) and Huginn O/down (5280 and 17920 inputs) projections."""
+
+    lib = _lib.lib()
+    bf16 = _lib.CDB_DTYPE_BF16
+    cases = {
+        (16, 2048, 2048): 4, (64, 2048, 2048): 4, (128, 2048, 2048): 2, (129, 2048, 2048): 0,
+        (1, 2048, 5632): 4, (256, 2048, 5632): 4, (257, 2048, 5632): 0,
+        (16, 5280, 5280): 3, (128, 5280, 5280): 3, (256, 5280, 5280): 3,
+        (16, 5280, 17920): 8, (64, 5280, 17920): 8, (65, 5280, 17920): 4, (128, 5280, 17920): 4,
+        (64, 2040, 2048): 0,   # out_features not a multiple of 16
+        (64, 5280, 4096): 0,   # no split form for this input width
+        (0, 2048, 2048): 0,
+    }
+    got = {key: lib.cdb_linear_parts_splits(*key, bf16) for key in cases}
+    assert got == cases
+    assert lib.cdb_linear_parts_splits(16, 2048, 2048, _lib.CDB_DTYPE_F32) == 0

@@ -604,6 +604,9 @@ def main() -> int:
         kv_pressure_mode="none")
     engine = ContinuousDepthBatchingEngine.from_model(model, engine_cfg)
     engine.runner.capture_all_buckets()
+    # The reference's steady-state window (benchmarks/runner.py:592-596): opens once twice the
+    # resident cap of requests have completed while prompts still wait.
+    engine.scheduler.steady_warmup_requests = 2 * engine_cfg.max_num_seqs
     for _ in range(args.warmup):
         k = min(32, len(prompts))
         engine.generate_batch(prompts[:k], max_new_tokens=[min(o, 24) for o in outputs[:k]], eos_token_id=None,
@@ -644,6 +647,9 @@ def main() -> int:
                    "coda_batches": stats.coda_batches, "prefill_batches": stats.prefill_batches,
                    "recurrent_steps": stats.recurrent_steps, "skipped_recurrent_steps": stats.skipped_recurrent_steps,
                    "graph_captures_in_timed_run": stats.recurrent_graph_captures},
+        "steady_window": engine.scheduler.steady_state_summary(),
+        "steady_window_note": "the reference's steady-state window (after 2 x max_num_seqs completions, while "
+                              "prompts wait); this batch admits every sequence at once, so it has none",
     })
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, prompts, outputs, depths, args.cpu_sample_tokens)

@@ -241,6 +241,7 @@ class ContinuousDepthBatchingEngine:
                     self._run_no_refill_loop()
         finally:
             self.runner.synchronize()
+            self.scheduler.close_steady_window()
             self.scheduler.free_unfinished_requests()
         outputs = [self.finished_outputs[s.request_id] for s in states]
         self.last_stats.generated_tokens = sum(len(o.generated_tokens) for o in outputs)

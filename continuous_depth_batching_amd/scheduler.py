@@ -12,6 +12,7 @@ budgets and block allocation follow scheduler_base.py:171-545.
 
 from __future__ import annotations
 
+import time
 from collections import deque
 from dataclasses import dataclass
 from itertools import islice
@@ -59,6 +60,8 @@ class CDBScheduler:
         self.min_free_slots = resolve_min_free_slots(min_free_slots, self.max_num_seqs)
         self.max_recurrent_steps = max_recurrent_steps
         self.min_coda_batch_size = min(min_coda_batch_size, self.max_num_seqs)
+        # Completions before the steady-state window opens (steady_state_summary); None leaves it off.
+        self.steady_warmup_requests: int | None = None
         if kv_pressure_mode == "reserve":
             if max_model_len is None:
                 raise ValueError("kv_pressure_mode='reserve' requires max_model_len")
@@ -86,6 +89,12 @@ class CDBScheduler:
         self.resident_sum = 0
         self.completed_requests = 0
         self.completed_generated_tokens = 0
+        self._steady_start_time: float | None = None
+        self._steady_end_time: float | None = None
+        self._steady_start_progress = (0, 0)
+        self._steady_end_progress = (0, 0)
+        self._steady_ticks = 0
+        self._steady_resident_sum = 0
 
     # -- bookkeeping -------------------------------------------------------------------------------------------
     def add_waiting_request(self, state: RequestState) -> None:
@@ -103,6 +112,59 @@ class CDBScheduler:
         self.max_resident_requests = max(self.max_resident_requests, resident)
         self.resident_samples += 1
         self.resident_sum += resident
+        self._advance_steady_window(resident)
+
+    # -- steady-state window (scheduler_base.py:315-398) --------------------------------------------------------
+    @property
+    def steady_window_open(self) -> bool:
+        return self._steady_start_time is not None and self._steady_end_time is None
+
+    def _advance_steady_window(self, resident: int) -> None:
+        """Open the window on the tick ``steady_warmup_requests`` requests have completed while prompts
+        still wait; close it on the first tick after the last admission (which belongs to the drain)."""
+
+        if self.steady_warmup_requests is None or self._steady_end_time is not None:
+            return
+        if self._steady_start_time is None:
+            if self.completed_requests < self.steady_warmup_requests or not self.waiting_requests:
+                return
+            self._steady_start_time = time.perf_counter()
+            self._steady_start_progress = self._progress_snapshot()
+        elif not self.waiting_requests:
+            self.close_steady_window()
+            return
+        self._steady_ticks += 1
+        self._steady_resident_sum += resident
+
+    def _progress_snapshot(self) -> tuple[int, int]:
+        """Requests completed and tokens generated so far, resident and re-queued requests included."""
+
+        generated = self.completed_generated_tokens
+        generated += sum(state.total_generated_len() for state in self.active_requests.values())
+        generated += sum(state.total_generated_len() for state in self.waiting_requests.values())
+        return self.completed_requests, generated
+
+    def close_steady_window(self) -> None:
+        if self._steady_start_time is None or self._steady_end_time is not None:
+            return
+        self._steady_end_time = time.perf_counter()
+        self._steady_end_progress = self._progress_snapshot()
+
+    def steady_state_summary(self) -> dict | None:
+        """Throughput inside the steady-state window, or None when the run held no such window
+        (the warm-up count was never reached, or only while draining, or nothing completed)."""
+
+        if self._steady_start_time is None or self._steady_end_time is None:
+            return None
+        window_s = self._steady_end_time - self._steady_start_time
+        completed = self._steady_end_progress[0] - self._steady_start_progress[0]
+        generated = self._steady_end_progress[1] - self._steady_start_progress[1]
+        if window_s <= 0.0 or completed <= 0:
+            return None
+        return {"warmup_requests": self.steady_warmup_requests, "window_s": window_s, "ticks": self._steady_ticks,
+                "completed_requests": completed, "generated_tokens": generated,
+                "requests_per_second": completed / window_s, "generated_tokens_per_second": generated / window_s,
+                "mean_resident_requests": self._steady_resident_sum / self._steady_ticks if self._steady_ticks else 0.0}
 
     def record_completion(self, state: RequestState) -> None:
         self.completed_requests += 1

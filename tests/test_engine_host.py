@@ -383,3 +383,25 @@ def test_no_refill_matches_refill_on_the_delayed_horizon() -> None:
     assert wave.last_stats.scheduler_refills == 0
     assert wave.last_stats.exit_depth_histogram == refill.last_stats.exit_depth_histogram
     assert wave.last_stats.recurrent_steps == refill.last_stats.recurrent_steps
+
+
+def test_steady_window_opens_after_warmup_and_closes_after_the_last_admission() -> None:
+    # scheduler_base.py:315-398: the window opens on the tick the warm-up count of requests has
+    # completed while prompts still wait, and closes on the first tick after the last admission.
+    prompts = [[1 + i, 2] for i in range(8)]
+    depths = [[1, 0, 2] for _ in range(8)]
+    engine = make_engine(synthetic_exit_replay=True, max_num_seqs=2, num_blocks=64, max_model_len=32)
+    engine.scheduler.steady_warmup_requests = 2
+    generate(engine, prompts, 4, exit_depths=depths)
+    summary = engine.scheduler.steady_state_summary()
+    assert summary is not None
+    assert 0 < summary["completed_requests"] < 8 and summary["generated_tokens"] > 0
+    assert 0 < summary["mean_resident_requests"] <= 2 and summary["ticks"] > 0
+    assert not engine.scheduler.steady_window_open
+    # No warm-up count, or every prompt admitted at once: no window.
+    generate(make_engine(synthetic_exit_replay=True), prompts, 4, exit_depths=depths)
+    wide = make_engine(synthetic_exit_replay=True, num_blocks=64, max_model_len=32, max_num_batched_tokens=16,
+                       max_num_seqs=8)
+    wide.scheduler.steady_warmup_requests = 2
+    generate(wide, prompts, 4, exit_depths=depths)
+    assert wide.scheduler.steady_state_summary() is None

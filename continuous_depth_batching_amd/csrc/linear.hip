@@ -568,10 +568,16 @@ int dispatch_rows(const LinearParams& prm, bool gated, int max_waves, hipStream_
 // of 4096+ columns (the Ouro-1.4B QKV and gate/up projections). Tiles from a
 // sweep over (row tiles, column tiles, chunk, stages) with cold weights.
 bool wide_path(const LinearParams& prm) {
+  // 5280-wide inputs (the Huginn QKV and gate/up projections) between 65 and 128 rows.
+  if (prm.K == 5280) return prm.M > 64 && prm.M <= 128 && prm.N >= 4096 && prm.N % 16 == 0;
   return prm.M > 32 && prm.M <= kLinearWideMaxRows && prm.K == 2048 && prm.N >= 4096 && prm.N % 128 == 0;
 }
 
 int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
+  if (prm.K == 5280) {  // 128-row tiles, from a cold-weight sweep at 64-128 rows
+    return gated ? launch_linear_wide<8, 1, 2, 4, true, 165, 1, true>(prm, stream)
+                 : launch_linear_wide<8, 1, 2, 4, false, 165, 1, true>(prm, stream);
+  }
   if (prm.M <= 64) {
     return gated ? launch_linear_wide<2, 1, 4, 4, true, 64>(prm, stream)
                  : launch_linear_wide<2, 1, 4, 4, false, 64>(prm, stream);

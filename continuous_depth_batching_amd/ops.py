@@ -395,14 +395,17 @@ def linear_prefers_kernel(rows: int, out_features: int, gated: bool, in_features
     """Whether cdb_linear beats torch.mm for this batch (measured on cold weights): always
     up to 32 rows; up to 64 for the gated MLP projection (its fused SiLU saves a pass) and
     for outputs of 4096 to 16384 columns; and up to 256 rows on the wide-tile kernel for
-    2048-wide inputs with such outputs (a multiple of 128 columns). The LM head (49152
-    columns) above 32 rows is faster on hipBLASLt, as are O and down projections."""
+    2048-wide inputs with such outputs (a multiple of 128 columns), and up to 128 rows for
+    5280-wide inputs with at least 4096 outputs. The LM head (49152 columns) above 32 rows
+    is faster on hipBLASLt, as are O and down projections."""
 
     if 1 <= rows <= 32:
         return True
     mid = 4096 <= out_features <= 16384
     if rows <= LINEAR_MAX_ROWS and (gated or mid):
         return True
+    if in_features == 5280:  # Huginn QKV and gate/up on the wide-tile kernel up to 128 rows
+        return rows <= 128 and out_features >= 4096
     return rows <= LINEAR_WIDE_MAX_ROWS and mid and out_features % 128 == 0 and in_features == 2048
 
 

@@ -64,7 +64,8 @@ def test_linear_matches_rounded_fp32_product(rows: int, k: int, n: int) -> None:
     _check_rounded(y, ref, max_mismatch=0.01, extra=_sum_error(x, w))
 
 
-@pytest.mark.parametrize("rows,k,n", [(r, 2048, n) for r in (33, 65, 96, 128, 129, 200, 256) for n in (6144, 4096)])
+@pytest.mark.parametrize("rows,k,n", [(r, 2048, n) for r in (33, 65, 96, 128, 129, 200, 256) for n in (6144, 4096)]
+                         + [(r, 5280, 15840) for r in (65, 100, 128)])
 def test_wide_tile_path_matches_rounded_fp32_product(rows: int, k: int, n: int) -> None:
     """Batches above 32 rows with 2048-wide inputs and 4096+ outputs take the wide-tile kernel."""
 

@@ -200,7 +200,8 @@ int cdb_linear_pack_weight(const void* w, int64_t ldw, void* w_packed, int64_t r
 /* Dense projection of a decode batch: y[r, n] = R(sum_k x[r, k] * w[n, k]) for
  * r < rows, n < out_features, bf16 only (fp32 accumulation, one rounding),
  * with w given packed by cdb_linear_pack_weight. rows <= 64, or up to 256 when
- * in_features is 2048 and out_features a multiple of 128 of at least 4096 (a
+ * in_features is 2048 and out_features a multiple of 128 of at least 4096, or
+ * up to 128 when in_features is 5280 and out_features at least 4096 (a
  * wide-tile kernel); other shapes above 64 rows return CDB_ERR_SHAPE.
  * Replaces the nn.Linear calls of a recurrent step (ouro/modeling_ouro.py:162-168,
  * :371-374,390-392,431; huginn/modeling_huginn.py:239-242,310-316,372).

@@ -620,6 +620,7 @@ def main() -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     stats = engine.last_stats
+    steady = engine.scheduler.steady_state_summary()
     value = generated / elapsed
     result.update({
         "metric": "output tok/s, Ouro-1.4B-shape CDB decode bs=256; decode-attn HBM GB/s % of peak",
@@ -647,10 +648,11 @@ def main() -> int:
                    "coda_batches": stats.coda_batches, "prefill_batches": stats.prefill_batches,
                    "recurrent_steps": stats.recurrent_steps, "skipped_recurrent_steps": stats.skipped_recurrent_steps,
                    "graph_captures_in_timed_run": stats.recurrent_graph_captures},
-        "steady_window": engine.scheduler.steady_state_summary(),
-        "steady_window_note": "the reference's steady-state window (after 2 x max_num_seqs completions, while "
-                              "prompts wait); this batch admits every sequence at once, so it has none",
+        "steady_window": steady,
     })
+    if steady is None:
+        result["steady_window_note"] = ("the reference's steady-state window (after 2 x max_num_seqs completions, "
+                                        "while prompts wait) never opened: no prompt was still waiting by then")
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, prompts, outputs, depths, args.cpu_sample_tokens)
     print(json.dumps(result), flush=True)

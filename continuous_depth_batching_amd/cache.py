@@ -131,12 +131,12 @@ class PagedKVCache:
     def allocate_blocks(self, n_blocks: int, request_id: str, allocated_blocks: int) -> int | None:
         if not self.will_allocation_be_successful(n_blocks, allocated_blocks):
             return None
+        if len(self.block_table.get(request_id, ())) + n_blocks > self.table_width:
+            raise ValueError(f"Request {request_id} needs more than {self.table_width} blocks (max_model_len)")
         blocks = self._block_manager.get_free_blocks(n_blocks)
         if blocks is None:
             raise ValueError(f"Failed to allocate {n_blocks} blocks for request {request_id}")
         owned = self.block_table.setdefault(request_id, [])
-        if len(owned) + n_blocks > self.table_width:
-            raise ValueError(f"Request {request_id} needs more than {self.table_width} blocks (max_model_len)")
         row = self.table_row_of.get(request_id)
         if row is None:
             if not self._free_table_rows:

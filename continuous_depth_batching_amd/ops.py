@@ -396,8 +396,8 @@ def linear_prefers_kernel(rows: int, out_features: int, gated: bool, in_features
     up to 32 rows; up to 64 for the gated MLP projection (its fused SiLU saves a pass) and
     for outputs of 4096 to 16384 columns; and up to 256 rows on the wide-tile kernel for
     2048-wide inputs with such outputs (a multiple of 128 columns), and up to 128 rows for
-    5280-wide inputs with at least 4096 outputs. The LM head (49152 columns) above 32 rows
-    is faster on hipBLASLt, as are O and down projections."""
+    5280-wide inputs with such outputs or a gated one. The LM heads (49152 and 65536
+    columns) above 32 rows are faster on hipBLASLt, as are O and down projections."""
 
     if 1 <= rows <= 32:
         return True
@@ -405,7 +405,7 @@ def linear_prefers_kernel(rows: int, out_features: int, gated: bool, in_features
     if rows <= LINEAR_MAX_ROWS and (gated or mid):
         return True
     if in_features == 5280:  # Huginn QKV and gate/up on the wide-tile kernel up to 128 rows
-        return rows <= 128 and out_features >= 4096
+        return rows <= 128 and (gated or mid)
     return rows <= LINEAR_WIDE_MAX_ROWS and mid and out_features % 128 == 0 and in_features == 2048
 
 

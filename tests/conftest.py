@@ -20,11 +20,10 @@ if str(REPO) not in sys.path:
 def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line("markers", "gpu: needs a HIP GPU and the built libcdb_amd.so")
     # The engine's host tick core is a small g++-built CPython extension that every engine test
-    # imports; a tree where it was never built gets it here (host code only, seconds to build).
+    # imports; it is (re)built here when missing or older than its source (host code only).
     from continuous_depth_batching_amd import _build
 
-    if not _build.TICK_PATH.exists():
-        _build.build_tick()
+    _build.build_tick()
 
 
 def gpu_available() -> bool:

@@ -38,7 +38,6 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s
-EXIT_PROBS = (0.15, 0.25, 0.30, 0.30)
 
 
 def parse_args() -> argparse.Namespace:
@@ -67,21 +66,15 @@ def parse_args() -> argparse.Namespace:
 
 
 def c2_workload(num_seqs: int, vocab: int):
-    from continuous_depth_batching_amd.workloads import categorical_exit_trace, lognormal_requests
+    from continuous_depth_batching_amd.workloads import ouro_decode_workload
 
-    prompts, outputs = lognormal_requests(num_requests=num_seqs, vocab_size=vocab, prompt_mu=5.5, prompt_sigma=1.0,
-                                          prompt_range=(8, 2048), output_mu=5.0, output_sigma=0.8,
-                                          output_range=(16, 1024), seed=1)
-    depths = categorical_exit_trace(outputs, EXIT_PROBS, seed=2)
-    return prompts, outputs, depths
+    return ouro_decode_workload(num_seqs, vocab)
 
 
 def ouro_1p4b_config():
-    from continuous_depth_batching_amd.ouro import OuroConfig
+    from continuous_depth_batching_amd.ouro import ouro_1p4b_config as config
 
-    return OuroConfig(vocab_size=49152, hidden_size=2048, intermediate_size=5632, num_hidden_layers=24,
-                      num_attention_heads=16, num_key_value_heads=16, head_dim=128, total_ut_steps=4,
-                      max_position_embeddings=16384)
+    return config()
 
 
 def time_decode_attention(case, split_pages: int, iters: int) -> dict:
@@ -489,8 +482,9 @@ def run_huginn_0125(num_seqs: int = 128, new_tokens: int = 256) -> dict:
                 round(sum(d + 1 for ds in depths for d in ds) / sum(len(ds) for ds in depths), 2)}
 
 
-def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
-    """Numpy oracle decoding a bounded sample of the workload on the host cores."""
+def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int, engine_tokens: list[list[int]]) -> dict:
+    """Numpy oracle decoding a bounded sample of the workload on the host cores; also compares its
+    tokens with the engine's tokens for the same request (matched prefix before the first divergence)."""
 
     import torch
 
@@ -512,10 +506,17 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int) -> dict:
     out = oracle.generate(prompts[idx], n, max_steps=cfg.total_ut_steps, kv_policy="single",
                           exit_depths=depths[idx][: n - 1])
     dt = time.perf_counter() - t0
+    got = engine_tokens[idx][: len(out.tokens)]
+    matched = 0
+    while matched < len(got) and got[matched] == out.tokens[matched]:
+        matched += 1
     return {"value": len(out.tokens) / dt, "unit": "output tok/s", "cores": threads, "kind": "port",
             "sample": f"request {idx} of the workload (prompt {len(prompts[idx])} tokens): full-depth prefill "
                       f"+ {len(out.tokens)} generated tokens with its replayed exit depths, one request at a time "
-                      f"in numpy (bf16-rounded fp32), {dt:.1f} s"}
+                      f"in numpy (bf16-rounded fp32), {dt:.1f} s",
+            "parity": {"request": idx, "tokens_compared": len(out.tokens), "matched_prefix": matched,
+                       "matched_prefix_frac": round(matched / len(out.tokens), 4),
+                       "first_token_equal": bool(got and got[0] == out.tokens[0])}}
 
 
 def main() -> int:
@@ -654,7 +655,9 @@ def main() -> int:
         result["steady_window_note"] = ("the reference's steady-state window (after 2 x max_num_seqs completions, "
                                         "while prompts wait) never opened: no prompt was still waiting by then")
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, prompts, outputs, depths, args.cpu_sample_tokens)
+        result["cpu_baseline"] = cpu_baseline(model, prompts, outputs, depths, args.cpu_sample_tokens,
+                                              [o.generated_tokens for o in outs])
+        result["matched_prefix_frac"] = result["cpu_baseline"]["parity"]["matched_prefix_frac"]
     print(json.dumps(result), flush=True)
     return 0
 

@@ -97,15 +97,8 @@ class ContinuousDepthBatchingStats:
         return self.coda_tokens / self.coda_batches if self.coda_batches else 0.0
 
 
-@dataclass
-class LaunchRecord:
-    """One launch as the engine issued it (for schedule-parity checks)."""
-
-    kind: str
-    request_ids: list[str]
-    positions: list[int] = field(default_factory=list)
-    steps: list[int] = field(default_factory=list)
-    exits: list[bool] = field(default_factory=list)
+def _prelude_event(site: str, items: list[DepthWorkItem]) -> tuple:
+    return ("prelude", site, tuple((i.state.request_id, i.token_position, i.hidden_slot) for i in items))
 
 
 DEFAULT_MEM_FRACTION_STATIC = 0.8
@@ -156,8 +149,16 @@ class ContinuousDepthBatchingEngine:
     pending_prefill_results: deque = field(default_factory=deque)
     stalled_decoders: dict = field(default_factory=dict)
     finished_outputs: dict = field(default_factory=dict)
+    # Schedule-parity hooks. ``record_launches`` logs every launch with the state it reads:
+    #   ("prefill",   ((request_id, start_position, query_length, has_new_token), ...))
+    #   ("prelude",   site, ((request_id, token_position, hidden_slot), ...))
+    #   ("recurrent", ((request_id, token_position, step, hidden_slot, block_ids), ...), exits, refills)
+    #   ("coda",      ((request_id, token_position, hidden_slot), ...))
+    # ``consume_all_results`` consumes every staged prefill/coda result at the next consume point
+    # (waiting for it), so the schedule depends on the inputs alone, not on device timing.
     record_launches: bool = False
     launch_log: list = field(default_factory=list)
+    consume_all_results: bool = False
     _exit_kv_backlog: list = field(default_factory=list)
     _pending_flags: dict = field(default_factory=dict)
 
@@ -332,8 +333,7 @@ class ContinuousDepthBatchingEngine:
         stats.prefill_recurrent_steps += scheduled.num_q_tokens * (self.cdb_config.max_recurrent_steps or 0)
         pending = self.runner.stage_prefill_batch(requests, allow_async=self.cdb_config.use_async_batching)
         if self.record_launches:
-            self.launch_log.append(LaunchRecord("prefill", [f.state.request_id for f in requests],
-                                                [f.state.position_offset for f in requests]))
+            self.launch_log.append(self._prefill_event(requests))
         eager_flags: list[bool] = []
         eager_items: list[DepthWorkItem] = []
         eager_rows: list[int] = []
@@ -354,10 +354,23 @@ class ContinuousDepthBatchingEngine:
         if eager_items:
             self._record_prelude("after_prefill_eager", len(eager_items), gathered=len(eager_items))
             self.runner.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
+            if self.record_launches:
+                self.launch_log.append(_prelude_event("after_prefill_eager", eager_items))
             self._enqueue_prelude_items(eager_items, front=False)
         self.pending_prefill_results.append(pending)
 
+    @staticmethod
+    def _prefill_event(requests) -> tuple:
+        return ("prefill", tuple((f.state.request_id, f.state.position_offset - f.query_length, f.query_length,
+                                  f.has_new_token) for f in requests))
+
+    def _recurrent_rows(self, items: list[DepthWorkItem]) -> tuple:
+        table = self.cache.block_table
+        return tuple((i.state.request_id, i.token_position, i.recurrent_step, i.hidden_slot,
+                      tuple(table.get(i.state.request_id, ()))) for i in items)
+
     def _consume_ready_prefill_results(self, *, block: bool) -> None:
+        block = block or self.consume_all_results
         while self.pending_prefill_results:
             pending = self.pending_prefill_results[0]
             if not block and not pending.is_ready():
@@ -402,6 +415,7 @@ class ContinuousDepthBatchingEngine:
         for step, count in depth_counts.items():
             stats.mixed_recurrent_depth_histogram[step] += count
             stats.recurrent_step_histogram[step] += count
+        rows = self._recurrent_rows(items) if self.record_launches else None
         flags = self.runner.compute_recurrent_batch(items)
         stats.recurrent_batches += 1
         stats.recurrent_steps += len(items)
@@ -417,8 +431,7 @@ class ContinuousDepthBatchingEngine:
                 self.scheduler.enqueue_depth_front(refills)
             self._flush_exit_kv_copies()
             if self.record_launches:
-                self.launch_log.append(LaunchRecord("recurrent", [i.state.request_id for i in items],
-                                                    [i.token_position for i in items], launch_steps, exits))
+                self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), self.scheduler.refill_events))
             return
         refills = []
         exits = []
@@ -441,8 +454,7 @@ class ContinuousDepthBatchingEngine:
             self.scheduler.enqueue_depth_front(refills)
         self._flush_exit_kv_copies()
         if self.record_launches:
-            self.launch_log.append(LaunchRecord("recurrent", [i.state.request_id for i in items],
-                                                [i.token_position for i in items], launch_steps, exits))
+            self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), self.scheduler.refill_events))
 
     def _record_exit(self, item: DepthWorkItem, step: int) -> None:
         if item.apply_exit_gate:
@@ -485,11 +497,13 @@ class ContinuousDepthBatchingEngine:
         pending = self.runner.stage_coda_batch(items, allow_async=use_async,
                                                successors=successors if use_async else None)
         if self.record_launches:
-            self.launch_log.append(LaunchRecord("coda", [i.state.request_id for i in items],
-                                                [i.token_position for i in items]))
+            self.launch_log.append(("coda", tuple((i.state.request_id, i.token_position, i.hidden_slot)
+                                                  for i in items)))
         if use_async:
             eager_items, _, flags = selected[0]
             pending.eager_reentries = flags
+            if self.record_launches and eager_items:
+                self.launch_log.append(_prelude_event("after_coda_eager", eager_items))
             self._enqueue_prelude_items(eager_items, front=True)
         self.pending_coda_results.append(pending)
         self.last_stats.max_pending_coda_results = max(self.last_stats.max_pending_coda_results,
@@ -517,6 +531,7 @@ class ContinuousDepthBatchingEngine:
         return items, rows, flags
 
     def _consume_ready_coda_results(self, *, block: bool) -> None:
+        block = block or self.consume_all_results
         while self.pending_coda_results:
             pending = self.pending_coda_results[0]
             if not block and not pending.is_ready():
@@ -587,6 +602,8 @@ class ContinuousDepthBatchingEngine:
         if items:
             self._record_prelude(site, len(items))
             self.runner.compute_prelude_batch(items)
+            if self.record_launches:
+                self.launch_log.append(_prelude_event(site, items))
         self._enqueue_prelude_items(items, front=front)
 
     def _enqueue_prelude_items(self, items: list[DepthWorkItem], *, front: bool) -> None:
@@ -712,6 +729,8 @@ class ContinuousDepthBatchingEngine:
                 continue
             self._record_prelude("wave_cohort", len(items))
             self.runner.compute_prelude_batch(items)
+            if self.record_launches:
+                self.launch_log.append(_prelude_event("wave_cohort", items))
             survivors = items
             exited: list[DepthWorkItem] = []
             # On the delayed horizon a launch's decisions route the item after its next launch,
@@ -721,18 +740,22 @@ class ContinuousDepthBatchingEngine:
             for step in range(max_steps):
                 for item in survivors:
                     item.recurrent_step = step
+                rows = self._recurrent_rows(survivors) if self.record_launches else None
                 flags = self.runner.compute_recurrent_batch(survivors)
                 self.last_stats.recurrent_batches += 1
                 self.last_stats.recurrent_steps += len(survivors)
                 self.last_stats.recurrent_step_histogram[step] += len(survivors)
                 continuing = []
+                exits = []
                 for idx, item in enumerate(survivors):
                     if delayed:
                         prev = previous.pop(id(item), None)
                         gate_exit = item.apply_exit_gate and prev is not None and prev[0].get(prev[1])
                     else:
                         gate_exit = item.apply_exit_gate and flags.get(idx)
-                    if step == max_steps - 1 or gate_exit:
+                    leave = step == max_steps - 1 or bool(gate_exit)
+                    exits.append(leave)
+                    if leave:
                         self._record_exit(item, step)
                         exited.append(item)
                     else:
@@ -740,10 +763,15 @@ class ContinuousDepthBatchingEngine:
                         if delayed:
                             previous[id(item)] = (flags, idx)
                 self._flush_exit_kv_copies()
+                if self.record_launches:
+                    self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), self.scheduler.refill_events))
                 survivors = continuing
                 if not survivors:
                     break
             pending = self.runner.stage_coda_batch(exited, allow_async=False)
+            if self.record_launches:
+                self.launch_log.append(("coda", tuple((i.state.request_id, i.token_position, i.hidden_slot)
+                                                      for i in exited)))
             tokens = self.runner.consume_coda_result(pending)
             self.last_stats.coda_batches += 1
             self.last_stats.coda_tokens += len(exited)
@@ -759,6 +787,8 @@ class ContinuousDepthBatchingEngine:
         stats.prefill_requests += len(requests)
         stats.prefill_recurrent_steps += scheduled.num_q_tokens * (self.cdb_config.max_recurrent_steps or 0)
         pending = self.runner.stage_prefill_batch(requests, allow_async=False)
+        if self.record_launches:
+            self.launch_log.append(self._prefill_event(requests))
         tokens = self.runner.consume_prefill_result(pending)
         k = 0
         for future in requests:
@@ -833,5 +863,5 @@ class ContinuousDepthBatchingEngine:
                                      f"kv_slots_per_layer={slots}, exit step {d + 1 + extra}")
 
 
-__all__ = ["ContinuousDepthBatchingEngine", "ContinuousDepthBatchingStats", "CacheFullError", "LaunchRecord",
+__all__ = ["ContinuousDepthBatchingEngine", "ContinuousDepthBatchingStats", "CacheFullError",
            "PendingFlags", "time"]

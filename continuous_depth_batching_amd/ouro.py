@@ -139,6 +139,15 @@ class OuroForCausalLM(nn.Module):
         return self.model
 
 
+def ouro_1p4b_config(num_hidden_layers: int = 24) -> OuroConfig:
+    """The Ouro-1.4B shape (48 layers: the Ouro-2.6B shape): hidden 2048, 16 heads x 128, MLP 5632,
+    vocab 49152, 4 loop steps."""
+
+    return OuroConfig(vocab_size=49152, hidden_size=2048, intermediate_size=5632,
+                      num_hidden_layers=num_hidden_layers, num_attention_heads=16, num_key_value_heads=16,
+                      head_dim=128, total_ut_steps=4, max_position_embeddings=16384)
+
+
 def init_ouro_weights(model: OuroForCausalLM, *, seed: int, std: float | None = None) -> OuroForCausalLM:
     """Random init: Linear/Embedding weights N(0, std), biases 0, RMSNorm weights 1, drawn from one
     seeded generator on the model's device in a fixed parameter order."""

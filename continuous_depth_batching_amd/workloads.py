@@ -188,3 +188,19 @@ def poisson_exit_trace(max_new_tokens: list[int], mean: float, max_steps: int, s
     rng = np.random.default_rng(seed)
     return [(np.clip(rng.poisson(mean, size=max(0, n - 1)), 1, max_steps) - 1).astype(int).tolist()
             for n in max_new_tokens]
+
+
+# The headline decode workload: 256 sequences at the Ouro-1.4B shape, prompts lognormal(5.5, 1.0)
+# clipped to [8, 2048], outputs lognormal(5.0, 0.8) clipped to [16, 1024], uniform token ids, and
+# 1-indexed exit depths drawn from the categorical {1: .15, 2: .25, 3: .30, 4: .30}.
+OURO_EXIT_PROBS = (0.15, 0.25, 0.30, 0.30)
+
+
+def ouro_decode_workload(num_seqs: int = 256, vocab_size: int = 49152) -> tuple[list[list[int]], list[int],
+                                                                                 list[list[int]]]:
+    """(prompts, max_new_tokens, 0-based exit depths) of the seeded headline decode workload."""
+
+    prompts, outputs = lognormal_requests(num_requests=num_seqs, vocab_size=vocab_size, prompt_mu=5.5,
+                                          prompt_sigma=1.0, prompt_range=(8, 2048), output_mu=5.0,
+                                          output_sigma=0.8, output_range=(16, 1024), seed=1)
+    return prompts, outputs, categorical_exit_trace(outputs, OURO_EXIT_PROBS, seed=2)

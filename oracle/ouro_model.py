@@ -44,7 +44,11 @@ class OracleOutput:
 class OuroOracle:
     def __init__(self, weights: dict[str, np.ndarray], *, num_layers: int, num_heads: int, num_kv_heads: int,
                  head_dim: int, rope_theta: float, eps: float, dtype: str = "f32", max_positions: int = 4096,
-                 gate: str = "early_exit") -> None:
+                 gate: str = "early_exit", accumulate: str = "f32") -> None:
+        """``accumulate`` is the dot-product precision of the projections ("f32", like the GPU
+        GEMMs, or "f64"); their results are rounded to ``dtype`` either way. Two settings give two
+        valid implementations, whose spread is the size of bf16 accumulation-order noise."""
+
         self.w = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
         self.L, self.H, self.Hkv, self.D = num_layers, num_heads, num_kv_heads, head_dim
         self.eps = eps
@@ -52,13 +56,20 @@ class OuroOracle:
         self.rnd = rounder(dtype)
         self.cos, self.sin = rope_tables(head_dim, rope_theta, max_positions, 1, dtype)
         self.gate = "model.lookahead_exit_gate" if gate == "lookahead" else "model.early_exit_gate"
+        self.acc = np.float64 if accumulate == "f64" else np.float32
+        self._w64: dict[int, np.ndarray] = {}
 
     def _p(self, name: str) -> np.ndarray:
         return self.w[name]
 
     def _mm(self, x: np.ndarray, weight: np.ndarray) -> np.ndarray:
-        # fp32 accumulation, like the GPU GEMMs; the result is rounded to the model dtype.
-        return self.rnd(np.asarray(x, np.float32) @ weight.T)
+        # fp32 (or fp64) accumulation; the result is rounded to the model dtype.
+        if self.acc is np.float32:
+            return self.rnd(np.asarray(x, np.float32) @ weight.T)
+        wide = self._w64.get(id(weight))
+        if wide is None:
+            wide = self._w64[id(weight)] = weight.astype(np.float64)
+        return self.rnd((np.asarray(x, np.float64) @ wide.T).astype(np.float32))
 
     def _layer_stack(self, h: np.ndarray, attend) -> np.ndarray:
         """One loop step over all layers; h is the step input (= residual). Returns final-normed hidden."""
@@ -124,7 +135,13 @@ class OuroOracle:
 
     def generate(self, prompt: list[int], max_new_tokens: int, *, max_steps: int, kv_policy: str = "single",
                  exit_depths: list[int] | None = None, threshold: float | None = None, min_steps: int = 1,
-                 delayed: bool = False, eos_token_id: int | None = None) -> OracleOutput:
+                 delayed: bool = False, eos_token_id: int | None = None, forced_tokens: list[int] | None = None,
+                 hidden_trace: list | None = None) -> OracleOutput:
+        """Greedy CDB decode of one request. ``forced_tokens`` feeds the given tokens back instead
+        of the oracle's own (teacher forcing; ``tokens`` still records the oracle's argmax), and
+        ``hidden_trace`` collects (token index, loop step, hidden after the step): index 0 is the
+        prompt's last position after the full-depth prefill, index j >= 1 the j-th decode token."""
+
         slots = {"single": 1, "depth_indexed": max_steps, "last_exited": max_steps}[kv_policy]
 
         def slot_of(step: int) -> int:
@@ -135,6 +152,10 @@ class OuroOracle:
         h = self.prefill_hidden(prompt, kv, steps=max_steps, slot_of=slot_of)
         token = self._coda(h[-1])
         out = OracleOutput(tokens=[token])
+        if hidden_trace is not None:
+            hidden_trace.append((0, max_steps - 1, h[-1].copy()))
+        if forced_tokens is not None:
+            token = forced_tokens[0]
         pos = len(prompt)
         gate_w = self._p(self.gate + ".weight").reshape(-1)
         gate_b = float(self._p(self.gate + ".bias").reshape(-1)[0])
@@ -149,6 +170,8 @@ class OuroOracle:
                 base = slot_of(step) * self.L
                 h = self._layer_stack(h, lambda l, q, k, v, base=base: self._attend(kv, base + l, q, k, v,
                                                                                    np.array([pos])))
+                if hidden_trace is not None:
+                    hidden_trace.append((k_idx + 1, step, h[0].copy()))
                 if step == max_steps - 1:
                     break
                 if depth is not None:
@@ -179,5 +202,7 @@ class OuroOracle:
                 out.exit_copies += 1
             token = self._coda(h[0])
             out.tokens.append(token)
+            if forced_tokens is not None:
+                token = forced_tokens[len(out.tokens) - 1]
             pos += 1
         return out

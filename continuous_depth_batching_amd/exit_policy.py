@@ -1,19 +1,26 @@
-"""Exit-decision policy: which rule interprets a gate signal and when it is consumed.
+"""The exit gate's launch record.
 
-Mirrors the reference's ExitPolicy surface (continuous_depth_batching/exit_policy.py:12-183):
-the rule (cumulative hazard for Ouro's sigmoid gate, direct threshold for
-Huginn's latent difference), the decision horizon (same step, or one launch
-later on the delayed/lookahead path) and the serving-time validation. The
-per-token arithmetic itself runs on the GPU in ``cdb_exit_gate``; this class
-only resolves the parameters the kernel is launched with. ``should_exit`` is
-kept as the host-side restatement of one decision for callers that hold a
-signal on the host.
+Every per-token exit decision runs on the device in ``cdb_exit_gate``. The host only needs the
+gate's launch parameters, and one routing fact: whether a launch's decisions route the item
+right away or one launch later. ``ExitPolicy`` takes the adapter's signal spec and the engine
+configuration (the reference's ExitPolicy fields, continuous_depth_batching/exit_policy.py:
+50-58) and resolves them once into that record:
+
+  * ``lag``           launches between a decision and the routing that applies it (0 or 1);
+  * ``round_hazard``  whether the hazard is rounded to the model dtype before it is accumulated
+                      (a synchronous decision reads the model-dtype sigmoid, a delayed one the
+                      float32 signal; cdb/model_runner.py:807-813);
+  * the rule, threshold and step bounds, checked against the rule's signal scale.
+
+Resolution (reference exit_policy.py:87-146): a live signal waits one launch when the adapter
+declares an offset-one signal or when delayed consumption runs on the async path; a replayed
+trace waits one launch only in the latter case; a pre-loop distribution never waits.
 """
 
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from enum import Enum, IntEnum
 
 
@@ -30,14 +37,19 @@ class DecisionHorizon(IntEnum):
 
 @dataclass(frozen=True)
 class ExitPolicySpec:
+    """What an adapter's gate signal means, and when the adapter can first deliver it."""
+
     rule: ExitDecisionRule
     decision_horizon: DecisionHorizon = DecisionHorizon.SAME_STEP
 
 
-@dataclass
-class TokenExitPolicyState:
-    exit_cdf: float = 0.0
-    survival: float = 1.0
+# The threshold each rule accepts: a probability for the CDF rules, a nonnegative score for the
+# direct comparison (the latent difference is a norm ratio).
+_THRESHOLD_SCALE = {
+    ExitDecisionRule.CUMULATIVE_HAZARD: ("in (0, 1] for probability policies", lambda t: 0.0 < t <= 1.0),
+    ExitDecisionRule.PRELOOP_DISTRIBUTION: ("in (0, 1] for probability policies", lambda t: 0.0 < t <= 1.0),
+    ExitDecisionRule.DIRECT_THRESHOLD: ("nonnegative for direct-threshold policies", lambda t: t >= 0.0),
+}
 
 
 @dataclass(frozen=True)
@@ -49,65 +61,34 @@ class ExitPolicy:
     delay_gate_consumption: bool
     use_async_batching: bool
     synthetic_exit_replay: bool
+    lag: int = field(init=False)
+    round_hazard: bool = field(init=False)
 
     def __post_init__(self) -> None:
-        if self.threshold is None:
-            return
-        if not math.isfinite(self.threshold):
-            raise ValueError("exit_threshold must be finite")
-        if self.spec.rule is ExitDecisionRule.DIRECT_THRESHOLD:
-            if self.threshold < 0:
-                raise ValueError("exit_threshold must be nonnegative for direct-threshold policies")
-        elif not 0 < self.threshold <= 1:
-            raise ValueError("exit_threshold must be in (0, 1] for probability policies")
+        if self.threshold is not None:
+            scale, accepts = _THRESHOLD_SCALE[self.spec.rule]
+            if not math.isfinite(self.threshold):
+                raise ValueError("exit_threshold must be finite")
+            if not accepts(self.threshold):
+                raise ValueError(f"exit_threshold must be {scale}, got {self.threshold}")
+        overlap = self.delay_gate_consumption and self.use_async_batching
+        preloop = self.spec.rule is ExitDecisionRule.PRELOOP_DISTRIBUTION
+        live_late = (self.threshold is not None and not preloop
+                     and (overlap or self.spec.decision_horizon is DecisionHorizon.OFFSET_ONE))
+        replay_late = self.synthetic_exit_replay and overlap
+        lag = 1 if (live_late or replay_late) else 0
+        object.__setattr__(self, "lag", lag)
+        object.__setattr__(self, "round_hazard", lag == 0)
 
-    @property
-    def delayed_transport_enabled(self) -> bool:
-        return self.delay_gate_consumption and self.use_async_batching
+    def delayed(self) -> bool:
+        """Whether a launch's decisions route the item only after its next launch."""
 
-    @property
-    def decision_horizon(self) -> DecisionHorizon:
-        if self.spec.rule is ExitDecisionRule.PRELOOP_DISTRIBUTION:
-            return DecisionHorizon.SAME_STEP
-        if self.spec.decision_horizon is DecisionHorizon.OFFSET_ONE or self.delayed_transport_enabled:
-            return DecisionHorizon.OFFSET_ONE
-        return DecisionHorizon.SAME_STEP
-
-    @property
-    def synthetic_decision_horizon(self) -> DecisionHorizon:
-        return DecisionHorizon.OFFSET_ONE if self.delayed_transport_enabled else DecisionHorizon.SAME_STEP
+        return self.lag == 1
 
     def validate_serving_timing(self) -> None:
-        if self.spec.decision_horizon is DecisionHorizon.OFFSET_ONE and not self.delayed_transport_enabled:
-            raise ValueError("An adapter-declared offset-1 exit signal requires the delayed-gate-consumption path "
+        """An offset-one signal exists only where a launch's decisions are applied one launch later."""
+
+        overlap = self.delay_gate_consumption and self.use_async_batching
+        if self.spec.decision_horizon is DecisionHorizon.OFFSET_ONE and not overlap:
+            raise ValueError("An offset-1 exit signal needs delayed gate consumption on the async path "
                              "(use_async_batching=True and delay_gate_consumption=True).")
-
-    def decides_before_loop(self) -> bool:
-        return self.spec.rule is ExitDecisionRule.PRELOOP_DISTRIBUTION
-
-    def uses_delayed_online_signal(self, *, signal_enabled: bool) -> bool:
-        return (signal_enabled and self.threshold is not None and not self.decides_before_loop()
-                and self.decision_horizon is DecisionHorizon.OFFSET_ONE)
-
-    def uses_delayed_synthetic_exit(self) -> bool:
-        return self.synthetic_exit_replay and self.synthetic_decision_horizon is DecisionHorizon.OFFSET_ONE
-
-    def delayed(self, *, signal_enabled: bool = True) -> bool:
-        """Whether routing after a launch uses the previous launch's decision input."""
-
-        return self.uses_delayed_online_signal(signal_enabled=signal_enabled) or self.uses_delayed_synthetic_exit()
-
-    def should_exit(self, state: TokenExitPolicyState, *, source_step: int, signal: float) -> bool:
-        """One host-side decision (exit_policy.py:150-169); the engine uses the device kernel instead."""
-
-        if self.threshold is None:
-            return False
-        can_exit = source_step + 1 >= self.min_recurrent_steps
-        if self.spec.rule is ExitDecisionRule.CUMULATIVE_HAZARD:
-            hazard = 1.0 / (1.0 + math.exp(-float(signal)))
-            state.exit_cdf += hazard * state.survival
-            state.survival *= 1.0 - hazard
-            return can_exit and state.exit_cdf >= self.threshold
-        if self.spec.rule is ExitDecisionRule.DIRECT_THRESHOLD:
-            return can_exit and float(signal) < self.threshold
-        raise RuntimeError("Preloop exit distributions do not consume per-step signals")

@@ -198,12 +198,10 @@ class ModelRunner:
         spec = model_adapter.exit_policy_spec()
         self.gate_rule = ops.RULE_DIRECT_THRESHOLD if spec.rule is ExitDecisionRule.DIRECT_THRESHOLD \
             else ops.RULE_CUMULATIVE_HAZARD
-        self.delayed = exit_policy.delayed()
         self.recurrent_graph_hits = 0
         self.recurrent_graph_captures = 0
         self.stage_graph_hits = 0
         self.stage_graph_captures = 0
-        self._slot_of_step: tuple[int, ...] | None = None
         self._coda_turns: list[_CodaTurn | None] = [None] * self.CODA_TURNS
         self._coda_turn_index = 0
 
@@ -336,7 +334,7 @@ class ModelRunner:
             rule=self.gate_rule,
             # The synchronous path reads the model-dtype hazard; the delayed path the fp32 one
             # (cdb/model_runner.py:807-813 vs continuous_api.py:1693-1697).
-            round_hazard=not self.delayed,
+            round_hazard=policy.round_hazard,
             min_steps=policy.min_recurrent_steps,
             max_steps=policy.max_recurrent_steps,
             threshold=policy.threshold,
@@ -392,12 +390,8 @@ class ModelRunner:
         slot -1 and position -1 make every kernel skip them
         (cdb/model_runner.py:704-754 assembles the same per-row facts)."""
 
-        slot_of_step = self._slot_of_step
-        if slot_of_step is None:
-            steps = self.engine_config.max_recurrent_steps or 0
-            slot_of_step = self._slot_of_step = tuple(self.layout.slot_for_step(s) for s in range(steps))
         _tick.fill_recurrent(items, i64, i32, self.cache.table_row_of, self.layout.core_base,
-                             self.layout.num_core_layers, slot_of_step)
+                             self.layout.num_core_layers, self.layout.step_slots)
 
     def capture_all_buckets(self, buckets: Sequence[int] | None = None) -> int:
         """Capture the recurrent-stage graph of every bucket ahead of time.

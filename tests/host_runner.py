@@ -124,7 +124,6 @@ class HostLoopRunner(ModelRunner):
         self.next_hidden_slot = 0
         self.recurrent_graph_hits = self.recurrent_graph_captures = 0
         self.stage_graph_hits = self.stage_graph_captures = 0
-        self._slot_of_step = None
         self.hidden: dict[int, float] = {}
         self.gate: dict[int, list[float]] = {}
         # Per recurrent launch: the padded bucket's metadata exactly as uploaded to the device.

@@ -48,6 +48,8 @@
 // split_prefix[0..B]] padded to 256 bytes, then fp32 partials
 // [total_splits, H, D + 2].
 
+#include <mutex>
+
 #include "cdb_common.h"
 #include "../../include/cdb_amd.h"
 
@@ -668,6 +670,12 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
 
 using namespace cdb;
 
+// The fixed scratch of cdb_paged_decode_attention_noalloc: a file-scope device array, one copy per
+// GPU, alive until the process ends. Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in symbol); scratch_address() resolves each device's own address once,
+// with that device current, and the launches use that address.
+static __device__ __align__(256) unsigned char scratch[CDB_DECODE_SCRATCH_BYTES];
+
 namespace {
 
 int g_num_cus = 0;
@@ -715,6 +723,33 @@ int dispatch_dim(const DecodeParams& P, int head_dim, int num_cus, hipStream_t s
   }
 }
 
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mutex;
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return CDB_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return CDB_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CDB_OK;
+}
+
+int decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                     int64_t layer_stride, int32_t num_cache_layers, int64_t pool_blocks, const int32_t* cache_layer,
+                     int32_t cache_layer0, const int32_t* block_table, const int32_t* table_row,
+                     int32_t table_width, const int32_t* seqlens, const float* rope_cos, const float* rope_sin,
+                     int32_t rope_style, int32_t max_positions, const void* q_bias, const void* k_bias, void* out,
+                     void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
+                     int32_t min_split_pages, int32_t max_split_pages, float scale, int64_t q_stride,
+                     int64_t kv_stride, int32_t dtype, hipStream_t stream);
+
 }  // namespace
 
 extern "C" {
@@ -739,6 +774,53 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages, float scale,
                                int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream) {
+  return decode_attention(q, k_new, v_new, k_pool, v_pool, layer_stride, num_cache_layers, pool_blocks, cache_layer,
+                          cache_layer0, block_table, table_row, table_width, seqlens, rope_cos, rope_sin, rope_style,
+                          max_positions, q_bias, k_bias, out, workspace, workspace_bytes, num_rows, num_heads,
+                          num_kv_heads, head_dim, block_size, split_pages, min_split_pages, max_split_pages, scale,
+                          q_stride, kv_stride, dtype, stream);
+}
+
+int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const void* v_new, void* k_pool,
+                                       void* v_pool, int64_t layer_stride, int32_t num_cache_layers,
+                                       int64_t pool_blocks, const int32_t* cache_layer, int32_t cache_layer0,
+                                       const int32_t* block_table, const int32_t* table_row, int32_t table_width,
+                                       const int32_t* seqlens, const float* rope_cos, const float* rope_sin,
+                                       int32_t rope_style, int32_t max_positions, const void* q_bias,
+                                       const void* k_bias, void* out, int32_t num_rows, int32_t num_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                       int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages,
+                                       float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype,
+                                       hipStream_t stream) {
+  if (num_rows == 0) return CDB_OK;
+  if (num_rows < 0 || num_heads <= 0 || head_dim <= 0) return CDB_ERR_SHAPE;
+  // The kernel lengthens splits until the partials fit, down to one split per row: the scratch
+  // must hold the header and one partial per row.
+  const int64_t need = header_bytes(num_rows) + (int64_t)num_rows * num_heads * (head_dim + 2) * (int64_t)sizeof(float);
+  if (need > CDB_DECODE_SCRATCH_BYTES) return CDB_ERR_CAPACITY;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != CDB_OK) return rc;
+  return decode_attention(q, k_new, v_new, k_pool, v_pool, layer_stride, num_cache_layers, pool_blocks, cache_layer,
+                          cache_layer0, block_table, table_row, table_width, seqlens, rope_cos, rope_sin, rope_style,
+                          max_positions, q_bias, k_bias, out, ws, CDB_DECODE_SCRATCH_BYTES, num_rows, num_heads,
+                          num_kv_heads, head_dim, block_size, split_pages, min_split_pages, max_split_pages, scale,
+                          q_stride, kv_stride, dtype, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                     int64_t layer_stride, int32_t num_cache_layers, int64_t pool_blocks, const int32_t* cache_layer,
+                     int32_t cache_layer0, const int32_t* block_table, const int32_t* table_row,
+                     int32_t table_width, const int32_t* seqlens, const float* rope_cos, const float* rope_sin,
+                     int32_t rope_style, int32_t max_positions, const void* q_bias, const void* k_bias, void* out,
+                     void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
+                     int32_t min_split_pages, int32_t max_split_pages, float scale, int64_t q_stride,
+                     int64_t kv_stride, int32_t dtype, hipStream_t stream) {
   if (num_rows == 0) return CDB_OK;
   if (!q || !k_new || !v_new || !k_pool || !v_pool || !block_table || !seqlens || !out || !workspace)
     return CDB_ERR_NULL;
@@ -790,4 +872,4 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
   return dispatch_dim<bf16_t>(P, head_dim, g_num_cus, stream);
 }
 
-}  // extern "C"
+}  // namespace

@@ -83,6 +83,29 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t min_split_pages, int32_t max_split_pages, float scale,
                                int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
 
+/* No counterpart in the reference. cdb_paged_decode_attention for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc. Same arguments and results without the workspace: the split header and partials
+ * live in a fixed device array of CDB_DECODE_SCRATCH_BYTES per GPU (resolved once per device,
+ * held until the process ends). The call allocates nothing and frees nothing. Nothing in the
+ * scratch must start at zero: each call writes its header and partials before reading them.
+ * Every call on one GPU shares that GPU's array, so calls that overlap on one GPU (two streams,
+ * or two threads) race; serialize them. Returns CDB_ERR_CAPACITY when the header plus one
+ * partial per row, num_rows * num_heads * (head_dim + 2) floats, exceeds the scratch (at
+ * 16 heads x 128: more than 2000 rows); a smaller surplus only lengthens the splits. */
+#define CDB_DECODE_SCRATCH_BYTES ((int64_t)16 << 20)
+int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const void* v_new, void* k_pool,
+                                       void* v_pool, int64_t layer_stride, int32_t num_cache_layers,
+                                       int64_t pool_blocks, const int32_t* cache_layer, int32_t cache_layer0,
+                                       const int32_t* block_table, const int32_t* table_row, int32_t table_width,
+                                       const int32_t* seqlens, const float* rope_cos, const float* rope_sin,
+                                       int32_t rope_style, int32_t max_positions, const void* q_bias,
+                                       const void* k_bias, void* out, int32_t num_rows, int32_t num_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                       int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages,
+                                       float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype,
+                                       hipStream_t stream);
+
 /* Fused RMSNorm sandwich over rows of `width` elements.
  *   norm_w(x) = R(w * R(x * rsqrt(mean(x^2) + eps)))  (R rounds to the storage dtype)
  *   mode 0: out_h = norm_a(x)

@@ -144,6 +144,229 @@ def decode_attention_c2_case(prompts, outputs, device):
                                rope_cos=cos, rope_sin=sin, block_size=bs, contexts=contexts)
 
 
+def graph_time_ms(fn, calls: int, reps: int = 3, warm: bool = True) -> float:
+    """Average milliseconds of one ``fn()`` call, from a captured graph of ``calls`` calls replayed
+    on a side stream and timed with events on that stream (launch gaps are the GPU's own).
+    ``warm=False`` times the first replay, before the graph's inputs were ever read by it."""
+
+    import torch
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        fn()  # first call outside the capture: lazy setup
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for _ in range(calls):
+                fn()
+        if warm:
+            graph.replay()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / (reps * calls)
+
+
+def decode_bytes(positions: np.ndarray, heads: int = 16, kv_heads: int = 16, dim: int = 128, bs: int = 16) -> int:
+    """Algorithmic bytes of one decode-attention call over rows at ``positions`` (bf16): K and V of
+    every attended position, q, out and the new K/V row, block ids and positions."""
+
+    p = positions.astype(np.int64)
+    return int((p + 1).sum() * kv_heads * dim * 4 + p.size * (heads * dim * 4 + kv_heads * dim * 4 + 4)
+               + ((p + bs) // bs).sum() * 4)
+
+
+def run_weighted_decode(launches: list[np.ndarray], pool_pages: int = 32768, group: int = 32) -> dict:
+    """Decode attention over every recurrent launch of the workload, at each launch's own rows and
+    positions, on a cold pool: every launch gets a fresh random block table over a 4 GiB pool of
+    pages, and launches run in graphs of ``group`` calls (one call per launch, as each of the 24
+    layers of a launch repeats the same call on its own cache layer)."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+    from continuous_depth_batching_amd.workloads import rope_tables_torch
+
+    dev = torch.device("cuda")
+    bs, heads, dim = 16, 16, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    pool = torch.empty((1, 2, pool_pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
+    pool.normal_(generator=gen)
+    view = ops.KVPoolView(pool, bs)
+    max_rows = max(len(p) for p in launches)
+    max_pos = max(int(p.max()) for p in launches)
+    q = torch.randn((max_rows, heads, dim), generator=gen, device=dev).bfloat16()
+    kn, vn = q.clone(), q.clone()
+    out = torch.empty_like(q)
+    cos, sin = rope_tables_torch(dim, 10000.0, max_pos + 1, torch.bfloat16, dev)
+    ws = torch.empty(ops.decode_workspace_bytes(max_rows, heads, dim, max_pos + 1, bs, ops.MIN_SPLIT_PAGES) // 4,
+                     dtype=torch.float32, device=dev)
+    zeros = torch.zeros(max_rows, dtype=torch.int32, device=dev)
+    rng = np.random.default_rng(12)
+    total_ms, total_bytes = 0.0, 0
+    classes: dict[str, int] = {}
+    for g0 in range(0, len(launches), group):
+        chunk = launches[g0:g0 + group]
+        tensors = []
+        for pos in chunk:
+            pages = (pos.astype(np.int64) + bs) // bs
+            width = int(pages.max())
+            ids = rng.choice(pool_pages, size=int(pages.sum()), replace=False).astype(np.int32)
+            table = np.full((len(pos), width), -1, np.int32)
+            off = np.concatenate([[0], np.cumsum(pages)])
+            for b in range(len(pos)):
+                table[b, :pages[b]] = ids[off[b]:off[b + 1]]
+            tensors.append((torch.from_numpy(table).to(dev), torch.from_numpy(pos.astype(np.int32)).to(dev)))
+        state = {"i": 0}
+
+        def call():
+            table, seqlens = tensors[state["i"] % len(tensors)]
+            n = seqlens.numel()
+            ops.paged_decode_attention_raw(q[:n], kn[:n], vn[:n], view.k_ptr, view.v_ptr, view.layer_stride,
+                                           view.num_cache_layers, view.pool_blocks, zeros[:n], 0, table, None,
+                                           seqlens, cos, sin, 1, None, None, out[:n], ws, bs, ops.ADAPTIVE_SPLIT,
+                                           dim ** -0.5)
+            state["i"] += 1
+
+        state["i"] = len(tensors) - 1  # the untimed first call takes the last launch; the capture starts at 0
+        total_ms += graph_time_ms(call, len(tensors), reps=1, warm=False) * len(tensors)
+        for pos in chunk:
+            n = len(pos)
+            key = "1-16" if n <= 16 else "17-64" if n <= 64 else "65-128" if n <= 128 else "129-256"
+            classes[key] = classes.get(key, 0) + 1
+            total_bytes += decode_bytes(pos)
+    del pool, ws
+    torch.cuda.empty_cache()
+    gbps = total_bytes / (total_ms * 1e-3) / 1e9
+    return {"launches": len(launches), "ms": round(total_ms, 2), "bytes": total_bytes, "GBps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "launches_by_rows": dict(sorted(classes.items())),
+            "note": "every recurrent launch of one generate_batch of the workload, one decode-attention call each, "
+                    "cold random block tables over a 4 GiB page pool, timed from captured graphs"}
+
+
+def time_by_rows(positions_by_rows: dict[int, np.ndarray], pool_pages: int = 32768, calls: int = 24) -> dict:
+    """Decode attention at fixed launch widths, each from a graph of ``calls`` calls that cycle
+    through cold block tables (one per call), reported per width."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+    from continuous_depth_batching_amd.workloads import rope_tables_torch
+
+    dev = torch.device("cuda")
+    bs, heads, dim = 16, 16, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(13)
+    pool = torch.empty((1, 2, pool_pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
+    pool.normal_(generator=gen)
+    view = ops.KVPoolView(pool, bs)
+    rng = np.random.default_rng(14)
+    results = {}
+    for rows, pos in positions_by_rows.items():
+        pos = pos.astype(np.int32)
+        pages = (pos.astype(np.int64) + bs) // bs
+        q = torch.randn((rows, heads, dim), generator=gen, device=dev).bfloat16()
+        out = torch.empty_like(q)
+        cos, sin = rope_tables_torch(dim, 10000.0, int(pos.max()) + 1, torch.bfloat16, dev)
+        ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(pos.max()) + 1, bs, ops.MIN_SPLIT_PAGES)
+                         // 4, dtype=torch.float32, device=dev)
+        seqlens = torch.from_numpy(pos).to(dev)
+        zeros = torch.zeros(rows, dtype=torch.int32, device=dev)
+        tables = []
+        for _ in range(calls):
+            ids = rng.choice(pool_pages, size=int(pages.sum()), replace=False).astype(np.int32)
+            table = np.full((rows, int(pages.max())), -1, np.int32)
+            off = np.concatenate([[0], np.cumsum(pages)])
+            for b in range(rows):
+                table[b, :pages[b]] = ids[off[b]:off[b + 1]]
+            tables.append(torch.from_numpy(table).to(dev))
+        state = {"i": 0}
+
+        def call():
+            table = tables[state["i"] % calls]
+            state["i"] += 1
+            ops.paged_decode_attention_raw(q, q, q, view.k_ptr, view.v_ptr, view.layer_stride, view.num_cache_layers,
+                                           view.pool_blocks, zeros, 0, table, None, seqlens, cos, sin, 1, None,
+                                           None, out, ws, bs, ops.ADAPTIVE_SPLIT, dim ** -0.5)
+
+        ms = graph_time_ms(call, calls, reps=1, warm=False)
+        nbytes = decode_bytes(pos)
+        results[str(rows)] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                              "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                              "mean_context": round(float(pos.mean()) + 1, 1)}
+    del pool
+    torch.cuda.empty_cache()
+    return results
+
+
+def time_companion_kernels(rows: int = 1024, hidden: int = 2048, heads: int = 16, dim: int = 128) -> dict:
+    """The per-row kernels around decode attention at the microbench's batch size: the RoPE + KV
+    write of ``rows`` tokens (the prefill append), and the exit gate plus the hidden-bank gather and
+    scatter that compact and refill a launch's rows, each timed from a captured graph."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+    from continuous_depth_batching_amd.workloads import rope_tables_torch
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(15)
+    bs = 16
+    pages = 4 * rows
+    pool = torch.zeros((1, 2, pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
+    view = ops.KVPoolView(pool, bs)
+    qkv = torch.randn((rows, 3, heads, dim), generator=gen, device=dev).bfloat16()
+    q_out = torch.empty((rows, heads, dim), dtype=torch.bfloat16, device=dev)
+    write_rows = torch.from_numpy(np.random.default_rng(16).choice(pages * bs, rows, replace=False)).to(dev)
+    positions = torch.randint(0, 4096, (rows,), generator=gen, device=dev, dtype=torch.int32)
+    cos, sin = rope_tables_torch(dim, 10000.0, 4096, torch.bfloat16, dev)
+
+    def rope_write():
+        ops.rope_kv_write_raw(qkv[:, 0], qkv[:, 1], qkv[:, 2], q_out, view, 0, write_rows, positions, cos, sin, 1,
+                              None, None)
+
+    rope_ms = graph_time_ms(rope_write, 20)
+    rope_bytes = 6 * rows * heads * dim * 2 + rows * 12
+
+    bank = torch.randn((4 * rows + 64, hidden), generator=gen, device=dev).bfloat16()
+    slots = torch.randperm(bank.shape[0], generator=gen, device=dev)[:rows].contiguous()
+    staged = torch.empty((rows, hidden), dtype=torch.bfloat16, device=dev)
+    weight = (torch.randn(hidden, generator=gen, device=dev) * 0.02).bfloat16()
+    bias = torch.zeros(1, dtype=torch.bfloat16, device=dev)
+    state = ops.GateState.allocate(bank.shape[0], dev)
+    signal = torch.empty(rows, dtype=torch.bfloat16, device=dev)
+    steps = torch.ones(rows, dtype=torch.int32, device=dev)
+    flags = torch.empty(rows, dtype=torch.uint8, device=dev)
+
+    def gate():
+        ops.exit_gate_raw(staged, None, weight, bias, signal, state, slots, steps, None, flags, rows,
+                          kind=ops.GATE_HAZARD, rule=ops.RULE_CUMULATIVE_HAZARD, delayed=False, round_hazard=True,
+                          min_steps=1, max_steps=4, threshold=0.5)
+
+    def compact():
+        ops.copy_rows_raw(bank, slots, staged, None, rows)   # gather the launch's rows by bank slot
+        ops.copy_rows_raw(staged, None, bank, slots, rows)   # scatter them back
+
+    gate_ms = graph_time_ms(gate, 20)
+    compact_ms = graph_time_ms(compact, 20)
+    gate_bytes = rows * hidden * 2 + hidden * 2 + rows * (8 + 8 + 4 + 4 + 1 + 2)
+    compact_bytes = 4 * rows * hidden * 2 + 2 * rows * 8
+    del pool, bank
+    torch.cuda.empty_cache()
+    row = lambda ms, b: {"us": round(ms * 1e3, 2), "bytes": b, "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+                         "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    return {"rows": rows, "rope_kv_write": row(rope_ms, rope_bytes), "exit_gate": row(gate_ms, gate_bytes),
+            "bank_gather_scatter": row(compact_ms, compact_bytes),
+            "note": f"{rows} tokens/rows, 16 heads x 128 (KV write) and hidden {hidden} (gate, bank rows), bf16; "
+                    "algorithmic bytes: q/k/v read + rotated q and k/v written; hidden read + gate state; "
+                    "bank rows read and written twice"}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per decode-attention call at this shape, from the FETCH_SIZE / WRITE_SIZE
     counter runs (scaled by a plain copy of known size) recorded under profiles/."""
@@ -383,7 +606,8 @@ def run_pressure_modes(model, prompts, outputs, depths, num_blocks: int, unpress
 
 def run_ouro_2p6b(num_seqs: int = 512) -> dict:
     """Ouro-2.6B shape (48 layers looped 4 steps), 512 sequences with the headline prompt, output
-    and exit-depth distributions, timed with shared (``single``) and per-step KV.
+    and exit-depth distributions, timed with shared (``single``) and per-step KV, the latter both
+    with the reference's slot-homogeneous launches and with mixed-slot launches.
 
     Single KV gets a pool sized for the whole batch. Per-step KV (``last_exited``: 192 cache
     layers, 1.5 MiB per token) needs about 2.5x this GPU's HBM for the batch, so its pool is
@@ -404,9 +628,11 @@ def run_ouro_2p6b(num_seqs: int = 512) -> dict:
     prompts, outputs, depths = c2_workload(num_seqs, cfg.vocab_size)
     need = sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, outputs))
     runs = {}
-    for policy in ("single", "last_exited"):
+    for name in ("single", "last_exited", "last_exited_mixed_slots"):
+        policy = "single" if name == "single" else "last_exited"
         common = dict(max_recurrent_steps=4, synthetic_exit_replay=True, delay_gate_consumption=False,
-                      kv_policy=policy, refill=True, block_size=16, max_num_seqs=num_seqs, max_model_len=4096)
+                      kv_policy=policy, refill=True, block_size=16, max_num_seqs=num_seqs, max_model_len=4096,
+                      mixed_slot_recurrent_batches=name.endswith("mixed_slots"))
         if policy == "single":
             extra = dict(num_blocks=int(need * 1.05) + 64, kv_pressure_mode="none")
         else:
@@ -424,7 +650,7 @@ def run_ouro_2p6b(num_seqs: int = 512) -> dict:
         generated = sum(len(o.generated_tokens) for o in outs)
         stats = engine.last_stats
         om = engine.offloading_manager
-        runs[policy] = {
+        runs[name] = {
             "tok_per_s": round(generated / elapsed, 1), "seconds": round(elapsed, 2), "generated_tokens": generated,
             "num_blocks": engine.cache.num_blocks, "blocks_for_whole_batch": need,
             "kv_bytes_per_block": om.bytes_per_block(), "cache_layers": engine.cache.num_layers,
@@ -432,7 +658,7 @@ def run_ouro_2p6b(num_seqs: int = 512) -> dict:
             "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1), "coda_batches": stats.coda_batches,
             "prefill_batches": stats.prefill_batches, "exit_kv_copies": stats.exit_kv_copies,
             **om.preemption_stats()}
-        print(json.dumps({"ouro_2p6b_done": policy, **runs[policy]}), flush=True)
+        print(json.dumps({"ouro_2p6b_done": name, **runs[name]}), flush=True)
         del engine, om
         torch.cuda.empty_cache()
     return runs
@@ -510,13 +736,36 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int, engine_tok
     matched = 0
     while matched < len(got) and got[matched] == out.tokens[matched]:
         matched += 1
+    # Teacher-forced with the engine's tokens (untimed): at every step, how far the engine's choice
+    # sits below the oracle's best logit. On this untrained model the top logits crowd together, so
+    # bf16 rounding noise flips greedy choices between any two correct implementations (the oracle
+    # with fp32 and with fp64 accumulation already disagree on this request's first token); the
+    # margin, against the spread of the logits, is what separates noise from a wrong result.
+    trace: list = []
+    forced = oracle.generate(prompts[idx], n, max_steps=cfg.total_ut_steps, kv_policy="single",
+                             exit_depths=depths[idx][: n - 1], forced_tokens=got, hidden_trace=trace)
+    final = {j: h for j, _, h in trace}
+    margins, spreads = [], []
+    for j, token in enumerate(got):
+        logits = oracle.logits(final[j]).astype(np.float64)
+        margins.append(float(logits.max() - logits[token]))
+        spreads.append(float(logits.std()))
     return {"value": len(out.tokens) / dt, "unit": "output tok/s", "cores": threads, "kind": "port",
             "sample": f"request {idx} of the workload (prompt {len(prompts[idx])} tokens): full-depth prefill "
                       f"+ {len(out.tokens)} generated tokens with its replayed exit depths, one request at a time "
                       f"in numpy (bf16-rounded fp32), {dt:.1f} s",
             "parity": {"request": idx, "tokens_compared": len(out.tokens), "matched_prefix": matched,
                        "matched_prefix_frac": round(matched / len(out.tokens), 4),
-                       "first_token_equal": bool(got and got[0] == out.tokens[0])}}
+                       "first_token_equal": bool(got and got[0] == out.tokens[0]),
+                       "teacher_forced_argmax_agreement": round(float(np.mean(
+                           [a == b for a, b in zip(forced.tokens, got)])), 4),
+                       "teacher_forced_max_logit_margin": round(max(margins), 4),
+                       "teacher_forced_mean_logit_margin": round(float(np.mean(margins)), 5),
+                       "logit_std": round(float(np.mean(spreads)), 4),
+                       "note": "bf16 greedy streams of an untrained model diverge on rounding noise; the "
+                               "teacher-forced margin (oracle max logit minus the oracle logit of the engine's "
+                               "token, in units of logits whose spread is logit_std) bounds how far each engine "
+                               "choice is from the oracle's"}}
 
 
 def main() -> int:
@@ -585,6 +834,9 @@ def main() -> int:
         del case
         torch.cuda.empty_cache()
 
+    companions = None
+    if not args.no_microbench:
+        companions = time_companion_kernels()
     projections = time_decode_projections()
     prefill = time_prefill_attention(first_prefill_batch(prompts), iters=max(3, args.attention_iters // 4))
     prefill["shape"] = (f"{prefill['sequences']} fresh prompts, {prefill['tokens']} tokens (max {prefill['max_len']}), "
@@ -594,8 +846,8 @@ def main() -> int:
     if args.workload == "decode-attention":
         print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
                           "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro,
-                          "prefill_attention": prefill, "decode_projections": projections,
-                          "copy_calibration": copy_calibration()}))
+                          "companion_kernels_1024": companions, "prefill_attention": prefill,
+                          "decode_projections": projections, "copy_calibration": copy_calibration()}))
         return 0
 
     model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device=device)
@@ -623,6 +875,24 @@ def main() -> int:
     stats = engine.last_stats
     steady = engine.scheduler.steady_state_summary()
     value = generated / elapsed
+    run_weighted = by_rows = None
+    if not args.no_microbench:
+        # One more (untimed) run records every recurrent launch's row positions; decode attention
+        # is then timed over exactly those launches, and at fixed widths of the same contexts.
+        launches: list[np.ndarray] = []
+        launch = engine.runner.compute_recurrent_batch
+
+        def recorded(items):
+            launches.append(np.fromiter((it.token_position for it in items), np.int32, len(items)))
+            return launch(items)
+
+        engine.runner.compute_recurrent_batch = recorded
+        engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+        engine.runner.compute_recurrent_batch = launch
+        torch.cuda.synchronize()
+        run_weighted = run_weighted_decode(launches)
+        mid = np.asarray([len(p) + max(1, o // 2) - 1 for p, o in zip(prompts, outputs)], dtype=np.int32)
+        by_rows = time_by_rows({n: mid[:n] for n in (1, 4, 16, 32, 64, 128, 256)})
     result.update({
         "metric": "output tok/s, Ouro-1.4B-shape CDB decode bs=256; decode-attn HBM GB/s % of peak",
         "value": round(value, 1),
@@ -641,7 +911,10 @@ def main() -> int:
                                "refill, block 16, kv single",
                    "global_batch": args.num_seqs, "parallelism": "none"},
         "roofline": roofline,
+        "decode_attention_run_weighted": run_weighted,
+        "decode_attention_by_rows": by_rows,
         "decode_attention_microbench": micro,
+        "companion_kernels_1024": companions,
         "prefill_attention": prefill,
         "decode_projections": projections,
         "engine": {"generated_tokens": generated, "recurrent_batches": stats.recurrent_batches,

@@ -95,6 +95,12 @@ class ContinuousDepthBatchingConfig:
     kv_slots_per_layer: int | None = None
     kv_pressure_mode: KVPressureMode = "recompute"
     cpu_offload_space: float | None = None
+    # Not a reference field. With a multi-slot KV policy, let one recurrent launch carry rows that
+    # write different KV slots: the decode kernel reads a cache layer per row, so the reference's
+    # slot-homogeneous launches are a constraint of its attention backend, not of the math. Off
+    # (the default) keeps the reference's schedule; on changes which rows share a launch, never a
+    # row's result.
+    mixed_slot_recurrent_batches: bool = False
 
     def decode_block_table_width(self) -> int:
         return -(-self.max_model_len // self.block_size)

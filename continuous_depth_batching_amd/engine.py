@@ -200,7 +200,8 @@ class ContinuousDepthBatchingEngine:
         scheduler = CDBScheduler(cache, cfg.max_recurrent_steps, safety_margin=cfg.safety_margin,
                                  kv_pressure_mode=cfg.kv_pressure_mode, max_model_len=cfg.max_model_len,
                                  max_num_seqs=cfg.max_num_seqs, min_free_slots=cfg.min_free_slots,
-                                 min_coda_batch_size=cfg.min_coda_batch_size)
+                                 min_coda_batch_size=cfg.min_coda_batch_size,
+                                 mixed_slot_launches=cfg.mixed_slot_recurrent_batches)
         exit_kv_layout = layout if copies_exit_kv(cfg.kv_policy) else None
         offloading_manager = OffloadingManager(cache, scheduler, cfg.cpu_offload_space,
                                                allow_recompute_fallback=not copies_exit_kv(cfg.kv_policy),

@@ -7,7 +7,8 @@ Recurrent work is a FIFO deque; a stepped batch's survivors and freshly
 sampled successors return to its head in launch order, which keeps a bounded
 working set advancing (:142-180). Under multi-slot KV layouts a recurrent
 batch holds only items writing the same slot (:322-346). Admission, token
-budgets and block allocation follow scheduler_base.py:171-545.
+budgets and block allocation follow scheduler_base.py:171-545. ``mixed_slot_launches`` lifts the
+slot rule (the kernels read a cache layer per row).
 """
 
 from __future__ import annotations
@@ -44,7 +45,8 @@ class ScheduledCDBBatch:
 class CDBScheduler:
     def __init__(self, cache: PagedKVCache, max_recurrent_steps: int, *, safety_margin: float = 0.2,
                  kv_pressure_mode: str = "recompute", max_model_len: int | None = None, max_num_seqs: int = 256,
-                 min_free_slots: int | None = None, min_coda_batch_size: int = 1) -> None:
+                 min_free_slots: int | None = None, min_coda_batch_size: int = 1,
+                 mixed_slot_launches: bool = False) -> None:
         if max_recurrent_steps <= 0:
             raise ValueError(f"max_recurrent_steps must be positive, got {max_recurrent_steps}")
         if min_coda_batch_size <= 0:
@@ -60,6 +62,7 @@ class CDBScheduler:
         self.min_free_slots = resolve_min_free_slots(min_free_slots, self.max_num_seqs)
         self.max_recurrent_steps = max_recurrent_steps
         self.min_coda_batch_size = min(min_coda_batch_size, self.max_num_seqs)
+        self.slot_homogeneous = cache.requires_slot_homogeneous_recurrent_batches and not mixed_slot_launches
         # Completions before the steady-state window opens (steady_state_summary); None leaves it off.
         self.steady_warmup_requests: int | None = None
         if kv_pressure_mode == "reserve":
@@ -424,7 +427,7 @@ class CDBScheduler:
             return []
         first = self.ready_queue.popleft()
         batch = [first]
-        if self.cache.requires_slot_homogeneous_recurrent_batches:
+        if self.slot_homogeneous:
             target = self.cache.kv_slot_for_recurrent_step(first.recurrent_step)
             deferred: deque[DepthWorkItem] = deque()
             while self.ready_queue and len(batch) < size:

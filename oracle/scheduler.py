@@ -29,7 +29,8 @@ Scheduling follows, in the reference:
     1671-1724, exit_policy.py:87-169;
   * the no-refill wave loop on the synchronous horizon -- continuous_api.py:608-944.
 
-``replay_offset_one`` forces the replay horizon (the reference's tests force the delayed replay
+``mixed_slot_recurrent_batches`` drops the slot-homogeneous launch rule (an option of this build's
+engine, not of the reference). ``replay_offset_one`` forces the replay horizon (the reference's tests force the delayed replay
 path on CPU the same way); by default it follows the configuration.
 
 Timing is taken out of the schedule: every staged prefill or coda result is treated as ready at
@@ -122,7 +123,7 @@ class ScheduleOracle:
                  synthetic_exit_replay: bool = False, exit_threshold: float | None = None,
                  rule: str = HAZARD, offset_one_signal: bool = False, min_recurrent_steps: int = 1,
                  vocab_size: int = 16, replay_eos_finishes: bool = False,
-                 replay_offset_one: bool | None = None) -> None:
+                 replay_offset_one: bool | None = None, mixed_slot_recurrent_batches: bool = False) -> None:
         self.R = max_recurrent_steps
         self.num_blocks = num_blocks
         self.bs = block_size
@@ -141,6 +142,7 @@ class ScheduleOracle:
         else:
             self.slots = 2 if kv_slots_per_layer is None else kv_slots_per_layer
         self.copy_on_exit = kv_policy == "last_exited"
+        self.slot_homogeneous = self.slots > 1 and not mixed_slot_recurrent_batches
         self.refill = refill
         self.use_async = use_async_batching
         overlap = delay_gate_consumption and use_async_batching
@@ -676,7 +678,7 @@ class ScheduleOracle:
         size = min(self.cap, len(self.ready))
         head = self.ready.popleft()
         batch = [head]
-        if self.slots > 1:
+        if self.slot_homogeneous:
             target = self._kv_slot(head.step)
             rest: deque[_Item] = deque()
             while self.ready and len(batch) < size:

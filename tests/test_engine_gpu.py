@@ -132,3 +132,25 @@ def test_bf16_model_tokens_track_oracle() -> None:
     first_agree = np.mean([o.generated_tokens[0] == w.tokens[0] for o, w in zip(outs, want)])
     assert first_agree >= 0.75
     assert all(len(o.generated_tokens) == m for o, m in zip(outs, mnt))
+
+
+@pytest.mark.parametrize("refill", [True])
+def test_mixed_slot_launches_last_exited_follow_the_oracle(refill: bool) -> None:
+    """Per-step KV with exit copies, one launch mixing rows that write different KV slots: the
+    per-row cache layers and the exit-copy flush before each launch keep every token's math the
+    per-request oracle's."""
+
+    model, weights = build_model(seed=7)
+    prompts, mnt = workload(seed=7, n=10, new_tokens=20)
+    rng = np.random.default_rng(8)
+    depths = [rng.choice(4, size=m - 1, p=[0.15, 0.25, 0.3, 0.3]).tolist() for m in mnt]
+    engine = make_engine(model, synthetic_exit_replay=True, kv_policy="last_exited", delay_gate_consumption=False,
+                         refill=refill, max_num_seqs=8, mixed_slot_recurrent_batches=True)
+    engine.record_launches = True
+    outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=None, exit_depths=depths)
+    want = run_oracle(weights, prompts, mnt, kv_policy="last_exited", exit_depths=depths)
+    assert [o.generated_tokens for o in outs] == [w.tokens for w in want]
+    assert [o.exit_depths for o in outs] == depths
+    assert engine.last_stats.exit_kv_copies == sum(w.exit_copies for w in want)
+    mixed = [ev for ev in engine.launch_log if ev[0] == "recurrent" and len({row[2] for row in ev[1]}) > 1]
+    assert mixed, "launches must mix loop steps (and so KV slots)"

@@ -155,3 +155,23 @@ def test_the_comparison_catches_a_planted_scheduling_mistake(monkeypatch, mistak
                synthetic_exit_replay=True)
     with pytest.raises(AssertionError):
         assert_same_schedule(*run_both(cfg, prompts, mnt, depths=depths))
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("policy", ["last_exited", "first_then_shared"])
+def test_mixed_slot_launches_match_the_oracle_and_keep_results(seed, policy) -> None:
+    """With mixed-slot launches the schedule still matches the oracle run with the same option,
+    launches do mix KV slots, and tokens and exit depths equal the slot-homogeneous run's."""
+
+    min_depth = 1 if policy == "first_then_shared" else 0
+    prompts, mnt, depths = workload(seed + 40, 10, 4, min_depth=min_depth)
+    base = dict(BIG, max_num_seqs=6, kv_policy=policy, use_async_batching=True, delay_gate_consumption=False,
+                synthetic_exit_replay=True)
+    engine, outs, want = run_both(dict(base, mixed_slot_recurrent_batches=True), prompts, mnt, depths=depths)
+    assert_same_schedule(engine, outs, want)
+    slot = (lambda t: t) if policy == "last_exited" else (lambda t: min(t, 1))
+    mixed = [ev for ev in engine.launch_log if ev[0] == "recurrent" and len({slot(r[2]) for r in ev[1]}) > 1]
+    assert mixed
+    _, homogeneous, _ = run_both(base, prompts, mnt, depths=depths)
+    assert [o.generated_tokens for o in outs] == [o.generated_tokens for o in homogeneous]
+    assert [o.exit_depths for o in outs] == [o.exit_depths for o in homogeneous]

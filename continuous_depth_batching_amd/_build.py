@@ -38,6 +38,14 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions. The prefill kernel keeps its MFMA accumulators in
+# ordinary VGPRs: its online softmax rescales them between products, which in
+# the accumulator-register form costs a move out and back for every element.
+FILE_FLAGS = {
+    "prefill_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _hipcc() -> str:
     for candidate in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if candidate and Path(candidate).exists():
@@ -53,11 +61,11 @@ def _needs_rebuild(obj: Path, src: Path, headers: list[Path]) -> bool:
     if not obj.exists():
         return True
     obj_mtime = obj.stat().st_mtime
-    return any(dep.stat().st_mtime > obj_mtime for dep in (src, *headers))
+    return any(dep.stat().st_mtime > obj_mtime for dep in (src, *headers, Path(__file__)))
 
 
 def _compile(hipcc: str, src: Path, obj: Path) -> None:
-    cmd = [hipcc, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc, *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")

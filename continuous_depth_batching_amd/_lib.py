@@ -109,6 +109,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P,  # H, Hkv, D, block_size, scale, dtype, stream
         ],
     ),
+    "cdb_prefill_partial_bytes": (c_int64, [c_int32, c_int32, c_int32]),
+    "cdb_prefill_attention_split": (
+        c_int32,
+        [
+            _P, _P, _P, c_int64, c_int32, c_int32, c_int64,  # q, k_pool, v_pool, layer_stride, layer, layers, blocks
+            _P, _P, c_int32, _P, _P, c_int32,  # block_table, table_row, width, cu_q, past, num_seqs
+            _P, c_int32, _P, c_int32, c_int32,  # items, num_items, merges, num_merges, num_slots
+            _P, c_int64, _P,  # partials, partials_bytes, out
+            c_int32, c_int32, c_int32, c_int32, c_float, c_int32, _P,  # H, Hkv, D, block_size, scale, dtype, stream
+        ],
+    ),
     "cdb_linear_pack_weight": (c_int32, [_P, c_int64, _P, c_int64, c_int32, c_int32, _P]),
     "cdb_linear": (
         c_int32,

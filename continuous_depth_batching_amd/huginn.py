@@ -393,8 +393,7 @@ class HuginnCDBAdapter(CDBModelAdapter):
             ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
                                   self.rope_cos, self.rope_sin, ROPE_INTERLEAVED, w["q_bias"], w["k_bias"])
             out = torch.empty_like(q_rot)
-            ops.prefill_attention_raw(q_rot, cache.view, layer, cache.device_table, launch.table_rows, launch.cu_q,
-                                      launch.past, launch.tile_seq, launch.tile_q0, out, self.scale)
+            ops.prefill_attention_launch(q_rot, cache.view, layer, cache.device_table, launch, out, self.scale)
             return out.view(tokens, self.num_heads, self.head_dim)
 
         return attend

@@ -91,6 +91,12 @@ class PrefillLaunch:
     tile_q0: torch.Tensor        # [tiles] int32
     last_index: torch.Tensor     # [N] int64 token index whose logits sample the next token
     cache: PagedKVCache
+    # bf16 only: the tiles as a split work list (cdb_prefill_attention_split), with its
+    # partial-result buffer; None runs the whole tiles above.
+    split_items: torch.Tensor | None = None   # [n, 4] int32
+    split_merges: torch.Tensor | None = None  # [m, 4] int32
+    split_slots: int = 0
+    partials: torch.Tensor | None = None
 
 
 class CDBModelAdapter(ABC):

@@ -193,6 +193,12 @@ class ModelRunner:
                                               cache.block_size, ops.MIN_SPLIT_PAGES)
         del num_kv_heads
         self.workspace = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=self.device)
+        # bf16 prefill attention splits long tiles over several workgroups (ops.prefill_split_work);
+        # the parts' partial results live in a buffer grown on demand on the runner's stream.
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.num_cus = torch.cuda.get_device_properties(self.device).multi_processor_count
+        self.partials = torch.empty(0, dtype=torch.float32, device=self.device)
         self._buckets: dict[int, _RecurrentBucket] = {}
         self.graph_pool = torch.cuda.graph_pool_handle() if self.use_graphs else None
         spec = model_adapter.exit_policy_spec()
@@ -204,6 +210,10 @@ class ModelRunner:
         self.stage_graph_captures = 0
         self._coda_turns: list[_CodaTurn | None] = [None] * self.CODA_TURNS
         self._coda_turn_index = 0
+        # The cache, bank and workspace above were filled on the caller's stream; the compute
+        # stream must not run ahead of those fills (a block table still being set to -1 while
+        # the first prefill reads it).
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
 
     # -- hidden slots (cdb/model_runner.py:1193-1203, 1359-1363) ------------------------------------------------
     def reset_cdb_runtime_counters(self) -> None:
@@ -232,8 +242,10 @@ class ModelRunner:
     # -- helpers --------------------------------------------------------------------------------------------------
     def stream_scope(self):
         """Make the compute stream current for a whole generate_batch, so the per-call
-        scopes below find it already set."""
+        scopes below find it already set. Work the caller queued before (on its own stream)
+        is ordered before everything the call runs."""
 
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
         return torch.cuda.stream(self.stream)
 
     def _on_stream(self):
@@ -241,10 +253,19 @@ class ModelRunner:
 
         if torch._C._cuda_getCurrentRawStream(self._device_index) == self._stream_handle:
             return nullcontext()
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
         return torch.cuda.stream(self.stream)
 
     def _pinned(self, shape: tuple[int, ...] | int, dtype: torch.dtype) -> torch.Tensor:
         return torch.empty(shape, dtype=dtype, pin_memory=True)
+
+    def _prefill_partials(self, num_slots: int) -> torch.Tensor:
+        """The split prefill's partial-result buffer for `num_slots` slots (call on the runner's stream)."""
+
+        need = -(-ops.prefill_partial_bytes(num_slots, self.num_heads, self.head_dim) // 4)
+        if self.partials.numel() < need:
+            self.partials = torch.empty(need, dtype=torch.float32, device=self.device)
+        return self.partials
 
     def _to_device(self, array: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
         host = self._pinned(array.shape, dtype)
@@ -531,6 +552,9 @@ class ModelRunner:
         meta = self.prefill_metadata(requests)
         last_index = meta.last_index
         tile_seq, tile_q0 = ops.prefill_tiles(meta.lens, meta.past)
+        split = None
+        if self.dtype == torch.bfloat16 and len(meta.lens):
+            split = ops.prefill_split_plan(meta.lens, meta.past, num_heads=self.num_heads, num_cus=self.num_cus)
         with self._on_stream():
             cache.flush_table_updates()
             launch = PrefillLaunch(
@@ -545,6 +569,11 @@ class ModelRunner:
                 last_index=self._to_device(last_index, torch.int64),
                 cache=cache,
             )
+            if split is not None:
+                launch.split_items = self._to_device(split.items, torch.int32)
+                launch.split_merges = self._to_device(split.merges, torch.int32)
+                launch.split_slots = split.num_slots
+                launch.partials = self._prefill_partials(split.num_slots)
             if len(last_index):
                 device_tokens = self.adapter.prefill(launch)
             else:

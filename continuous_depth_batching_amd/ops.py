@@ -817,12 +817,12 @@ def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: 
     _lib.check(code, "cdb_rope_kv_write")
 
 
-PREFILL_TILE = 64
+PREFILL_TILE = 128
 
 
 def prefill_tiles(query_lens: "list[int] | np.ndarray",
                   past: "list[int] | np.ndarray | None" = None) -> tuple["np.ndarray", "np.ndarray"]:
-    """Tile -> (sequence, first query) arrays for cdb_prefill_attention (64 queries per tile),
+    """Tile -> (sequence, first query) arrays for cdb_prefill_attention (128 queries per tile),
     longest causal prefix (past + last query of the tile) first, so the heaviest workgroups
     start first and the launch ends on short ones. Any order computes the same outputs."""
 
@@ -837,6 +837,148 @@ def prefill_tiles(query_lens: "list[int] | np.ndarray",
     key_end = base[seq] + np.minimum(q0 + PREFILL_TILE, lens[seq])
     order = np.argsort(-key_end, kind="stable")
     return seq[order].astype(np.int32), q0[order].astype(np.int32)
+
+
+PREFILL_KEY_BLOCK = 32  # keys per block of the bf16 prefill kernel's key loop
+
+
+@dataclass(frozen=True)
+class PrefillSplitWork:
+    """Host work list of cdb_prefill_attention_split.
+
+    items  [n, 4] int32: (sequence, first query, first key block | end key block << 16, slot or -1)
+    merges [m, 4] int32: (sequence, first query, first slot, parts)
+    """
+
+    items: "np.ndarray"
+    merges: "np.ndarray"
+    num_slots: int
+    max_blocks: int
+
+
+PREFILL_WGS_PER_CU = 3  # resident bf16 prefill workgroups per CU (LDS and registers)
+
+
+def prefill_split_blocks(total_blocks: int, num_heads: int, num_cus: int) -> int:
+    """Longest key range, in 32-key blocks, that one workgroup takes when tiles are split: an
+    even share of all key blocks over the resident workgroup slots, at least 16 blocks (a part
+    re-reads its tile's queries and writes a 66 KiB partial per head, which the merge reads)."""
+
+    slots = PREFILL_WGS_PER_CU * int(num_cus)
+    return max(16, -(-int(total_blocks) * int(num_heads) // slots))
+
+
+def prefill_split_plan(query_lens: "list[int] | np.ndarray", past: "list[int] | np.ndarray | None" = None, *,
+                       num_heads: int, num_cus: int = 256) -> "PrefillSplitWork | None":
+    """The split work list when one tile's key range is long enough to outlast the whole rest of
+    the launch (more than four times an even share of the key blocks over the workgroup slots,
+    e.g. a chunk appended to a long history); None when whole tiles are the faster launch, as
+    for a batch of fresh prompts, where the throughput of the full GPU sets the time."""
+
+    import numpy as np
+
+    seq, q0 = prefill_tiles(query_lens, past)
+    if seq.size == 0:
+        return None
+    lens = np.asarray(query_lens, dtype=np.int64)
+    base = np.zeros(lens.size, np.int64) if past is None else np.asarray(past, dtype=np.int64)
+    key_end = base[seq] + np.minimum(q0 + PREFILL_TILE, lens[seq])
+    blocks = (key_end + PREFILL_KEY_BLOCK - 1) // PREFILL_KEY_BLOCK
+    share = int(blocks.sum()) * int(num_heads) / (PREFILL_WGS_PER_CU * int(num_cus))
+    max_blocks = prefill_split_blocks(int(blocks.sum()), num_heads, num_cus)
+    if int(blocks.max()) <= max(4 * share, max_blocks):
+        return None
+    return prefill_split_work(query_lens, past, num_heads=num_heads, num_cus=num_cus, max_blocks=max_blocks)
+
+
+def prefill_split_work(query_lens: "list[int] | np.ndarray", past: "list[int] | np.ndarray | None" = None, *,
+                       num_heads: int, num_cus: int = 256, max_blocks: int | None = None) -> PrefillSplitWork:
+    """Split the 128-query tiles whose key range exceeds `max_blocks` blocks into parts of at
+    most about that many blocks. A tile's last part holds its diagonal (it starts at or before
+    the block of the tile's first query position), so every query sees a key in every part.
+    Items are listed longest key range first."""
+
+    import numpy as np
+
+    seq, q0 = prefill_tiles(query_lens, past)
+    lens = np.asarray(query_lens, dtype=np.int64)
+    base = np.zeros(lens.size, np.int64) if past is None else np.asarray(past, dtype=np.int64)
+    first_pos = base[seq] + q0
+    key_end = first_pos + np.minimum(PREFILL_TILE, lens[seq] - q0)
+    blocks = (key_end + PREFILL_KEY_BLOCK - 1) // PREFILL_KEY_BLOCK
+    if max_blocks is None:
+        max_blocks = prefill_split_blocks(int(blocks.sum()), num_heads, num_cus)
+    if max_blocks < 8 or int(blocks.max(initial=0)) >= 1 << 15:
+        raise ValueError("need max_blocks >= 8 and fewer than 32768 key blocks per tile")
+    items, merges, slot = [], [], 0
+    for s_, t0, nb, pos in zip(seq.tolist(), q0.tolist(), blocks.tolist(), first_pos.tolist()):
+        if nb <= max_blocks:
+            items.append((s_, t0, nb << 16, -1))
+            continue
+        parts = -(-nb // max_blocks)
+        step = -(-nb // parts)
+        starts = [k * step for k in range(parts)]
+        starts[-1] = min(starts[-1], pos // PREFILL_KEY_BLOCK)
+        ends = starts[1:] + [nb]
+        assert all(a < b for a, b in zip(starts, ends))
+        items.extend((s_, t0, a | (b << 16), slot + k) for k, (a, b) in enumerate(zip(starts, ends)))
+        merges.append((s_, t0, slot, parts))
+        slot += parts
+    items_arr = np.asarray(items, dtype=np.int32).reshape(-1, 4)
+    length = (items_arr[:, 2] >> 16) - (items_arr[:, 2] & 0xFFFF)
+    items_arr = items_arr[np.argsort(-length, kind="stable")]
+    return PrefillSplitWork(items=items_arr, merges=np.asarray(merges, dtype=np.int32).reshape(-1, 4),
+                            num_slots=slot, max_blocks=int(max_blocks))
+
+
+def prefill_partial_bytes(num_slots: int, num_heads: int, head_dim: int) -> int:
+    n = int(_lib.lib().cdb_prefill_partial_bytes(num_slots, num_heads, head_dim))
+    if n < 0:
+        raise ValueError("invalid prefill partial-buffer shape")
+    return n
+
+
+def prefill_attention_split_raw(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor,
+                                table_row: torch.Tensor, cu_q: torch.Tensor, past: torch.Tensor,
+                                items: torch.Tensor, merges: torch.Tensor, num_slots: int, partials: torch.Tensor,
+                                out: torch.Tensor, scale: float) -> None:
+    """Launch ``cdb_prefill_attention_split`` (bf16; no allocation): items [n, 4] and merges [m, 4]
+    int32 on the GPU, partials a caller buffer of at least prefill_partial_bytes(num_slots) bytes."""
+
+    tokens, num_heads, head_dim = q.shape
+    pool = view.pool
+    if out.shape != q.shape or out.dtype != q.dtype or pool.dtype != q.dtype:
+        raise ValueError("out/pool must match q")
+    num_seqs = past.numel()
+    if cu_q.numel() != num_seqs + 1 or table_row.numel() < num_seqs:
+        raise ValueError("inconsistent prefill metadata")
+    if items.dim() != 2 or items.shape[1] != 4 or merges.dim() != 2 or merges.shape[1] != 4:
+        raise ValueError("items and merges must be [n, 4]")
+    _require_int32(block_table=block_table, table_row=table_row, cu_q=cu_q, past=past, items=items, merges=merges)
+    _require_cuda(q, pool, block_table, table_row, cu_q, past, items, merges, partials, out)
+    _require_contiguous(q=q, out=out, block_table=block_table, items=items, merges=merges, partials=partials)
+    nbytes = partials.numel() * partials.element_size()
+    code = _lib.lib().cdb_prefill_attention_split(
+        q.data_ptr(), view.k_ptr, view.v_ptr, view.layer_stride, layer, view.num_cache_layers, view.pool_blocks,
+        block_table.data_ptr(), table_row.data_ptr(), block_table.shape[1], cu_q.data_ptr(), past.data_ptr(),
+        num_seqs, items.data_ptr(), items.shape[0], merges.data_ptr() if merges.numel() else None, merges.shape[0],
+        num_slots, partials.data_ptr() if num_slots else None, nbytes, out.data_ptr(), num_heads, pool.shape[3],
+        head_dim, view.block_size, scale, dtype_code(q.dtype), _stream())
+    _lib.check(code, "cdb_prefill_attention_split")
+
+
+def prefill_attention_launch(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor, launch,
+                             out: torch.Tensor, scale: float) -> None:
+    """Prefill attention of one layer for a prefill launch (model_adapter.PrefillLaunch): the
+    split work list when the launch carries one, else its whole tiles."""
+
+    if launch.split_items is not None:
+        prefill_attention_split_raw(q, view, layer, block_table, launch.table_rows, launch.cu_q, launch.past,
+                                    launch.split_items, launch.split_merges, launch.split_slots, launch.partials,
+                                    out, scale)
+    else:
+        prefill_attention_raw(q, view, layer, block_table, launch.table_rows, launch.cu_q, launch.past,
+                              launch.tile_seq, launch.tile_q0, out, scale)
 
 
 def prefill_attention_raw(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor,

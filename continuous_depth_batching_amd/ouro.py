@@ -358,8 +358,7 @@ class OuroCDBAdapter(CDBModelAdapter):
                 ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
                                       self.rope_cos, self.rope_sin, 1, None, None)
                 out = torch.empty_like(q_rot)
-                ops.prefill_attention_raw(q_rot, cache.view, layer, cache.device_table, launch.table_rows,
-                                          launch.cu_q, launch.past, launch.tile_seq, launch.tile_q0, out, self.scale)
+                ops.prefill_attention_launch(q_rot, cache.view, layer, cache.device_table, launch, out, self.scale)
                 return out
 
             hidden = self._layer_stack(x, residual, attend)

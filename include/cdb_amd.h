@@ -202,14 +202,42 @@ int cdb_rope_kv_write(const void* q, const void* k, const void* v, void* q_out, 
  * cu_q[s] .. cu_q[s+1]-1 of q [T,H,D] (already rotated) at positions
  * past[s] + i; each attends to positions 0..(its own) of cache layer `layer`
  * through block-table row table_row[s]. The chunk's own K/V must already be in
- * the pool. Work is split into tiles of 64 query tokens: tile n covers
- * sequence tile_seq[n], queries tile_q0[n] .. +63. out is [T,H,D]. */
+ * the pool. Work is split into tiles of 128 query tokens: tile n covers
+ * sequence tile_seq[n], queries tile_q0[n] .. +127. out is [T,H,D]. scale must
+ * be positive and finite (CDB_ERR_SHAPE otherwise). */
 int cdb_prefill_attention(const void* q, const void* k_pool, const void* v_pool, int64_t layer_stride, int32_t layer,
                           int32_t num_cache_layers, int64_t pool_blocks, const int32_t* block_table,
                           const int32_t* table_row, int32_t table_width, const int32_t* cu_q, const int32_t* past,
                           int32_t num_seqs, const int32_t* tile_seq, const int32_t* tile_q0, int32_t num_tiles,
                           void* out, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                           float scale, int32_t dtype, hipStream_t stream);
+
+/* Bytes of the partial-result buffer cdb_prefill_attention_split needs for
+ * num_slots partial slots (-1 for invalid arguments). No reference counterpart:
+ * a sizing helper for the split work list below. */
+int64_t cdb_prefill_partial_bytes(int32_t num_slots, int32_t num_heads, int32_t head_dim);
+
+/* cdb_prefill_attention with the key range of long tiles split over several
+ * workgroups (bf16 only), so that one long sequence does not set the length of
+ * the whole launch; same operation, same outputs up to fp32 rounding of the
+ * merge. Replaces the same flash_attn_varlen_func call as cdb_prefill_attention
+ * (continuous_batching/prefill_graph.py:265-309).
+ *   items  [num_items][4] int32: (sequence, first query of the 128-query tile,
+ *          first key block | end key block << 16 (blocks of 32 keys),
+ *          partial slot, or -1 for a whole tile written straight to out).
+ *          A part must not start past the tile's first query position.
+ *   merges [num_merges][4] int32: (sequence, first query, first slot, parts):
+ *          the parts of one split tile occupy consecutive slots.
+ *   partials: cdb_prefill_partial_bytes(num_slots, ...) bytes of scratch.
+ * Two launches on `stream`: the tiles and parts, then the merge. */
+int cdb_prefill_attention_split(const void* q, const void* k_pool, const void* v_pool, int64_t layer_stride,
+                                int32_t layer, int32_t num_cache_layers, int64_t pool_blocks,
+                                const int32_t* block_table, const int32_t* table_row, int32_t table_width,
+                                const int32_t* cu_q, const int32_t* past, int32_t num_seqs, const int32_t* items,
+                                int32_t num_items, const int32_t* merges, int32_t num_merges, int32_t num_slots,
+                                void* partials, int64_t partials_bytes, void* out, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                int32_t dtype, hipStream_t stream);
 
 /* Repack a bf16 weight w [rows, in_features] (row stride ldw) into the operand
  * order cdb_linear reads: for each tile of 16 rows and each 32-element step of

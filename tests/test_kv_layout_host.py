@@ -139,3 +139,57 @@ def test_prefill_tiles_cover_every_query_tile_once_longest_prefix_first() -> Non
     # Without past lengths the prefixes are the query positions alone.
     seq0, q00 = ops.prefill_tiles(lens)
     assert sorted(zip(seq0.tolist(), q00.tolist())) == want
+
+
+@pytest.mark.parametrize("max_blocks", [8, 16, 37])
+def test_prefill_split_work_partitions_each_tile_and_keeps_the_diagonal_in_the_last_part(max_blocks: int) -> None:
+    """Every tile's key blocks [0, blocks) are covered once by consecutive parts of at most about
+    max_blocks blocks; a split tile's last part starts at or before the block of the tile's first
+    query (so each query sees a key of every part); slots are consecutive per merge and unique;
+    items are listed longest first."""
+
+    import numpy as np
+
+    from continuous_depth_batching_amd import ops
+
+    lens = np.array([130, 1, 64, 65, 300, 900])
+    past = np.array([0, 5000, 10, 1000, 64, 0])
+    work = ops.prefill_split_work(lens, past, num_heads=4, max_blocks=max_blocks)
+    parts: dict[tuple[int, int], list[tuple[int, int, int]]] = {}
+    for s, q0, kv, slot in work.items.tolist():
+        parts.setdefault((s, q0), []).append((kv & 0xFFFF, kv >> 16, slot))
+    want_tiles = sorted((s, t) for s, n in enumerate(lens.tolist()) for t in range(0, n, ops.PREFILL_TILE))
+    assert sorted(parts) == want_tiles
+    merges = {(s, q0): (first, n) for s, q0, first, n in work.merges.tolist()}
+    slots = []
+    for (s, q0), ps in parts.items():
+        ps.sort()
+        key_end = past[s] + min(q0 + ops.PREFILL_TILE, lens[s])
+        blocks = -(-key_end // ops.PREFILL_KEY_BLOCK)
+        assert ps[0][0] == 0 and ps[-1][1] == blocks
+        assert all(a[1] == b[0] for a, b in zip(ps, ps[1:]))
+        if len(ps) == 1:
+            assert ps[0][2] == -1 and (s, q0) not in merges
+            assert blocks <= max_blocks
+            continue
+        assert ps[-1][0] <= (past[s] + q0) // ops.PREFILL_KEY_BLOCK
+        assert all(b - a <= max_blocks + 5 for a, b, _ in ps)
+        first, n = merges[(s, q0)]
+        assert [slot for _, _, slot in ps] == list(range(first, first + n))
+        slots.extend(range(first, first + n))
+    assert sorted(slots) == list(range(work.num_slots))
+    length = (work.items[:, 2] >> 16) - (work.items[:, 2] & 0xFFFF)
+    assert (np.diff(length) <= 0).all()
+
+
+def test_prefill_split_plan_splits_only_a_tile_that_outlasts_the_launch() -> None:
+    import numpy as np
+
+    from continuous_depth_batching_amd import ops
+
+    # Fresh prompts: many tiles, none longer than four even shares -> whole tiles.
+    assert ops.prefill_split_plan(np.full(27, 300), None, num_heads=16, num_cus=256) is None
+    # A short chunk after a long history: a handful of tiles with thousands of keys each.
+    plan = ops.prefill_split_plan([128] * 4, [16000] * 4, num_heads=16, num_cus=256)
+    assert plan is not None and plan.num_slots > 0 and len(plan.merges) == 4
+    assert ops.prefill_partial_bytes(plan.num_slots, 16, 128) == plan.num_slots * 16 * 128 * 130 * 4

@@ -270,3 +270,62 @@ def test_rope_kv_write_and_prefill_attention(dtype: str, head_dim: int, heads: i
     assert err.max() <= max_tol, err.max()
     assert err.mean() <= mean_tol, err.mean()
     del seq_of
+
+
+@pytest.mark.parametrize("dtype,head_dim,heads,kv_heads,q_gain", [("bf16", 128, 4, 4, 1.0), ("bf16", 128, 4, 2, 6.0),
+                                                                  ("bf16", 64, 4, 1, 6.0), ("f32", 64, 2, 2, 6.0)])
+def test_prefill_attention_long_prefixes(dtype: str, head_dim: int, heads: int, kv_heads: int, q_gain: float) -> None:
+    """Prefixes of up to 17k cached positions (past the 1024 block ids a workgroup keeps
+    in LDS), chunks that are not whole 128-query tiles, a one-token chunk, and with
+    q_gain 6 scores spread wide enough that the running max moves by more than 2^8
+    (exp2 units) many times along a row."""
+
+    from continuous_depth_batching_amd import ops
+
+    rng = np.random.default_rng(head_dim + kv_heads)
+    rnd = rounder(dtype)
+    bs = 16
+    pasts = np.array([700, 0, 17000, 3000, 255], np.int64)
+    lens = np.array([300, 129, 128, 1, 257], np.int64)
+    totals = pasts + lens
+    pages = (totals + bs - 1) // bs
+    perm = rng.permutation(int(pages.sum()) + 3).astype(np.int32)
+    table = np.full((lens.size, int(pages.max())), -1, np.int32)
+    cur = 0
+    for s, n in enumerate(pages):
+        table[s, :n] = perm[cur:cur + n]
+        cur += n
+    rows_total = (int(pages.sum()) + 3) * bs
+    pool = rnd(rng.standard_normal((1, 2, rows_total, kv_heads, head_dim)).astype(np.float32))
+    q = rnd((q_gain * rng.standard_normal((int(lens.sum()), heads, head_dim))).astype(np.float32))
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    scale = head_dim ** -0.5
+    want = prefill_attention(q, pool, 0, table, np.arange(lens.size), cu, pasts, bs, scale, dtype)
+    view = ops.KVPoolView(dev(pool, DT[dtype]).contiguous(), bs)
+    qt = dev(q, DT[dtype])
+    tile_seq, tile_q0 = ops.prefill_tiles(lens, pasts)
+    out = torch.empty_like(qt)
+    ops.prefill_attention_raw(qt, view, 0, dev(table), dev(np.arange(lens.size, dtype=np.int32)), dev(cu),
+                              dev(pasts.astype(np.int32)), dev(tile_seq), dev(tile_q0), out, scale)
+    # With q_gain 6 an output is close to one value row, up to |v| ~ 4.5, where one bf16 ulp of
+    # the output is 0.03: the bound is 2e-2 (2e-5 in fp32) relative to max(1, |want|).
+    max_tol, mean_tol = (2e-2, 2e-3) if dtype == "bf16" else (2e-5, 2e-6)
+    scale_ = np.maximum(1.0, np.abs(want))
+    err = np.abs(host(out) - want)
+    assert (err / scale_).max() <= max_tol, (err / scale_).max()
+    assert err.mean() <= mean_tol, err.mean()
+    if dtype != "bf16":
+        return
+    # The same tiles with their key ranges split over workgroups (8 blocks of 32 keys at most,
+    # so the 17k-key prefix takes dozens of parts) and merged: the oracle's tolerance again.
+    work = ops.prefill_split_work(lens, pasts, num_heads=heads, max_blocks=8)
+    assert work.num_slots > 0 and len(work.merges) > 0
+    partials = torch.empty(ops.prefill_partial_bytes(work.num_slots, heads, head_dim) // 4, dtype=torch.float32,
+                           device="cuda")
+    out_split = torch.full_like(qt, float("nan"))
+    ops.prefill_attention_split_raw(qt, view, 0, dev(table), dev(np.arange(lens.size, dtype=np.int32)), dev(cu),
+                                    dev(pasts.astype(np.int32)), dev(work.items), dev(work.merges), work.num_slots,
+                                    partials, out_split, scale)
+    err = np.abs(host(out_split) - want)
+    assert (err / scale_).max() <= max_tol, (err / scale_).max()
+    assert err.mean() <= mean_tol, err.mean()

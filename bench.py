@@ -377,23 +377,36 @@ def measured_traffic() -> int | None:
     return int(json.loads(path.read_text())["traffic_bytes_per_call"])
 
 
-def time_prefill_attention(prompt_lens, iters: int) -> dict:
-    """Average duration of one prefill-attention launch over a batch of fresh prompts, on its stream."""
+def time_prefill_attention(prompt_lens, iters: int, past=None) -> dict:
+    """Average duration of one prefill-attention call over a batch (fresh prompts, or new tokens
+    after `past` cached positions), on its stream, through the path the engine takes for it:
+    whole tiles, or the split work list with its merge when one tile would outlast the rest."""
 
     import torch
 
     from continuous_depth_batching_amd import ops, workloads
 
-    case = workloads.prefill_attention_batch(lens=prompt_lens)
+    case = workloads.prefill_attention_batch(lens=prompt_lens, past=past)
     view = ops.KVPoolView(case.kv_pool, case.block_size)
     out = torch.empty_like(case.q)
     stream = torch.cuda.Stream()
-
-    def launch():
-        ops.prefill_attention_raw(case.q, view, 0, case.block_table, case.table_row, case.cu_q, case.past,
-                                  case.tile_seq, case.tile_q0, out, case.q.shape[-1] ** -0.5)
-
+    scale = case.q.shape[-1] ** -0.5
+    plan = ops.prefill_split_plan(case.lens, case.past_lens, num_heads=case.q.shape[1],
+                                  num_cus=torch.cuda.get_device_properties(0).multi_processor_count)
     with torch.cuda.stream(stream):
+        if plan is None:
+            def launch():
+                ops.prefill_attention_raw(case.q, view, 0, case.block_table, case.table_row, case.cu_q, case.past,
+                                          case.tile_seq, case.tile_q0, out, scale)
+        else:
+            items = torch.from_numpy(plan.items).cuda()
+            merges = torch.from_numpy(plan.merges).cuda()
+            partials = torch.empty(ops.prefill_partial_bytes(plan.num_slots, case.q.shape[1], case.q.shape[2]) // 4,
+                                   dtype=torch.float32, device="cuda")
+
+            def launch():
+                ops.prefill_attention_split_raw(case.q, view, 0, case.block_table, case.table_row, case.cu_q,
+                                                case.past, items, merges, plan.num_slots, partials, out, scale)
         for _ in range(2):
             launch()
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -404,9 +417,13 @@ def time_prefill_attention(prompt_lens, iters: int) -> dict:
     end.synchronize()
     ms = start.elapsed_time(end) / iters
     flops = case.flops()
-    return {"ms": round(ms, 4), "flops": flops, "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
-            "mfma_frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "tokens": int(case.lens.sum()),
-            "sequences": int(case.lens.size), "max_len": int(case.lens.max())}
+    result = {"ms": round(ms, 4), "flops": flops, "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+              "mfma_frac": round(flops / (ms * 1e-3) / MFMA_BF16_PEAK, 4), "tokens": int(case.lens.sum()),
+              "sequences": int(case.lens.size), "max_len": int(case.lens.max()),
+              "path": "tiles" if plan is None else "split"}
+    if plan is not None:
+        result.update(items=int(len(plan.items)), merges=int(len(plan.merges)), max_blocks=plan.max_blocks)
+    return result
 
 
 def time_decode_projections(rows: int = 16, layers: int = 24, reps: int = 4) -> dict:
@@ -841,12 +858,15 @@ def main() -> int:
     prefill = time_prefill_attention(first_prefill_batch(prompts), iters=max(3, args.attention_iters // 4))
     prefill["shape"] = (f"{prefill['sequences']} fresh prompts, {prefill['tokens']} tokens (max {prefill['max_len']}), "
                         "16 heads x 128, causal")
+    prefill_history = time_prefill_attention([128] * 4, iters=max(3, args.attention_iters // 4), past=[16000] * 4)
+    prefill_history["shape"] = "4 sequences x 128 new tokens after 16000 cached positions, 16 heads x 128"
     torch.cuda.empty_cache()
 
     if args.workload == "decode-attention":
         print(json.dumps({"metric": "decode-attention HBM GB/s", "value": roofline["achieved"], "unit": "GB/s",
                           "n_gpus": 1, "roofline": roofline, "decode_attention_microbench": micro,
                           "companion_kernels_1024": companions, "prefill_attention": prefill,
+                          "prefill_attention_after_history": prefill_history,
                           "decode_projections": projections, "copy_calibration": copy_calibration()}))
         return 0
 
@@ -916,6 +936,7 @@ def main() -> int:
         "decode_attention_microbench": micro,
         "companion_kernels_1024": companions,
         "prefill_attention": prefill,
+        "prefill_attention_after_history": prefill_history,
         "decode_projections": projections,
         "engine": {"generated_tokens": generated, "recurrent_batches": stats.recurrent_batches,
                    "mean_recurrent_batch": round(stats.mean_recurrent_batch_size, 1),

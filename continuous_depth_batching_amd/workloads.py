@@ -122,24 +122,30 @@ class PrefillAttentionCase:
     tile_q0: torch.Tensor
     lens: np.ndarray
     block_size: int
+    past_lens: np.ndarray | None = None
 
     def flops(self) -> int:
         """4 * H * D * causal (query, key) pairs: QK^T and PV, 2 flops per multiply-add."""
 
         _, h, d = self.q.shape
-        pairs = int((self.lens * (self.lens + 1) // 2).sum())
+        past = np.zeros_like(self.lens) if self.past_lens is None else self.past_lens
+        pairs = int((self.lens * past + self.lens * (self.lens + 1) // 2).sum())
         return 4 * h * d * pairs
 
 
 def prefill_attention_batch(*, lens: np.ndarray, num_heads: int = 16, head_dim: int = 128, block_size: int = 16,
-                            seed: int = 0, dtype: torch.dtype = torch.bfloat16,
+                            seed: int = 0, dtype: torch.dtype = torch.bfloat16, past: np.ndarray | None = None,
                             device: torch.device | str = "cuda") -> PrefillAttentionCase:
+    """A prefill batch: sequence s has `past[s]` cached positions (zero: fresh prompts) and
+    `lens[s]` new query tokens; the pool holds random K/V for every position."""
+
     from . import ops
 
     device = torch.device(device)
     rng = np.random.default_rng(seed)
     lens = np.asarray(lens, dtype=np.int64)
-    pages = (lens + block_size - 1) // block_size
+    past_arr = np.zeros_like(lens) if past is None else np.asarray(past, dtype=np.int64)
+    pages = (past_arr + lens + block_size - 1) // block_size
     perm = rng.permutation(int(pages.sum())).astype(np.int32)
     table = np.full((lens.size, int(pages.max())), -1, dtype=np.int32)
     off = np.concatenate([[0], np.cumsum(pages)])
@@ -150,11 +156,12 @@ def prefill_attention_batch(*, lens: np.ndarray, num_heads: int = 16, head_dim: 
     pool = torch.empty((1, 2, int(pages.sum()) * block_size, num_heads, head_dim), dtype=dtype, device=device)
     pool.normal_(generator=gen)
     q = torch.randn((int(lens.sum()), num_heads, head_dim), generator=gen, device=device).to(dtype)
-    tile_seq, tile_q0 = ops.prefill_tiles(lens)
+    tile_seq, tile_q0 = ops.prefill_tiles(lens, past_arr)
     i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a).astype(np.int32)).to(device)
     return PrefillAttentionCase(q=q, kv_pool=pool, block_table=i32(table), table_row=i32(np.arange(lens.size)),
-                                cu_q=i32(np.concatenate([[0], np.cumsum(lens)])), past=i32(np.zeros(lens.size)),
-                                tile_seq=i32(tile_seq), tile_q0=i32(tile_q0), lens=lens, block_size=block_size)
+                                cu_q=i32(np.concatenate([[0], np.cumsum(lens)])), past=i32(past_arr),
+                                tile_seq=i32(tile_seq), tile_q0=i32(tile_q0), lens=lens, block_size=block_size,
+                                past_lens=past_arr)
 
 
 def lognormal_lengths(rng: np.random.Generator, n: int, mu: float, sigma: float, lo: int, hi: int) -> np.ndarray:

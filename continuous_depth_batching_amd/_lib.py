@@ -146,6 +146,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_int32, c_int32, c_int32, c_int32, _P,  # rows, out_features, in_features, dtype, stream
         ],
     ),
+    "cdb_coda_greedy": (
+        c_int32,
+        [
+            _P, _P, c_int32, c_int32,  # host_upload, dev_upload, rows, num_successors
+            _P, c_int64, c_int32, _P, _P, c_int32,  # bank, bank_rows, width, hidden, w_packed, vocab
+            _P, _P, c_int64, _P, _P,  # tokens, workspace, workspace_bytes, embed, host_tokens
+            _P, _P, _P, c_int64, c_int32, _P,  # cdf, survival, pending, state_capacity, dtype, stream
+        ],
+    ),
 }
 
 

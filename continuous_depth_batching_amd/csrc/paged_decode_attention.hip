@@ -630,6 +630,19 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
   for (int base = 0; base < nsplit; base += 64) {
     const int cnt = min(64, nsplit - base);
     const float* chunk_part = part + (int64_t)base * stride;
+    float a0[8], a1[8];
+    auto load_group = [&](int s0) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const bool ok = s0 + j < cnt;
+        const float* ps = chunk_part + (int64_t)(s0 + j) * stride;
+        a0[j] = ok && d0 < D ? ps[d0] : 0.f;
+        a1[j] = ok && d1 < D ? ps[d1] : 0.f;
+      }
+    };
+    // The first eight splits' accumulators are read with the (max, sum) pairs, so
+    // their loads overlap instead of waiting for the wave reductions.
+    load_group(0);
     float ms = -INFINITY, ls = 0.f;
     if (lane < cnt) {
       ms = chunk_part[lane * stride + D];
@@ -643,14 +656,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
     const float ws = ms == -INFINITY ? 0.f : exp2f(ms - new_m);
     den += wave_sum(ws * ls);
     for (int s0 = 0; s0 < cnt; s0 += 8) {
-      float a0[8], a1[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const bool ok = s0 + j < cnt;
-        const float* ps = chunk_part + (int64_t)(s0 + j) * stride;
-        a0[j] = ok && d0 < D ? ps[d0] : 0.f;
-        a1[j] = ok && d1 < D ? ps[d1] : 0.f;
-      }
+      if (s0 > 0) load_group(s0);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         // Lanes at or past cnt hold a zero weight.

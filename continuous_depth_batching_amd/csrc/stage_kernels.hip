@@ -57,6 +57,9 @@ struct NormParams {
 template <typename T, int NV>
 __global__ void __launch_bounds__(kThreads) rmsnorm_kernel(NormParams P) {
   constexpr int V = 16 / sizeof(T);  // elements per 16-byte vector
+  // Split partials loaded together before any is added: the reads of one row's
+  // partials then overlap instead of paying one cache round trip per split.
+  constexpr int kPartChunk = NV == 1 ? 8 : (NV <= 4 ? 4 : 2);
   __shared__ float lds[kThreads / 64];
   const int64_t row = blockIdx.x;
   if (row >= P.rows) return;
@@ -67,50 +70,93 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_kernel(NormParams P) {
   const T* wb = static_cast<const T*>(P.w_b);
   T* out_h = static_cast<T*>(P.out_h) + row * W;
   T* out_y = P.out_y ? static_cast<T*>(P.out_y) + row * W : nullptr;
+  const bool second = wb != nullptr && out_y != nullptr;
 
   float v[NV][V];
   float rv[NV][V];
   bool live[NV];
-  float ss = 0.f;
+  // The weight vectors do not depend on the row's reductions: their loads are issued
+  // with the row's, so no reduction waits on them.
+  Vec<T, V> wav[NV], wbv[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int col = (k * kThreads + threadIdx.x) * V;
     live[k] = col < W;
     if (live[k]) {
-      if (P.x_parts) {
-        // Split-K partials of the producing projection, summed in split order and
-        // rounded once, as the projection's own output would be.
-#pragma unroll
-        for (int i = 0; i < V; ++i) v[k][i] = 0.f;
-        for (int sp = 0; sp < P.x_splits; ++sp) {
-          const float* part = P.x_parts + ((int64_t)sp * P.rows + row) * W + col;
-#pragma unroll
-          for (int i = 0; i < V; i += 4) {
-            const float4 q4 = *reinterpret_cast<const float4*>(part + i);
-            v[k][i] += q4.x; v[k][i + 1] += q4.y; v[k][i + 2] += q4.z; v[k][i + 3] += q4.w;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < V; ++i) v[k][i] = Elem<T>::round(v[k][i]);
-      } else {
-        Vec<T, V> a;
-        a.load(x + col);
-#pragma unroll
-        for (int i = 0; i < V; ++i) v[k][i] = a.get(i);
-      }
+      wav[k].load(wa + col);
+      if (second) wbv[k].load(wb + col);
       if (r) {
         Vec<T, V> b;
         b.load(r + col);
 #pragma unroll
         for (int i = 0; i < V; ++i) rv[k][i] = b.get(i);
       }
-      if (P.mode == 2) {
+    }
+  }
+  if (P.x_parts) {
+    // Split-K partials of the producing projection, summed in split order and rounded
+    // once, as the projection's own output would be. A chunk's loads use a clamped
+    // split index, so they are unconditional; only the adds are predicated.
 #pragma unroll
-        for (int i = 0; i < V; ++i) v[k][i] = Elem<T>::round(add_rn(rv[k][i], v[k][i]));
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[k][i] = 0.f;
+    const int splits = P.x_splits;
+    for (int s0 = 0; s0 < splits; s0 += kPartChunk) {
+      float4 q[kPartChunk][NV][V / 4];
+#pragma unroll
+      for (int c = 0; c < kPartChunk; ++c) {
+        const int sp = min(s0 + c, splits - 1);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          const int col = (k * kThreads + threadIdx.x) * V;
+          if (!live[k]) continue;
+          const float* part = P.x_parts + ((int64_t)sp * P.rows + row) * W + col;
+#pragma unroll
+          for (int j = 0; j < V / 4; ++j) q[c][k][j] = *reinterpret_cast<const float4*>(part + 4 * j);
+        }
       }
 #pragma unroll
-      for (int i = 0; i < V; ++i) ss = fmaf(v[k][i], v[k][i], ss);
+      for (int c = 0; c < kPartChunk; ++c) {
+        if (s0 + c >= splits) break;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          if (!live[k]) continue;
+#pragma unroll
+          for (int j = 0; j < V / 4; ++j) {
+            v[k][4 * j] += q[c][k][j].x;
+            v[k][4 * j + 1] += q[c][k][j].y;
+            v[k][4 * j + 2] += q[c][k][j].z;
+            v[k][4 * j + 3] += q[c][k][j].w;
+          }
+        }
+      }
     }
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[k][i] = Elem<T>::round(v[k][i]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (!live[k]) continue;
+      const int col = (k * kThreads + threadIdx.x) * V;
+      Vec<T, V> a;
+      a.load(x + col);
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[k][i] = a.get(i);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    if (!live[k]) continue;
+    if (P.mode == 2) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) v[k][i] = Elem<T>::round(add_rn(rv[k][i], v[k][i]));
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss = fmaf(v[k][i], v[k][i], ss);
   }
   const float inv_a = rsqrtf(block_sum(ss, lds) / (float)W + P.eps_a);
   float ss2 = 0.f;
@@ -118,13 +164,11 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_kernel(NormParams P) {
   for (int k = 0; k < NV; ++k) {
     if (!live[k]) continue;
     const int col = (k * kThreads + threadIdx.x) * V;
-    Vec<T, V> w;
-    w.load(wa + col);
     Vec<T, V> o;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       float n = Elem<T>::round(mul_rn(v[k][i], inv_a));
-      n = Elem<T>::round(mul_rn(w.get(i), n));
+      n = Elem<T>::round(mul_rn(wav[k].get(i), n));
       if (P.mode == 1) n = Elem<T>::round(add_rn(rv[k][i], n));
       v[k][i] = n;
       o.set(i, n);
@@ -132,14 +176,13 @@ __global__ void __launch_bounds__(kThreads) rmsnorm_kernel(NormParams P) {
     }
     o.store(out_h + col);
   }
-  if (wb == nullptr || out_y == nullptr) return;
+  if (!second) return;
   const float inv_b = rsqrtf(block_sum(ss2, lds) / (float)W + P.eps_b);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     if (!live[k]) continue;
     const int col = (k * kThreads + threadIdx.x) * V;
-    Vec<T, V> w;
-    w.load(wb + col);
+    const Vec<T, V>& w = wbv[k];
     Vec<T, V> o;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -769,6 +812,38 @@ int cdb_rope_kv_write(const void* q, const void* k, const void* v, void* q_out, 
   if (dtype == CDB_DTYPE_F32) return by_dim(float{});
   if (dtype == CDB_DTYPE_BF16) return by_dim(bf16_t{});
   return CDB_ERR_UNSUPPORTED;
+}
+
+int cdb_coda_greedy(const int64_t* host_upload, int64_t* dev_upload, int32_t rows, int32_t num_successors,
+                    void* bank, int64_t bank_rows, int32_t width, void* hidden, const void* w_packed, int32_t vocab,
+                    int64_t* tokens, void* workspace, int64_t workspace_bytes, const void* embed,
+                    int64_t* host_tokens, double* cdf, double* survival, float* pending, int64_t state_capacity,
+                    int32_t dtype, hipStream_t stream) {
+  if (rows == 0) return CDB_OK;
+  if (!host_upload || !dev_upload || !bank || !hidden || !w_packed || !tokens || !workspace || !host_tokens)
+    return CDB_ERR_NULL;
+  if (rows < 0 || num_successors < 0 || num_successors > rows || width <= 0 || bank_rows <= 0 || vocab <= 0)
+    return CDB_ERR_SHAPE;
+  if (num_successors > 0 && (!embed || !cdf || !survival || !pending)) return CDB_ERR_NULL;
+  if (dtype != CDB_DTYPE_BF16) return CDB_ERR_UNSUPPORTED;
+  // Upload layout: [coda rows' bank slots | per-row successor slot or -1 | successors' slots],
+  // the last two parts only when the successors' prelude is fused (embed given).
+  const int64_t count = embed ? 2 * (int64_t)rows + num_successors : rows;
+  if (hipMemcpyAsync(dev_upload, host_upload, count * sizeof(int64_t), hipMemcpyHostToDevice, stream) != hipSuccess)
+    return CDB_ERR_HIP;
+  const int64_t row_bytes = (int64_t)width * 2;
+  int code = cdb_copy_rows(bank, dev_upload, bank_rows, hidden, nullptr, rows, rows, row_bytes, stream);
+  if (code) return code;
+  code = cdb_linear_argmax(hidden, width, w_packed, tokens, workspace, workspace_bytes, rows, vocab, width, embed,
+                           embed ? bank : nullptr, embed ? bank_rows : 0, embed ? dev_upload + rows : nullptr,
+                           embed ? width : 0, dtype, stream);
+  if (code) return code;
+  if (hipMemcpyAsync(host_tokens, tokens, rows * sizeof(int64_t), hipMemcpyDeviceToHost, stream) != hipSuccess)
+    return CDB_ERR_HIP;
+  if (num_successors > 0)
+    return cdb_exit_gate_reset(cdf, survival, pending, state_capacity, dev_upload + 2 * (int64_t)rows,
+                               num_successors, stream);
+  return CDB_OK;
 }
 
 }  // extern "C"

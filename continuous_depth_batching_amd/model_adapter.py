@@ -159,6 +159,13 @@ class CDBModelAdapter(ABC):
     def coda(self, launch: StageLaunch) -> torch.Tensor:
         """Greedy next tokens [n] int64 for the hidden states in bank rows launch.slots."""
 
+    def coda_weights(self) -> Any | None:
+        """The LM head (and embedding, for the fused successor prelude) of a coda that is
+        exactly an LM head + argmax over the bank rows, as ``ops.CodaWeights``; the runner
+        then runs small codas as one C-ABI call. None keeps every coda on ``coda``."""
+
+        return None
+
 
 def resolve_cdb_model_adapter(model: Any, adapter: CDBModelAdapter | None = None) -> CDBModelAdapter:
     """Explicit adapter, or one inferred from the model type (model_adapter.py:105-122)."""

@@ -156,6 +156,7 @@ class _CodaTurn:
     dev_upload: torch.Tensor
     host_tokens: torch.Tensor  # pinned int64 greedy tokens
     event: Any
+    direct: ops.CodaScratch | None = None  # one-call coda of up to CODA_DIRECT_MAX_ROWS rows
 
 
 class ModelRunner:
@@ -210,6 +211,7 @@ class ModelRunner:
         self.stage_graph_captures = 0
         self._coda_turns: list[_CodaTurn | None] = [None] * self.CODA_TURNS
         self._coda_turn_index = 0
+        self._coda_weights = model_adapter.coda_weights() if self.dtype is torch.bfloat16 else None
         # The cache, bank and workspace above were filled on the caller's stream; the compute
         # stream must not run ahead of those fills (a block table still being set to -1 while
         # the first prefill reads it).
@@ -495,19 +497,27 @@ class ModelRunner:
             successor[:] = -1
             successor[eager_rows] = new_slots
             upload[2 * n:m] = new_slots
+        direct = turn.direct if n <= ops.CODA_DIRECT_MAX_ROWS and (fused or not eager_items) else None
         with self._on_stream():
-            dev = turn.dev_upload[:m]
-            dev.copy_(turn.host_upload[:m], non_blocking=True)
-            launch = self._stage_launch(items, dev[:n])
-            if fused:
-                launch.successor_slots = dev[n:2 * n]
-            tokens = self.adapter.coda(launch)
-            host = turn.host_tokens[:n]
-            host.copy_(tokens, non_blocking=True)
             event = turn.event
-            event.record()
-            if fused:
-                self.gate_state.reset(dev[2 * n:], len(eager_items))
+            host = turn.host_tokens[:n]
+            if direct is not None:
+                # Upload, gather, LM head + argmax (+ successors' prelude), token download
+                # and the successors' gate reset in one call.
+                direct.launch(n, len(eager_items), fused, self._stream_handle)
+                tokens = direct.tokens[:n]
+                event.record(self.stream)
+            else:
+                dev = turn.dev_upload[:m]
+                dev.copy_(turn.host_upload[:m], non_blocking=True)
+                launch = self._stage_launch(items, dev[:n])
+                if fused:
+                    launch.successor_slots = dev[n:2 * n]
+                tokens = self.adapter.coda(launch)
+                host.copy_(tokens, non_blocking=True)
+                event.record()
+                if fused:
+                    self.gate_state.reset(dev[2 * n:], len(eager_items))
         pending = PendingCodaResult(items=items, host_tokens=host, device_tokens=tokens, ready_event=event)
         if fused:
             for item, slot in zip(eager_items, new_slots):
@@ -529,12 +539,16 @@ class ModelRunner:
         if turn is not None:
             turn.event.synchronize()
         if turn is None or turn.host_upload.numel() < upload or turn.host_tokens.numel() < rows:
-            cap = max(upload, 3 * self.max_num_seqs)
+            seqs = max(self.max_num_seqs, ops.CODA_DIRECT_MAX_ROWS)
+            cap = max(upload, 3 * seqs)
             turn = self._coda_turns[k] = _CodaTurn(
                 host_upload=self._pinned((cap,), torch.int64),
                 dev_upload=torch.empty(cap, dtype=torch.int64, device=self.device),
-                host_tokens=self._pinned((max(rows, self.max_num_seqs),), torch.int64),
+                host_tokens=self._pinned((max(rows, seqs),), torch.int64),
                 event=torch.cuda.Event())
+            if self._coda_weights is not None:
+                turn.direct = ops.CodaScratch(self._coda_weights, self.bank, self.gate_state, turn.host_upload,
+                                              turn.dev_upload, turn.host_tokens)
         return turn
 
     def consume_coda_result(self, pending: PendingCodaResult) -> list[int]:

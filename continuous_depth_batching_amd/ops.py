@@ -685,6 +685,69 @@ def lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, packed: torch.Tensor |
     return tokens
 
 
+CODA_DIRECT_MAX_ROWS = 64  # the fused LM head + argmax serves coda batches up to this size
+
+
+@dataclass
+class CodaWeights:
+    """What cdb_coda_greedy reads besides the bank: the packed LM head and, when the coda
+    fuses the successors' prelude, the token embedding."""
+
+    packed: torch.Tensor  # bf16 LM head in cdb_linear_pack_weight order
+    vocab: int
+    width: int
+    embed: torch.Tensor | None
+
+
+class CodaScratch:
+    """Device scratch of one coda turn plus the fixed arguments of cdb_coda_greedy.
+
+    The pointers are resolved once, so a coda tick is one foreign call whose
+    per-call arguments are the row and successor counts and the stream."""
+
+    def __init__(self, weights: CodaWeights, bank: torch.Tensor, state: "GateState", host_upload: torch.Tensor,
+                 dev_upload: torch.Tensor, host_tokens: torch.Tensor) -> None:
+        rows = CODA_DIRECT_MAX_ROWS
+        _require_cuda(bank, weights.packed, dev_upload)
+        if bank.dtype is not torch.bfloat16 or bank.dim() != 2 or bank.shape[1] != weights.width \
+                or not bank.is_contiguous():
+            raise ValueError("the coda reads a contiguous bf16 bank of the LM head's input width")
+        if weights.packed.dtype is not torch.bfloat16 or weights.packed.numel() != weights.vocab * weights.width:
+            raise ValueError("the LM head must be packed bf16 [vocab, width]")
+        if weights.embed is not None and (weights.embed.dtype is not torch.bfloat16
+                                          or weights.embed.shape[1] != weights.width
+                                          or not weights.embed.is_contiguous()):
+            raise ValueError("the embedding must be a contiguous bf16 [vocab, width] table")
+        if host_upload.numel() < 3 * rows or dev_upload.numel() < 3 * rows or host_tokens.numel() < rows:
+            raise ValueError("coda upload buffers are smaller than a full direct coda")
+        self.hidden = torch.empty((rows, weights.width), dtype=torch.bfloat16, device=bank.device)
+        self.tokens = torch.empty((rows,), dtype=torch.int64, device=bank.device)
+        ws_bytes = int(_lib.lib().cdb_linear_argmax_workspace_bytes(rows, weights.vocab))
+        if ws_bytes < 0:
+            raise ValueError(f"no fused argmax for a {weights.vocab}-column LM head")
+        self.workspace = torch.empty((max(ws_bytes // 4, 4),), dtype=torch.float32, device=bank.device)
+        embed = weights.embed.data_ptr() if weights.embed is not None else None
+        self.head = (host_upload.data_ptr(), dev_upload.data_ptr())
+        self.tail_plain = (bank.data_ptr(), bank.shape[0], weights.width, self.hidden.data_ptr(),
+                           weights.packed.data_ptr(), weights.vocab, self.tokens.data_ptr(),
+                           self.workspace.data_ptr(), self.workspace.numel() * 4, None, host_tokens.data_ptr(),
+                           state.cdf.data_ptr(), state.survival.data_ptr(), state.pending.data_ptr(),
+                           state.capacity, _lib.CDB_DTYPE_BF16)
+        self.tail_fused = self.tail_plain[:9] + (embed,) + self.tail_plain[10:] if embed is not None else None
+
+    def launch(self, rows: int, num_successors: int, fused: bool, stream: int) -> None:
+        """Greedy tokens of `rows` coda rows whose slots (and successors) are in the host upload."""
+
+        if not 1 <= rows <= CODA_DIRECT_MAX_ROWS:
+            raise ValueError(f"a direct coda takes 1..{CODA_DIRECT_MAX_ROWS} rows, got {rows}")
+        tail = self.tail_fused if fused else self.tail_plain
+        if tail is None:
+            raise ValueError("the fused successor prelude needs the token embedding")
+        code = _lib.lib().cdb_coda_greedy(*self.head, rows, num_successors if fused else 0, *tail, stream)
+        if code:
+            _lib.check(code, "cdb_coda_greedy")
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """Greedy token per row (first index of the max), without op dispatch."""
 

@@ -365,6 +365,14 @@ class OuroCDBAdapter(CDBModelAdapter):
         last = torch.ops.cdb.gather_rows(hidden, launch.last_index)
         return self.coda_from_hidden(last)
 
+    def coda_weights(self) -> ops.CodaWeights | None:
+        # The coda is the LM head + argmax of the bank rows (the final norm is applied at
+        # the end of every loop step), so the direct call computes exactly coda().
+        if self.lm_head_p is None or self._dtype is not torch.bfloat16 or self.lm_head_w.shape[0] % 16:
+            return None
+        return ops.CodaWeights(packed=self.lm_head_p, vocab=self.lm_head_w.shape[0], width=self.lm_head_w.shape[1],
+                               embed=self.embed.contiguous())
+
     def coda_from_hidden(self, hidden: torch.Tensor) -> torch.Tensor:
         return ops.lm_head_argmax(hidden, self.lm_head_w, self.lm_head_p)
 

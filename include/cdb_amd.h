@@ -309,6 +309,27 @@ int cdb_linear_argmax(const void* x, int64_t ldx, const void* w_packed, int64_t*
                       const void* embed, void* bank, int64_t bank_rows, const int64_t* bank_slots, int32_t width,
                       int32_t dtype, hipStream_t stream);
 
+/* One greedy coda tick in a single call on `stream`, replacing the coda stage's
+ * slot upload, hidden-row gather, LM head + argmax, token download and the
+ * successors' gate-state reset (cdb/model_runner.py:1036-1125, 439-457,
+ * 1359-1363; cdb/exit_policy.py:43-48):
+ *   1. dev_upload[:count] = host_upload[:count] (pinned host memory), where the
+ *      upload is [coda rows' bank slots (rows) | each row's successor bank slot
+ *      or -1 (rows) | the successors' slots (num_successors)] when embed is given
+ *      and only the first part otherwise (count = 2*rows + num_successors or rows);
+ *   2. hidden[r] = bank[dev_upload[r]]  (hidden: [rows, width] device scratch);
+ *   3. cdb_linear_argmax over hidden (ldx = in_features = width) into tokens,
+ *      with the successors' embedding rows written when embed is given;
+ *   4. host_tokens[:rows] = tokens  (pinned host memory, asynchronous);
+ *   5. the gate state of the num_successors successor slots is reset.
+ * The same preconditions as cdb_linear_argmax apply (bf16, 1 <= rows <= 64). The
+ * host buffers must stay untouched until the stream has passed this call. */
+int cdb_coda_greedy(const int64_t* host_upload, int64_t* dev_upload, int32_t rows, int32_t num_successors,
+                    void* bank, int64_t bank_rows, int32_t width, void* hidden, const void* w_packed, int32_t vocab,
+                    int64_t* tokens, void* workspace, int64_t workspace_bytes, const void* embed,
+                    int64_t* host_tokens, double* cdf, double* survival, float* pending, int64_t state_capacity,
+                    int32_t dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,7 @@ import argparse
 import json
 import os
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -38,6 +39,7 @@ sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK = 2.5e15  # dense bf16 MFMA flop/s
+FORCED_TOKENS = 64  # tokens of the teacher-forced parity pass
 
 
 def parse_args() -> argparse.Namespace:
@@ -75,6 +77,49 @@ def ouro_1p4b_config():
     from continuous_depth_batching_amd.ouro import ouro_1p4b_config as config
 
     return config()
+
+
+class GpuActivity:
+    """GPU activity (amdsmi gfx_activity, percent) sampled every `interval` seconds while
+    active, on a side thread; None when amdsmi is not importable or has no device."""
+
+    def __init__(self, interval: float = 0.02) -> None:
+        self.interval = interval
+        self.samples: list[float] = []
+        self._stop = threading.Event()
+        self._thread: threading.Thread | None = None
+        self.error: str | None = None
+
+    def _run(self) -> None:
+        try:
+            import amdsmi
+
+            amdsmi.amdsmi_init()
+            try:
+                handle = amdsmi.amdsmi_get_processor_handles()[0]
+                while not self._stop.is_set():
+                    self.samples.append(float(amdsmi.amdsmi_get_gpu_activity(handle)["gfx_activity"]))
+                    self._stop.wait(self.interval)
+            finally:
+                amdsmi.amdsmi_shut_down()
+        except Exception as exc:  # noqa: BLE001 - reported, never fatal to the benchmark
+            self.error = f"{type(exc).__name__}: {exc}"
+
+    def __enter__(self) -> "GpuActivity":
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc) -> None:
+        self._stop.set()
+        if self._thread is not None:
+            self._thread.join(timeout=5)
+
+    def summary(self) -> dict | None:
+        if not self.samples:
+            return {"mean_pct": None, "samples": 0, "error": self.error}
+        return {"mean_pct": round(float(np.mean(self.samples)), 1), "samples": len(self.samples),
+                "interval_s": self.interval, "source": "amdsmi gfx_activity during the timed generate_batch calls"}
 
 
 def time_decode_attention(case, split_pages: int, iters: int) -> dict:
@@ -758,12 +803,15 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int, engine_tok
     # bf16 rounding noise flips greedy choices between any two correct implementations (the oracle
     # with fp32 and with fp64 accumulation already disagree on this request's first token); the
     # margin, against the spread of the logits, is what separates noise from a wrong result.
+    # The forced pass covers the first FORCED_TOKENS tokens only: it is a check, not the
+    # timed sample, and the GPU idles while it runs.
     trace: list = []
-    forced = oracle.generate(prompts[idx], n, max_steps=cfg.total_ut_steps, kv_policy="single",
-                             exit_depths=depths[idx][: n - 1], forced_tokens=got, hidden_trace=trace)
+    nf = min(len(got), FORCED_TOKENS)
+    forced = oracle.generate(prompts[idx], nf, max_steps=cfg.total_ut_steps, kv_policy="single",
+                             exit_depths=depths[idx][: nf - 1], forced_tokens=got[:nf], hidden_trace=trace)
     final = {j: h for j, _, h in trace}
     margins, spreads = [], []
-    for j, token in enumerate(got):
+    for j, token in enumerate(got[:nf]):
         logits = oracle.logits(final[j]).astype(np.float64)
         margins.append(float(logits.max() - logits[token]))
         spreads.append(float(logits.std()))
@@ -774,8 +822,9 @@ def cpu_baseline(model, prompts, outputs, depths, sample_tokens: int, engine_tok
             "parity": {"request": idx, "tokens_compared": len(out.tokens), "matched_prefix": matched,
                        "matched_prefix_frac": round(matched / len(out.tokens), 4),
                        "first_token_equal": bool(got and got[0] == out.tokens[0]),
+                       "teacher_forced_tokens": nf,
                        "teacher_forced_argmax_agreement": round(float(np.mean(
-                           [a == b for a, b in zip(forced.tokens, got)])), 4),
+                           [a == b for a, b in zip(forced.tokens, got[:nf])])), 4),
                        "teacher_forced_max_logit_margin": round(max(margins), 4),
                        "teacher_forced_mean_logit_margin": round(float(np.mean(margins)), 5),
                        "logit_std": round(float(np.mean(spreads)), 4),
@@ -886,12 +935,13 @@ def main() -> int:
                               exit_depths=[d[: min(o, 24) - 1] for d, o in zip(depths[:k], outputs[:k])])
     torch.cuda.synchronize()
     generated = 0
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
-        generated += sum(len(o.generated_tokens) for o in outs)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
+    with GpuActivity() as activity:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            outs = engine.generate_batch(prompts, max_new_tokens=outputs, eos_token_id=None, exit_depths=depths)
+            generated += sum(len(o.generated_tokens) for o in outs)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
     stats = engine.last_stats
     steady = engine.scheduler.steady_state_summary()
     value = generated / elapsed
@@ -944,6 +994,7 @@ def main() -> int:
                    "recurrent_steps": stats.recurrent_steps, "skipped_recurrent_steps": stats.skipped_recurrent_steps,
                    "graph_captures_in_timed_run": stats.recurrent_graph_captures},
         "steady_window": steady,
+        "gpu_activity_timed": activity.summary(),
     })
     if steady is None:
         result["steady_window_note"] = ("the reference's steady-state window (after 2 x max_num_seqs completions, "

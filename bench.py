@@ -348,10 +348,9 @@ def time_by_rows(positions_by_rows: dict[int, np.ndarray], pool_pages: int = 327
     return results
 
 
-def time_companion_kernels(rows: int = 1024, hidden: int = 2048, heads: int = 16, dim: int = 128) -> dict:
-    """The per-row kernels around decode attention at the microbench's batch size: the RoPE + KV
-    write of ``rows`` tokens (the prefill append), and the exit gate plus the hidden-bank gather and
-    scatter that compact and refill a launch's rows, each timed from a captured graph."""
+def time_rope_kv_write(tokens: int, heads: int = 16, dim: int = 128) -> tuple[float, int]:
+    """(ms, algorithmic bytes) of one prefill RoPE + KV write of ``tokens`` tokens, reading q, k and
+    v as column slices of one fused QKV output as the engine does, timed from a captured graph."""
 
     import torch
 
@@ -362,21 +361,40 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, heads: int = 16
     gen = torch.Generator(device=dev)
     gen.manual_seed(15)
     bs = 16
-    pages = 4 * rows
+    pages = 4 * tokens // bs + 64
     pool = torch.zeros((1, 2, pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
     view = ops.KVPoolView(pool, bs)
-    qkv = torch.randn((rows, 3, heads, dim), generator=gen, device=dev).bfloat16()
-    q_out = torch.empty((rows, heads, dim), dtype=torch.bfloat16, device=dev)
-    write_rows = torch.from_numpy(np.random.default_rng(16).choice(pages * bs, rows, replace=False)).to(dev)
-    positions = torch.randint(0, 4096, (rows,), generator=gen, device=dev, dtype=torch.int32)
+    qkv = torch.randn((tokens, 3, heads, dim), generator=gen, device=dev).bfloat16()
+    q_out = torch.empty((tokens, heads, dim), dtype=torch.bfloat16, device=dev)
+    write_rows = torch.from_numpy(np.random.default_rng(16).choice(pages * bs, tokens, replace=False)).to(dev)
+    positions = torch.randint(0, 4096, (tokens,), generator=gen, device=dev, dtype=torch.int32)
     cos, sin = rope_tables_torch(dim, 10000.0, 4096, torch.bfloat16, dev)
 
     def rope_write():
         ops.rope_kv_write_raw(qkv[:, 0], qkv[:, 1], qkv[:, 2], q_out, view, 0, write_rows, positions, cos, sin, 1,
                               None, None)
 
-    rope_ms = graph_time_ms(rope_write, 20)
-    rope_bytes = 6 * rows * heads * dim * 2 + rows * 12
+    ms = graph_time_ms(rope_write, 20)
+    del pool, qkv, q_out
+    # q, k, v read; rotated q, k and v written (16-byte rows per head); positions and pool rows.
+    return ms, 6 * tokens * heads * dim * 2 + tokens * 12
+
+
+def time_companion_kernels(rows: int = 1024, hidden: int = 2048, prefill_tokens: int | None = None) -> dict:
+    """The per-row kernels around decode attention at the microbench's batch size: the RoPE + KV
+    write of ``rows`` tokens (the prefill append; also at ``prefill_tokens``, the workload's first
+    prefill batch), and the exit gate plus the hidden-bank gather and scatter that compact and
+    refill a launch's rows, each timed from a captured graph."""
+
+    import torch
+
+    from continuous_depth_batching_amd import ops
+
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(17)
+    rope_ms, rope_bytes = time_rope_kv_write(rows)
+    rope_batch = time_rope_kv_write(prefill_tokens) if prefill_tokens else None
 
     bank = torch.randn((4 * rows + 64, hidden), generator=gen, device=dev).bfloat16()
     slots = torch.randperm(bank.shape[0], generator=gen, device=dev)[:rows].contiguous()
@@ -401,15 +419,18 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, heads: int = 16
     compact_ms = graph_time_ms(compact, 20)
     gate_bytes = rows * hidden * 2 + hidden * 2 + rows * (8 + 8 + 4 + 4 + 1 + 2)
     compact_bytes = 4 * rows * hidden * 2 + 2 * rows * 8
-    del pool, bank
+    del bank
     torch.cuda.empty_cache()
     row = lambda ms, b: {"us": round(ms * 1e3, 2), "bytes": b, "GBps": round(b / (ms * 1e-3) / 1e9, 1),
                          "frac": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-    return {"rows": rows, "rope_kv_write": row(rope_ms, rope_bytes), "exit_gate": row(gate_ms, gate_bytes),
-            "bank_gather_scatter": row(compact_ms, compact_bytes),
-            "note": f"{rows} tokens/rows, 16 heads x 128 (KV write) and hidden {hidden} (gate, bank rows), bf16; "
-                    "algorithmic bytes: q/k/v read + rotated q and k/v written; hidden read + gate state; "
-                    "bank rows read and written twice"}
+    out = {"rows": rows, "rope_kv_write": row(rope_ms, rope_bytes), "exit_gate": row(gate_ms, gate_bytes),
+           "bank_gather_scatter": row(compact_ms, compact_bytes),
+           "note": f"{rows} tokens/rows, 16 heads x 128 (KV write) and hidden {hidden} (gate, bank rows), bf16; "
+                   "algorithmic bytes: q/k/v read + rotated q and k/v written; hidden read + gate state; "
+                   "bank rows read and written twice"}
+    if rope_batch is not None:
+        out["rope_kv_write_first_prefill_batch"] = dict(row(*rope_batch), tokens=prefill_tokens)
+    return out
 
 
 def measured_traffic() -> int | None:
@@ -902,7 +923,7 @@ def main() -> int:
 
     companions = None
     if not args.no_microbench:
-        companions = time_companion_kernels()
+        companions = time_companion_kernels(prefill_tokens=int(sum(first_prefill_batch(prompts))))
     projections = time_decode_projections()
     prefill = time_prefill_attention(first_prefill_batch(prompts), iters=max(3, args.attention_iters // 4))
     prefill["shape"] = (f"{prefill['sequences']} fresh prompts, {prefill['tokens']} tokens (max {prefill['max_len']}), "

@@ -510,6 +510,29 @@ struct RopeWriteParams {
   int32_t num_heads, num_kv_heads, rope_style, max_positions;
 };
 
+// N consecutive floats at p, with the widest loads p's guaranteed byte alignment allows.
+template <int N, int kAlign>
+CDB_DEVICE void load_floats(const float* p, float (&out)[N]) {
+  if constexpr (kAlign % 16 == 0 && N % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < N / 4; ++j) {
+      const float4 v = reinterpret_cast<const float4*>(p)[j];
+      out[4 * j] = v.x; out[4 * j + 1] = v.y; out[4 * j + 2] = v.z; out[4 * j + 3] = v.w;
+    }
+  } else if constexpr (kAlign % 8 == 0 && N % 2 == 0) {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const float2 v = reinterpret_cast<const float2*>(p)[j];
+      out[2 * j] = v.x; out[2 * j + 1] = v.y;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = p[j];
+  }
+}
+
+constexpr int pow2_alignment(int bytes) { return bytes % 16 == 0 ? 16 : bytes % 8 == 0 ? 8 : 4; }
+
 template <typename T, int D>
 CDB_DEVICE void rotate_chunk(const RopeWriteParams& P, const T* base, const T* bias, int pos, int chunk, float* out) {
   constexpr int C = D / 16;
@@ -540,23 +563,34 @@ CDB_DEVICE void rotate_chunk(const RopeWriteParams& P, const T* base, const T* b
     for (int i = 0; i < C; ++i) out[i] = own[i];
     return;
   }
+  // A table row is D/2 floats (a multiple of 16 bytes for the supported head sizes);
+  // a chunk's angles are one run of consecutive entries, read as vectors.
   const int half = D / 2;
   const float* cr = P.rope_cos + (int64_t)pos * half;
   const float* sr = P.rope_sin + (int64_t)pos * half;
   if (split_half) {
+    // Elements d and d + D/2 share angle d mod D/2: the chunk's angles start at (chunk mod 8) * C.
+    float cs[C], sn[C];
+    const int f0 = (chunk & 7) * C;
+    load_floats<C, pow2_alignment(C * 4)>(cr + f0, cs);
+    load_floats<C, pow2_alignment(C * 4)>(sr + f0, sn);
+    const bool low = chunk < 8;
 #pragma unroll
     for (int i = 0; i < C; ++i) {
-      const int d = chunk * C + i;
-      const int f = d < half ? d : d - half;
-      const float rot = d < half ? -partner[i] : partner[i];
-      out[i] = Elem<T>::round(add_rn(Elem<T>::round(mul_rn(own[i], cr[f])), Elem<T>::round(mul_rn(rot, sr[f]))));
+      const float rot = low ? -partner[i] : partner[i];
+      out[i] = Elem<T>::round(add_rn(Elem<T>::round(mul_rn(own[i], cs[i])), Elem<T>::round(mul_rn(rot, sn[i]))));
     }
   } else {
+    // Interleaved pairs (2f, 2f + 1) share angle f: the chunk's angles start at chunk * C / 2.
+    float cs[C / 2], sn[C / 2];
+    const int f0 = chunk * (C / 2);
+    load_floats<C / 2, pow2_alignment(C * 2)>(cr + f0, cs);
+    load_floats<C / 2, pow2_alignment(C * 2)>(sr + f0, sn);
 #pragma unroll
     for (int i = 0; i < C; i += 2) {
-      const int f = (chunk * C + i) >> 1;
-      out[i] = Elem<T>::round(sub_rn(mul_rn(own[i], cr[f]), mul_rn(own[i + 1], sr[f])));
-      out[i + 1] = Elem<T>::round(add_rn(mul_rn(own[i + 1], cr[f]), mul_rn(own[i], sr[f])));
+      const float c = cs[i >> 1], sv = sn[i >> 1];
+      out[i] = Elem<T>::round(sub_rn(mul_rn(own[i], c), mul_rn(own[i + 1], sv)));
+      out[i + 1] = Elem<T>::round(add_rn(mul_rn(own[i + 1], c), mul_rn(own[i], sv)));
     }
   }
 }
@@ -591,6 +625,10 @@ __global__ void __launch_bounds__(kThreads) rope_kv_write_kernel(RopeWriteParams
     return;
   }
   const int kvh = hh - P.num_heads;
+  // The value row is read first: it depends on neither the pool row nor the key's
+  // rotation, and issued after the key store it would wait for that store.
+  Vec<T, C> vv;
+  vv.load(static_cast<const T*>(P.v) + t * P.kv_stride + (int64_t)kvh * D + chunk * C);
   const int64_t row = P.rows[t];
   if (row < 0 || row >= P.pool_rows || !rope_ok) return;
   float o[C];
@@ -601,8 +639,6 @@ __global__ void __launch_bounds__(kThreads) rope_kv_write_kernel(RopeWriteParams
 #pragma unroll
   for (int i = 0; i < C; ++i) kw.set(i, o[i]);
   kw.store(static_cast<T*>(P.k_pool) + off);
-  Vec<T, C> vv;
-  vv.load(static_cast<const T*>(P.v) + t * P.kv_stride + (int64_t)kvh * D + chunk * C);
   vv.store(static_cast<T*>(P.v_pool) + off);
 }
 

@@ -182,7 +182,58 @@ def test_exit_gate_synthetic_replay_and_latent_difference() -> None:
                               rule="direct", threshold=None, min_steps=1) for s, d in zip(steps, synth)]
     assert flags.cpu().numpy().astype(bool).tolist() == want
     want_sig = stage.latent_diff(h, prev, "bf16")
-    np.testing.assert_allclose(host(signal), want_sig, rtol=1e-2)
+    np.testing.assert_allclose(host(signal), want_sig, rtol=2 ** -7)  # within one bf16 step; pinned exactly below
+
+
+def test_latent_difference_signal_and_threshold_decisions_are_exact() -> None:
+    """Huginn's exit signal R(|R(h - prev)| / |h|) (huginn/exit_gates.py:33-40) and the direct
+    threshold rule (signal < threshold, cdb/exit_policy.py:165-169), pinned tighter than a
+    tolerance: the signal must equal the oracle's bf16 value exactly on nearly every row (the
+    float32 sums differ from the oracle's float64 ones only in order, which can move a value
+    across a bf16 rounding boundary) and within one bf16 step on all; and the decision must
+    flip exactly at each row's own signal: a threshold equal to the signal keeps the row, the
+    next float64 above it lets the row exit."""
+
+    from continuous_depth_batching_amd import ops
+
+    rng = np.random.default_rng(14)
+    rows, width = 64, 5280
+    h = rounder("bf16")(rng.standard_normal((rows, width)).astype(np.float32))
+    scales = np.logspace(-3, 0.5, rows).astype(np.float32)[:, None]   # signals over three decades
+    prev = rounder("bf16")(h + scales * rng.standard_normal((rows, width)).astype(np.float32))
+    state = ops.GateState.allocate(rows, torch.device("cuda"))
+    idx = dev(np.arange(rows, dtype=np.int64))
+    steps = dev(np.ones(rows, np.int32))
+    synth = dev(np.full(rows, -1, np.int32))
+    signal = torch.empty(rows, dtype=torch.bfloat16, device="cuda")
+    flags = torch.empty(rows, dtype=torch.uint8, device="cuda")
+    h_d, prev_d = dev(h, torch.bfloat16), dev(prev, torch.bfloat16)
+
+    def gate(threshold):
+        state.reset(idx)
+        ops.exit_gate_raw(h_d, prev_d, None, None, signal, state, idx, steps, synth, flags, rows,
+                          kind=ops.GATE_LATENT_DIFF, rule=ops.RULE_DIRECT_THRESHOLD, delayed=False,
+                          round_hazard=False, min_steps=1, max_steps=4, threshold=threshold)
+        torch.cuda.synchronize()
+        return host(signal).astype(np.float64), flags.cpu().numpy().astype(bool)
+
+    got, _ = gate(None)
+    want = stage.latent_diff(h, prev, "bf16").astype(np.float64)
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(want))) - 7)
+    assert np.all(np.abs(got - want) <= ulp), np.abs(got - want).max()
+    assert np.mean(got == want) >= 0.95, np.mean(got == want)
+    for b in range(0, rows, 7):
+        s = float(got[b])
+        _, at = gate(s)
+        _, above = gate(float(np.nextafter(s, np.inf)))
+        np.testing.assert_array_equal(at, got < s)
+        np.testing.assert_array_equal(above, got <= s)
+        assert not at[b] and above[b]
+        # The engine's decision path on the oracle's own signal agrees wherever the signals agree.
+        oracle = np.array([stage.decide_exit(step=1, max_steps=4, synthetic_depth=None, policy=stage.TokenPolicy(),
+                                             signal=float(w), rule="direct", threshold=s, min_steps=1) for w in want])
+        same = got == want
+        np.testing.assert_array_equal(at[same], oracle[same])
 
 
 def test_exit_kv_copy_bit_exact() -> None:

@@ -433,14 +433,22 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, prefill_tokens:
     return out
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per decode-attention call at this shape, from the FETCH_SIZE / WRITE_SIZE
-    counter runs (scaled by a plain copy of known size) recorded under profiles/."""
+TRAFFIC_RECORD = "profiles/decode_attention_c2_256rows_traffic.json"
 
-    path = REPO / "profiles" / "decode_attention_c2_256rows_traffic.json"
+
+def measured_traffic(algorithmic_bytes: int) -> int | None:
+    """HBM bytes per decode-attention call at this shape, from the FETCH_SIZE / WRITE_SIZE
+    counter runs (scaled by a plain copy of known size) recorded with the profiles. A counter
+    run cannot happen inside this process, so the record is used only when it was taken on
+    this very shape (its algorithmic bytes equal this run's); otherwise the figure is null."""
+
+    path = REPO / TRAFFIC_RECORD
     if not path.exists():
         return None
-    return int(json.loads(path.read_text())["traffic_bytes_per_call"])
+    record = json.loads(path.read_text())
+    if int(record.get("algorithmic_bytes_per_call", -1)) != int(algorithmic_bytes):
+        return None
+    return int(record["traffic_bytes_per_call"])
 
 
 def time_prefill_attention(prompt_lens, iters: int, past=None) -> dict:
@@ -908,7 +916,9 @@ def main() -> int:
                                       split_pages=0, iters=args.attention_iters)
     torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(attention["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
+                "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(attention["bytes"]),
+                "traffic_source": f"{TRAFFIC_RECORD}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this shape, "
+                                  "scaled by a 1 GiB copy",
                 "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_merge_kernel",
                 "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
                 "shape": f"{attention['rows']} rows x 16 heads x 128, mean context {attention['mean_context']:.0f}"}

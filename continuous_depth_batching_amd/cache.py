@@ -194,6 +194,20 @@ class PagedKVCache:
         return self.kv_slots_per_layer > 1
 
     # -- device table sync ----------------------------------------------------------------------------------
+    def take_table_updates(self, idx_out: np.ndarray, val_out: np.ndarray) -> int | None:
+        """Move the queued cell updates into a launch's own upload buffers: cell indices into
+        ``idx_out`` (int64) and values into ``val_out`` (int32); returns their count, or None
+        (and leaves them queued for flush_table_updates) when they do not fit."""
+
+        n = len(self._dirty)
+        if n > len(idx_out):
+            return None
+        if n:
+            idx_out[:n] = np.fromiter(self._dirty, dtype=np.int64, count=n)
+            val_out[:n] = self.host_table.reshape(-1)[idx_out[:n]]
+            self._dirty.clear()
+        return n
+
     def flush_table_updates(self) -> None:
         """Apply queued block-table updates on the current stream (one H2D pair + one scatter)."""
 

@@ -219,6 +219,22 @@ __global__ void __launch_bounds__(kThreads) silu_mul_kernel(const T* gu, T* out,
 }
 
 // ---------------------------------------------------------------------------
+// Block-table cell updates whose count lives in device memory: table[idx[i]] =
+// val[i] for i < min(*count, capacity), cells outside [0, cells) skipped. The
+// count is read on the device, so a captured graph applies whatever the launch's
+// metadata upload carried (cdb/cache.py:115-144 refreshes the same table rows).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads) table_update_kernel(int32_t* table, int64_t cells, const int64_t* idx,
+                                                               const int32_t* val, const int32_t* count,
+                                                               int32_t capacity) {
+  const int n = min(*count, capacity);
+  for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
+    const int64_t c = idx[i];
+    if (c >= 0 && c < cells) table[c] = val[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row copy with optional gather/scatter indices: dst[di[i]] = src[si[i]].
 // si[i] < 0 writes zeros; di[i] < 0 skips the row. Covers the hidden-bank
 // index_select/index_copy_ (cdb/model_runner.py:685-693, :559, :1101), the
@@ -744,6 +760,16 @@ int cdb_copy_rows(const void* src, const int64_t* src_index, int64_t src_rows, v
   hipLaunchKernelGGL(copy_rows_kernel, dim3(grid_for(rows * (row_bytes / unit))), dim3(kThreads), 0, stream,
                      static_cast<const uint8_t*>(src), src_index, static_cast<uint8_t*>(dst), dst_index, rows,
                      row_bytes, src_rows, dst_rows);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
+}
+
+int cdb_table_updates(int32_t* table, int64_t cells, const int64_t* idx, const int32_t* val, const int32_t* count,
+                      int32_t capacity, hipStream_t stream) {
+  if (capacity == 0) return CDB_OK;
+  if (!table || !idx || !val || !count) return CDB_ERR_NULL;
+  if (capacity < 0 || cells <= 0) return CDB_ERR_SHAPE;
+  hipLaunchKernelGGL(table_update_kernel, dim3(grid_for(capacity)), dim3(kThreads), 0, stream, table, cells, idx, val,
+                     count, capacity);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 

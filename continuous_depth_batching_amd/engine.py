@@ -518,16 +518,24 @@ class ContinuousDepthBatchingEngine:
         flags = [False] * len(coda_items)
         items: list[DepthWorkItem] = []
         rows: list[int] = []
+        block = self.cache.block_size
+        allocate = self._try_allocate_one_decode_token
         for idx, item in enumerate(coda_items):
             state = item.state
             if state.will_finish_on_pending_token():
                 continue
-            state.position_offset += 1
-            if not self._try_allocate_one_decode_token(state):
-                state.position_offset -= 1
+            pos = state.position_offset + 1
+            state.position_offset = pos
+            held = state.allocated_blocks
+            # Most successors' positions still fit the request's last block: no allocation then
+            # (the first test of _try_allocate_one_decode_token, without the call).
+            if not (held > 0 and held * block > pos) and not allocate(state):
+                state.position_offset = pos - 1
                 continue
             flags[idx] = True
-            items.append(self._build_decode_item(state, token_id=TMP_TOKEN_ID))
+            # _build_decode_item with a placeholder token, inline.
+            state.current_token_exit_depth = None
+            items.append(DepthWorkItem(state, TMP_TOKEN_ID, pos, 0, state.next_synthetic_exit_depth()))
             rows.append(idx)
         return items, rows, flags
 

@@ -136,13 +136,21 @@ class PrefillMetadata:
 @dataclass
 class _RecurrentBucket:
     rows: int
-    host_meta: torch.Tensor  # pinned int32 [7 * rows]: the int64 bank slots, then the int32 rows
+    # pinned int32: the int64 bank slots (2 * rows), the int32 rows (5 * rows), then the
+    # block-table updates the launch carries: [count, pad | int64 cells (U) | int32 values (U)]
+    host_meta: torch.Tensor
     dev_meta: torch.Tensor
     host_i64: torch.Tensor   # views of host_meta / dev_meta
     host_i32: torch.Tensor
     dev_i64: torch.Tensor
     dev_i32: torch.Tensor
     launch: RecurrentLaunch
+    host_upd_count: Any = None  # numpy views of the update region
+    host_upd_idx: Any = None
+    host_upd_val: Any = None
+    dev_upd_count: torch.Tensor | None = None
+    dev_upd_idx: torch.Tensor | None = None
+    dev_upd_val: torch.Tensor | None = None
     staged: Any | None = None
     graph: torch.cuda.CUDAGraph | None = None
     turn: int = 0
@@ -163,6 +171,9 @@ class ModelRunner:
     META_POSITIONS, META_TABLE_ROWS, META_LAYER_OFFSET, META_STEPS, META_SYNTHETIC = range(5)
     FLAG_TURNS = 4
     CODA_TURNS = 4
+    # Block-table cell updates a recurrent launch carries in its metadata upload and applies
+    # inside its graph; more queued updates than this take the separate flush first.
+    TABLE_UPDATE_SLOTS = 256
 
     def __init__(self, *, engine_config: ContinuousDepthBatchingConfig, cache: PagedKVCache,
                  model_adapter: CDBModelAdapter, exit_policy: ExitPolicy) -> None:
@@ -340,10 +351,14 @@ class ModelRunner:
             return b
         # One pinned buffer and one device buffer per bucket, so a launch uploads its
         # metadata with a single copy.
-        host_meta = self._pinned((7 * rows,), torch.int32)
-        dev_meta = torch.zeros((7 * rows,), dtype=torch.int32, device=self.device)
-        host_i64, host_i32 = host_meta[:2 * rows].view(torch.int64), host_meta[2 * rows:].view(5, rows)
-        dev_i64, dev_i32 = dev_meta[:2 * rows].view(torch.int64), dev_meta[2 * rows:].view(5, rows)
+        u = self.TABLE_UPDATE_SLOTS
+        base = 7 * rows + (7 * rows) % 2  # the int64 cells start 8-byte aligned
+        total = base + 2 + 3 * u
+        host_meta = self._pinned((total,), torch.int32)
+        host_meta.zero_()
+        dev_meta = torch.zeros((total,), dtype=torch.int32, device=self.device)
+        host_i64, host_i32 = host_meta[:2 * rows].view(torch.int64), host_meta[2 * rows:7 * rows].view(5, rows)
+        dev_i64, dev_i32 = dev_meta[:2 * rows].view(torch.int64), dev_meta[2 * rows:7 * rows].view(5, rows)
         dev_i64.fill_(-1)
         dev_i32[self.META_POSITIONS].fill_(-1)
         dev_i32[self.META_SYNTHETIC].fill_(-1)
@@ -369,6 +384,13 @@ class ModelRunner:
             split_pages=ops.decode_split_pages(rows), gate=gate)
         b = _RecurrentBucket(rows=rows, host_meta=host_meta, dev_meta=dev_meta, host_i64=host_i64,
                              host_i32=host_i32, dev_i64=dev_i64, dev_i32=dev_i32, launch=launch)
+        hn = host_meta.numpy()
+        b.host_upd_count = hn[base:base + 1]
+        b.host_upd_idx = hn[base + 2:base + 2 + 2 * u].view(np.int64)
+        b.host_upd_val = hn[base + 2 + 2 * u:total]
+        b.dev_upd_count = dev_meta[base:base + 1]
+        b.dev_upd_idx = dev_meta[base + 2:base + 2 + 2 * u].view(torch.int64)
+        b.dev_upd_val = dev_meta[base + 2 + 2 * u:total]
         b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]
         b.flag_events = [None] * self.FLAG_TURNS
         self._buckets[rows] = b
@@ -390,7 +412,13 @@ class ModelRunner:
         if b.flag_events[turn] is not None:
             b.flag_events[turn].synchronize()
         with self._on_stream():
-            self.cache.flush_table_updates()
+            # The block-table cells changed since the last launch ride in this launch's metadata
+            # upload and are applied by the graph's first kernel; a larger backlog is flushed first.
+            count = self.cache.take_table_updates(b.host_upd_idx, b.host_upd_val)
+            if count is None:
+                self.cache.flush_table_updates()
+                count = 0
+            b.host_upd_count[0] = count
             b.dev_meta.copy_(b.host_meta, non_blocking=True)
             if b.staged is None:
                 b.staged = torch.cuda.Event()
@@ -439,9 +467,9 @@ class ModelRunner:
             i32[self.META_LAYER_OFFSET] = self.layout.core_base
             i32[self.META_STEPS] = 0
             i32[self.META_SYNTHETIC] = -1
+            b.host_upd_count[0] = 0
             with self._on_stream():
-                b.dev_i64.copy_(b.host_i64, non_blocking=True)
-                b.dev_i32.copy_(b.host_i32, non_blocking=True)
+                b.dev_meta.copy_(b.host_meta, non_blocking=True)
                 if b.staged is None:
                     b.staged = torch.cuda.Event()
                 b.staged.record()
@@ -451,8 +479,13 @@ class ModelRunner:
         self.recurrent_graph_captures = 0
         return captured
 
+    def _apply_table_updates(self, b: _RecurrentBucket) -> None:
+        ops.table_updates_raw(self.cache.device_table, b.dev_upd_idx, b.dev_upd_val, b.dev_upd_count,
+                              self.TABLE_UPDATE_SLOTS)
+
     def _run_recurrent(self, b: _RecurrentBucket) -> None:
         if not self.use_graphs:
+            self._apply_table_updates(b)
             self.adapter.recurrent_step(b.launch)
             return
         if b.graph is not None:
@@ -461,9 +494,11 @@ class ModelRunner:
             return
         # First use of this bucket: run it eagerly (this launch's real work), then capture.
         with gc_paused():
+            self._apply_table_updates(b)
             self.adapter.recurrent_step(b.launch)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=self.stream, pool=self.graph_pool, capture_error_mode="thread_local"):
+                self._apply_table_updates(b)
                 self.adapter.recurrent_step(b.launch)
         b.graph = graph
         self.recurrent_graph_captures += 1

@@ -748,6 +748,22 @@ class CodaScratch:
             _lib.check(code, "cdb_coda_greedy")
 
 
+def table_updates_raw(table: torch.Tensor, idx: torch.Tensor, val: torch.Tensor, count: torch.Tensor,
+                      capacity: int) -> None:
+    """table.view(-1)[idx[i]] = val[i] for i < min(count[0], capacity), the count read on the device
+    (a captured graph applies whatever the launch uploaded)."""
+
+    if (table.dtype is not torch.int32 or idx.dtype is not torch.int64 or val.dtype is not torch.int32
+            or count.dtype is not torch.int32):
+        raise TypeError("table, val and count must be int32 and idx int64")
+    if idx.numel() < capacity or val.numel() < capacity or count.numel() < 1 or not table.is_contiguous():
+        raise ValueError(f"update buffers must hold {capacity} entries and the table be contiguous")
+    code = _lib.lib().cdb_table_updates(table.data_ptr(), table.numel(), idx.data_ptr(), val.data_ptr(),
+                                        count.data_ptr(), capacity, _stream())
+    if code:
+        _lib.check(code, "cdb_table_updates")
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """Greedy token per row (first index of the max), without op dispatch."""
 

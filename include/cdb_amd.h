@@ -142,6 +142,14 @@ int cdb_silu_mul(const void* gate_up, void* out, int64_t rows, int32_t width, in
 int cdb_copy_rows(const void* src, const int64_t* src_index, int64_t src_rows, void* dst, const int64_t* dst_index,
                   int64_t dst_rows, int64_t rows, int64_t row_bytes, hipStream_t stream);
 
+/* Block-table cell updates with the count in device memory: table[idx[i]] = val[i]
+ * for i < min(*count, capacity); cells outside [0, cells) are skipped. It lets a
+ * launch's metadata upload carry the table cells its rows' new blocks changed and
+ * a captured graph apply them, in place of a separate flush
+ * (the block-table refresh of cdb/cache.py:115-144, cache_manager.py:72-90). */
+int cdb_table_updates(int32_t* table, int64_t cells, const int64_t* idx, const int32_t* val, const int32_t* count,
+                      int32_t capacity, hipStream_t stream);
+
 /* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
  * (torch.argmax semantics incl. NaN; cdb/model_runner.py:1062,1105). */
 int cdb_argmax(const void* logits, int64_t* out, int64_t rows, int32_t vocab, int32_t dtype, hipStream_t stream);

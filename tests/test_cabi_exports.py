@@ -81,6 +81,20 @@ def test_decode_argument_errors_without_gpu() -> None:
     assert call(q_stride=100) == _lib.CDB_ERR_SHAPE
 
 
+def test_table_update_argument_errors_without_gpu() -> None:
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("runs only where no device exists: the stand-in addresses must never reach a kernel")
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.cdb_table_updates(fake, 64, fake, fake, fake, 0, None) == _lib.CDB_OK   # no slots: nothing to do
+    assert lib.cdb_table_updates(None, 64, fake, fake, fake, 8, None) == _lib.CDB_ERR_NULL
+    assert lib.cdb_table_updates(fake, 64, fake, fake, None, 8, None) == _lib.CDB_ERR_NULL
+    assert lib.cdb_table_updates(fake, 0, fake, fake, fake, 8, None) == _lib.CDB_ERR_SHAPE
+    assert lib.cdb_table_updates(fake, 64, fake, fake, fake, -1, None) == _lib.CDB_ERR_SHAPE
+
+
 def test_linear_argument_errors_without_gpu() -> None:
     import torch
 

@@ -236,6 +236,48 @@ def test_latent_difference_signal_and_threshold_decisions_are_exact() -> None:
         np.testing.assert_array_equal(at[same], oracle[same])
 
 
+def test_table_updates_apply_the_device_count_inside_a_graph() -> None:
+    """cdb_table_updates writes table[idx[i]] = val[i] for i < min(count, capacity), with the count
+    read on the device: a captured graph applies whatever the buffers hold at replay time.
+    Cells outside the table are skipped. Each replay is checked against the host's own copy,
+    with eager work and synchronizations between replays."""
+
+    from continuous_depth_batching_amd import ops
+
+    rng = np.random.default_rng(9)
+    rows, width, capacity = 40, 24, 64
+    table = torch.full((rows, width), -1, dtype=torch.int32, device="cuda")
+    want = np.full((rows, width), -1, np.int32)
+    idx = torch.zeros(capacity, dtype=torch.int64, device="cuda")
+    val = torch.zeros(capacity, dtype=torch.int32, device="cuda")
+    count = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        ops.table_updates_raw(table, idx, val, count, capacity)   # warm-up with count 0: no change
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            ops.table_updates_raw(table, idx, val, count, capacity)
+    stream.synchronize()
+    assert bool((table == -1).all())
+    for replay, n in enumerate((5, 64, 0, 70, 17)):
+        cells = rng.choice(rows * width, size=min(n, capacity), replace=False).astype(np.int64)
+        values = rng.integers(0, 1 << 20, size=cells.size).astype(np.int32)
+        if n >= 17:
+            cells[3] = rows * width + 5      # outside the table: skipped
+            cells[4] = -2
+        idx[:cells.size].copy_(torch.from_numpy(cells))
+        val[:values.size].copy_(torch.from_numpy(values))
+        count.fill_(n)
+        torch.cuda.synchronize()
+        print(f"[table updates] replay {replay}: count {n}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        for c, v in zip(cells[:min(n, capacity)], values[:min(n, capacity)]):
+            if 0 <= c < rows * width:
+                want.reshape(-1)[c] = v
+        np.testing.assert_array_equal(table.cpu().numpy(), want)
+
+
 def test_exit_kv_copy_bit_exact() -> None:
     from continuous_depth_batching_amd import ops
 

@@ -23,47 +23,12 @@ from collections import deque
 import numpy as np
 import torch
 
-from . import ops
+from . import _tick, ops
 from .kv_cache_policy import LoopedKvLayout
 
 
 class CacheFullError(RuntimeError):
     """The KV cache cannot place work and no preemption can relieve it."""
-
-
-class BlockManager:
-    def __init__(self, num_blocks: int, block_size: int) -> None:
-        self.num_blocks = num_blocks
-        self.block_size = block_size
-        self._free: deque[int] = deque(range(num_blocks))
-        self._allocated: set[int] = set()
-        self.peak_num_allocated_blocks = 0
-
-    @property
-    def num_free_blocks(self) -> int:
-        return len(self._free)
-
-    @property
-    def num_allocated_blocks(self) -> int:
-        return len(self._allocated)
-
-    def get_free_blocks(self, n: int) -> list[int] | None:
-        if len(self._free) < n:
-            return None
-        blocks = [self._free.popleft() for _ in range(n)]
-        self._allocated.update(blocks)
-        self.peak_num_allocated_blocks = max(self.peak_num_allocated_blocks, len(self._allocated))
-        return blocks
-
-    def free_blocks(self, blocks: list[int]) -> None:
-        for b in blocks:
-            if b not in self._allocated:
-                raise ValueError(f"Cannot free block {b}: block is not currently allocated")
-            self._allocated.remove(b)
-            self._free.append(b)
-
-    def reset_peak_usage(self) -> None:
-        self.peak_num_allocated_blocks = self.num_allocated_blocks
 
 
 class PagedKVCache:
@@ -90,7 +55,8 @@ class PagedKVCache:
         rows = (num_blocks + self.EXTRA_BLOCKS) * block_size
         self.pool = torch.zeros((self.num_layers, 2, rows, num_kv_heads, head_dim), dtype=dtype, device=device)
         self.view = ops.KVPoolView(self.pool, block_size)
-        self._block_manager = BlockManager(num_blocks, block_size)
+        # FIFO block ids, allocated map and peak (cb/cache_manager.py:72-90), in the tick core.
+        self._block_manager = _tick.BlockPool(num_blocks, block_size)
         self.block_table: dict[str, list[int]] = {}
         # Device block table: one row per active request.
         self.table_rows = max_requests

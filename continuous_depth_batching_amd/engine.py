@@ -515,29 +515,10 @@ class ContinuousDepthBatchingEngine:
         """Successors staged ahead of their token (cdb/continuous_api.py:1304-1327): every coda
         row whose request will not finish on the pending token and gets a KV slot."""
 
-        flags = [False] * len(coda_items)
-        items: list[DepthWorkItem] = []
-        rows: list[int] = []
-        block = self.cache.block_size
-        allocate = self._try_allocate_one_decode_token
-        for idx, item in enumerate(coda_items):
-            state = item.state
-            if state.will_finish_on_pending_token():
-                continue
-            pos = state.position_offset + 1
-            state.position_offset = pos
-            held = state.allocated_blocks
-            # Most successors' positions still fit the request's last block: no allocation then
-            # (the first test of _try_allocate_one_decode_token, without the call).
-            if not (held > 0 and held * block > pos) and not allocate(state):
-                state.position_offset = pos - 1
-                continue
-            flags[idx] = True
-            # _build_decode_item with a placeholder token, inline.
-            state.current_token_exit_depth = None
-            items.append(DepthWorkItem(state, TMP_TOKEN_ID, pos, 0, state.next_synthetic_exit_depth()))
-            rows.append(idx)
-        return items, rows, flags
+        # Per row: skip a request that finishes on its pending token, else advance its position
+        # and keep a KV slot for it (its last block, or a new one), then build its successor.
+        return _tick.select_eager(coda_items, self.cache.block_size, self._try_allocate_one_decode_token,
+                                  DepthWorkItem, TMP_TOKEN_ID)
 
     def _consume_ready_coda_results(self, *, block: bool) -> None:
         block = block or self.consume_all_results
@@ -591,9 +572,8 @@ class ContinuousDepthBatchingEngine:
         self.scheduler.block_new_requests = False
 
     def _drop_cancelled_items(self, items: list[DepthWorkItem]) -> list[DepthWorkItem]:
-        live = [i for i in items if i.state.status != RequestStatus.FINISHED]
-        if len(live) != len(items):
-            dead = [i for i in items if i.state.status == RequestStatus.FINISHED]
+        live, dead = _tick.split_live(items, RequestStatus.FINISHED)
+        if dead:
             self.runner.release_hidden_slots(dead)
             for i in dead:
                 self._pending_flags.pop(id(i), None)

@@ -19,6 +19,7 @@ from dataclasses import dataclass
 from itertools import islice
 from typing import Literal
 
+from . import _tick
 from .cache import PagedKVCache
 from .config import resolve_min_free_slots
 from .requests import DepthWorkItem, FutureRequestState, RequestState, RequestStatus, logger
@@ -63,6 +64,8 @@ class CDBScheduler:
         self.max_recurrent_steps = max_recurrent_steps
         self.min_coda_batch_size = min(min_coda_batch_size, self.max_num_seqs)
         self.slot_homogeneous = cache.requires_slot_homogeneous_recurrent_batches and not mixed_slot_launches
+        self._slot_of_step = tuple(cache.kv_slot_for_recurrent_step(s) for s in range(max_recurrent_steps)) \
+            if self.slot_homogeneous else None
         # Completions before the steady-state window opens (steady_state_summary); None leaves it off.
         self.steady_warmup_requests: int | None = None
         if kv_pressure_mode == "reserve":
@@ -79,8 +82,10 @@ class CDBScheduler:
         self.waiting_requests: dict[str, RequestState] = {}
         self.waiting_requests_order: deque[str] = deque()
         self.block_new_requests = False
-        self.ready_queue: deque[DepthWorkItem] = deque()
-        self.coda_queue: deque[DepthWorkItem] = deque()
+        # Deques of work items in the tick core; the per-tick head re-insertion and bucket
+        # pops run there (enqueue_front, pop_batch, pop_front).
+        self.ready_queue = _tick.ItemQueue()
+        self.coda_queue = _tick.ItemQueue()
         self.mixed_batches_scheduled = 0
         self.refill_events = 0
         self.max_depth_queue_size = 0
@@ -323,16 +328,16 @@ class CDBScheduler:
         """Return items to the queue head preserving their order (enqueue_depth(front=True)
         applied from the last item to the first, in one pass)."""
 
+        if not items:
+            return
         queue = self.ready_queue
-        limit = self.max_recurrent_steps
-        for item in reversed(items):
-            step = item.recurrent_step
-            if not 0 <= step < limit:
-                raise ValueError(f"recurrent_step must be in [0, {limit}), got {step}")
-            self._mark_request_in_flight(item.state.request_id)
-            if step == 0 and queue:
-                self.refill_events += 1
-            queue.appendleft(item)
+        self.refill_events += _tick.enqueue_front(queue, items, self.max_recurrent_steps, self.in_flight_request_ids)
+        # The in-flight set only grew inside, so its peak is its size now.
+        if len(self.in_flight_request_ids) > self.max_in_flight_requests:
+            self.max_in_flight_requests = len(self.in_flight_request_ids)
+        live = len(self.active_requests) + len(self.waiting_requests)
+        if live > self.max_live_requests:
+            self.max_live_requests = live
         if len(queue) > self.max_depth_queue_size:
             self.max_depth_queue_size = len(queue)
 
@@ -422,30 +427,17 @@ class CDBScheduler:
         state.tokens_to_process = tokens[:request_len]
 
     def _schedule_recurrent_batch(self) -> list[DepthWorkItem]:
+        # The head item, then queue order; under the slot-homogeneous rule only items writing the
+        # head's KV slot, the skipped ones kept in order ahead of the rest (tick core pop_batch).
         size = min(self.max_num_seqs, len(self.ready_queue))
         if size == 0:
             return []
-        first = self.ready_queue.popleft()
-        batch = [first]
-        if self.slot_homogeneous:
-            target = self.cache.kv_slot_for_recurrent_step(first.recurrent_step)
-            deferred: deque[DepthWorkItem] = deque()
-            while self.ready_queue and len(batch) < size:
-                item = self.ready_queue.popleft()
-                if self.cache.kv_slot_for_recurrent_step(item.recurrent_step) == target:
-                    batch.append(item)
-                else:
-                    deferred.append(item)
-            deferred.extend(self.ready_queue)
-            self.ready_queue = deferred
-        else:
-            while self.ready_queue and len(batch) < size:
-                batch.append(self.ready_queue.popleft())
+        batch = _tick.pop_batch(self.ready_queue, size, self._slot_of_step)
         self.mixed_batches_scheduled += 1
         return batch
 
     def _schedule_coda_batch(self) -> list[DepthWorkItem]:
-        return [self.coda_queue.popleft() for _ in range(min(self.max_num_seqs, len(self.coda_queue)))]
+        return _tick.pop_front(self.coda_queue, min(self.max_num_seqs, len(self.coda_queue)))
 
 
 __all__ = ["CDBScheduler", "ScheduledCDBBatch", "reserved_peak_blocks", "logger"]

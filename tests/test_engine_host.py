@@ -227,7 +227,7 @@ def test_block_allocation_is_fifo_and_blocks_return_after_generation() -> None:
     generate(engine, [[1, 2, 3], [4, 5, 6, 7, 8]], 4, exit_depths=[[0, 1, 2], [2, 2, 2]])
     assert engine.cache.get_num_free_blocks() == 16
     bm = engine.cache._block_manager
-    assert sorted(bm._free) == list(range(16))
+    assert sorted(bm.free_list()) == list(range(16))
     assert np.all(engine.cache.host_table == -1)
 
 

@@ -136,3 +136,195 @@ def test_fill_recurrent_errors() -> None:
     with pytest.raises(ValueError):
         _tick.fill_recurrent(items, np.empty(4, np.int64)[::-1], np.empty((5, 4), np.int32), row_of, 0, 1,
                              (0, 1, 2, 3))
+
+
+# -- block manager, queues and eager successors -------------------------------------------------------------
+def test_block_pool_is_fifo_with_a_peak_and_rejects_double_frees() -> None:
+    # cb/cache_manager.py:72-90: popleft on allocate, append on free.
+    pool = _tick.BlockPool(8, 16)
+    assert (pool.num_blocks, pool.block_size, pool.num_free_blocks) == (8, 16, 8)
+    assert pool.get_free_blocks(3) == [0, 1, 2]
+    assert pool.get_free_blocks(6) is None and pool.num_free_blocks == 5
+    assert pool.get_free_blocks(2) == [3, 4]
+    assert pool.num_allocated_blocks == 5 and pool.peak_num_allocated_blocks == 5
+    pool.free_blocks([1, 3])
+    assert pool.free_list() == [5, 6, 7, 1, 3]
+    assert pool.get_free_blocks(4) == [5, 6, 7, 1]
+    assert pool.peak_num_allocated_blocks == 7
+    pool.free_blocks([0, 2, 4, 5, 6, 7, 1])
+    assert pool.num_allocated_blocks == 0 and pool.peak_num_allocated_blocks == 7
+    pool.reset_peak_usage()
+    assert pool.peak_num_allocated_blocks == 0
+    with pytest.raises(ValueError, match="Cannot free block 2"):
+        pool.free_blocks([2])
+    with pytest.raises(ValueError, match="Cannot free block 99"):
+        pool.free_blocks([99])
+    with pytest.raises(ValueError):
+        pool.get_free_blocks(-1)
+    assert pool.get_free_blocks(0) == []
+
+
+def test_item_queue_behaves_as_a_deque() -> None:
+    q = _tick.ItemQueue()
+    assert len(q) == 0 and not q
+    a, b, c = object(), object(), object()
+    q.append(a)
+    q.appendleft(b)
+    q.extend([c])
+    assert list(q) == [b, a, c] and len(q) == 3 and q
+    assert q.popleft() is b
+    q.clear()
+    assert not q
+    with pytest.raises(IndexError):
+        q.popleft()
+
+
+def _enqueue_front_python(queue: list, items, limit: int, in_flight: set) -> int:
+    refills = 0
+    for item in reversed(items):
+        step = item.recurrent_step
+        if not 0 <= step < limit:
+            raise ValueError(f"recurrent_step must be in [0, {limit}), got {step}")
+        in_flight.add(item.state.request_id)
+        if step == 0 and queue:
+            refills += 1
+        queue.insert(0, item)
+    return refills
+
+
+def _pop_batch_python(queue: list, size: int, slot_of_step):
+    first = queue.pop(0)
+    batch = [first]
+    if slot_of_step is None:
+        while queue and len(batch) < size:
+            batch.append(queue.pop(0))
+        return batch
+    target = slot_of_step[first.recurrent_step]
+    deferred = []
+    while queue and len(batch) < size:
+        item = queue.pop(0)
+        (batch if slot_of_step[item.recurrent_step] == target else deferred).append(item)
+    queue[:0] = deferred
+    return batch
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_queue_operations_match_the_scheduler_python(seed: int) -> None:
+    # continuous_depth_batching/scheduler.py:142-180 (head re-insertion, refill counting) and
+    # :322-346 (slot-homogeneous bucket); random interleavings of pushes and pops.
+    rng = random.Random(seed)
+    max_steps = 4
+    slot_of_step = rng.choice([None, (0, 1, 2, 3), (0, 1, 1, 1), (0, 0, 0, 0)])
+    q, ref = _tick.ItemQueue(), []
+    in_flight, ref_in_flight = set(), set()
+    refills = ref_refills = 0
+    for _ in range(60):
+        op = rng.random()
+        if op < 0.5:
+            items = _items(rng, rng.randrange(0, 6), max_steps)
+            refills += _tick.enqueue_front(q, items, max_steps, in_flight)
+            ref_refills += _enqueue_front_python(ref, items, max_steps, ref_in_flight)
+        elif op < 0.6:
+            item = _items(rng, 1, max_steps)[0]
+            q.append(item)
+            ref.append(item)
+        elif len(ref):
+            size = rng.randrange(1, 8)
+            got = _tick.pop_batch(q, size, slot_of_step)
+            assert got == _pop_batch_python(ref, size, slot_of_step)
+        assert list(q) == ref and refills == ref_refills and in_flight == ref_in_flight
+    n = rng.randrange(0, len(ref) + 2)
+    assert _tick.pop_front(q, n) == ref[:n] and list(q) == ref[n:]
+    bad = _items(rng, 1, max_steps)[0]
+    bad.recurrent_step = max_steps
+    with pytest.raises(ValueError, match="recurrent_step must be in"):
+        _tick.enqueue_front(q, [bad], max_steps, in_flight)
+
+
+def test_split_live_keeps_order() -> None:
+    from continuous_depth_batching_amd.requests import RequestStatus
+
+    rng = random.Random(3)
+    items = _items(rng, 12, 4)
+    for i, item in enumerate(items):
+        if i % 3 == 1:
+            item.state._status = RequestStatus.FINISHED
+    live, dead = _tick.split_live(items, RequestStatus.FINISHED)
+    assert live == [x for x in items if x.state.status != RequestStatus.FINISHED]
+    assert dead == [x for x in items if x.state.status == RequestStatus.FINISHED]
+
+
+def _select_eager_python(coda_items, block, allocate, token):
+    """The engine's per-row eager successor selection (cdb/continuous_api.py:1304-1327)."""
+
+    flags = [False] * len(coda_items)
+    items, rows = [], []
+    for idx, item in enumerate(coda_items):
+        state = item.state
+        if state.will_finish_on_pending_token():
+            continue
+        state.position_offset += 1
+        current = state.current_len()
+        fits = state.allocated_blocks * block - current >= 1 and state.allocated_blocks > 0
+        if not fits and not allocate(state):
+            state.position_offset -= 1
+            continue
+        flags[idx] = True
+        state.reset_depth_state_for_next_token()
+        items.append(DepthWorkItem(state=state, token_id=token, token_position=state.position_offset,
+                                   recurrent_step=0, synthetic_exit_depth=state.next_synthetic_exit_depth()))
+        rows.append(idx)
+    return items, rows, flags
+
+
+def _coda_states(rng: random.Random, n: int):
+    from continuous_depth_batching_amd.requests import RequestStatus
+
+    out = []
+    for i in range(n):
+        limit = rng.randrange(2, 12)
+        state = RequestState(request_id=f"c{i}", initial_tokens=[1, 2, 3], max_new_tokens=limit,
+                             synthetic_exit_depths=[rng.randrange(4) for _ in range(limit)],
+                             replay_eos_finishes=rng.random() < 0.2)
+        state._status = RequestStatus.DECODING
+        state.generated_tokens = [7] * rng.randrange(0, limit)
+        state.tokens_in_flight = rng.randrange(0, 3)
+        state.position_offset = 3 + len(state.generated_tokens) + rng.randrange(0, 3)
+        state.allocated_blocks = rng.choice([0, -(-state.position_offset // 4), -(-(state.position_offset + 1) // 4)])
+        state._synthetic_exit_cursor = rng.randrange(0, 2)
+        state.current_token_exit_depth = rng.randrange(4)
+        out.append(DepthWorkItem(state=state, token_id=5, token_position=state.position_offset, recurrent_step=2))
+    return out
+
+
+def _eager_snapshot(items):
+    return [(i.state.position_offset, i.state.allocated_blocks, i.state.current_token_exit_depth,
+             i.state._synthetic_exit_cursor) for i in items]
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_select_eager_matches_the_per_row_python(seed: int) -> None:
+    block = 4
+    built = []
+    for impl in ("c", "python"):
+        rng = random.Random(seed)
+        coda = _coda_states(rng, 24)
+        budget = {"blocks": rng.randrange(0, 6)}
+
+        def allocate(state, budget=budget):
+            # Exact-ceil allocation from a small budget, as the engine's allocator takes blocks.
+            need = -(-(state.position_offset + 1) // block) - state.allocated_blocks
+            if need > budget["blocks"]:
+                return False
+            budget["blocks"] -= need
+            state.allocated_blocks += need
+            return True
+
+        if impl == "c":
+            items, rows, flags = _tick.select_eager(coda, block, allocate, DepthWorkItem, -1)
+        else:
+            items, rows, flags = _select_eager_python(coda, block, allocate, -1)
+        built.append(([(i.state.request_id, i.token_id, i.token_position, i.recurrent_step, i.synthetic_exit_depth)
+                       for i in items], rows, flags, _eager_snapshot(coda), budget["blocks"]))
+    assert built[0] == built[1]
+    assert any(built[0][2]) and not all(built[0][2])

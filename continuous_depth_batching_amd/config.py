@@ -81,7 +81,7 @@ class ContinuousDepthBatchingConfig:
     max_model_len: int = 16384
     use_async_batching: bool = True
     use_cuda_graph: bool = True
-    use_cuda_graph_prefill: bool = True
+    use_cuda_graph_prefill: bool = True  # accepted; prefill chunks always run eagerly
     max_recurrent_steps: int | None = None
     exit_threshold: float | None = None
     synthetic_exit_replay: bool = False

@@ -14,6 +14,12 @@
 //                   (continuous_depth_batching/scheduler.py:101-180, 322-346).
 //   split_live      drops work items of finished requests before a launch.
 //   select_eager    chooses a coda's eager successors (cdb/continuous_api.py:1304-1327).
+//   consume_coda    a coda batch's sampled tokens: token append and finish checks
+//                   (continuous_batching/requests.py:208-237) row by row.
+//   schedule_next   the scheduler's per-tick bucket choice (coda > prefill > recurrent >
+//                   undersized coda) with prompt admission and chunking
+//                   (continuous_depth_batching/scheduler.py:101-140, 205-296;
+//                   continuous_batching/scheduler_base.py:171-201, 416-545).
 //
 // The functions read and write the engine's own Python objects (DepthWorkItem,
 // RequestState), so request state stays in one place; they replace the
@@ -570,20 +576,12 @@ PyObject* enqueue_front(PyObject*, PyObject* args) {
 // the head item, then up to size - 1 more in queue order. With slot_of_step (a tuple,
 // the KV slot each step writes) only items writing the head item's slot are taken;
 // skipped items keep their order ahead of the untouched rest.
-PyObject* pop_batch(PyObject*, PyObject* args) {
-  PyObject *queue, *slot_of_step;
-  Py_ssize_t size;
-  if (!PyArg_ParseTuple(args, "OnO", &queue, &size, &slot_of_step)) return nullptr;
-  if (!is_queue(queue)) {
-    PyErr_SetString(PyExc_TypeError, "queue must be an ItemQueue");
-    return nullptr;
-  }
+PyObject* pop_batch_from(std::deque<PyObject*>* q, Py_ssize_t size, PyObject* slot_of_step) {
   const bool filter = slot_of_step != Py_None;
   if (filter && !PyTuple_Check(slot_of_step)) {
     PyErr_SetString(PyExc_TypeError, "slot_of_step must be a tuple or None");
     return nullptr;
   }
-  auto* q = reinterpret_cast<ItemQueue*>(queue)->items;
   PyObject* batch = PyList_New(0);
   if (!batch || size <= 0 || q->empty()) return batch;
   auto slot_of = [&](PyObject* item, long* slot) -> bool {
@@ -628,16 +626,19 @@ PyObject* pop_batch(PyObject*, PyObject* args) {
   return batch;
 }
 
-// pop_front(queue, n) -> the first min(n, len) items.
-PyObject* pop_front(PyObject*, PyObject* args) {
-  PyObject* queue;
-  Py_ssize_t n;
-  if (!PyArg_ParseTuple(args, "On", &queue, &n)) return nullptr;
+PyObject* pop_batch(PyObject*, PyObject* args) {
+  PyObject *queue, *slot_of_step;
+  Py_ssize_t size;
+  if (!PyArg_ParseTuple(args, "OnO", &queue, &size, &slot_of_step)) return nullptr;
   if (!is_queue(queue)) {
     PyErr_SetString(PyExc_TypeError, "queue must be an ItemQueue");
     return nullptr;
   }
-  auto* q = reinterpret_cast<ItemQueue*>(queue)->items;
+  return pop_batch_from(reinterpret_cast<ItemQueue*>(queue)->items, size, slot_of_step);
+}
+
+// pop_front(queue, n) -> the first min(n, len) items.
+PyObject* pop_front_from(std::deque<PyObject*>* q, Py_ssize_t n) {
   const Py_ssize_t k = std::max<Py_ssize_t>(0, std::min<Py_ssize_t>(n, (Py_ssize_t)q->size()));
   PyObject* out = PyList_New(k);
   if (!out) return nullptr;
@@ -646,6 +647,17 @@ PyObject* pop_front(PyObject*, PyObject* args) {
     q->pop_front();
   }
   return out;
+}
+
+PyObject* pop_front(PyObject*, PyObject* args) {
+  PyObject* queue;
+  Py_ssize_t n;
+  if (!PyArg_ParseTuple(args, "On", &queue, &n)) return nullptr;
+  if (!is_queue(queue)) {
+    PyErr_SetString(PyExc_TypeError, "queue must be an ItemQueue");
+    return nullptr;
+  }
+  return pop_front_from(reinterpret_cast<ItemQueue*>(queue)->items, n);
 }
 
 // split_live(items, finished) -> (live, dead): work items whose request status
@@ -756,6 +768,702 @@ PyObject* select_eager(PyObject*, PyObject* args) {
   return Py_BuildValue("(NNN)", items, rows, flags);
 }
 
+// ---------------------------------------------------------------------------
+// Scheduler tick: bucket selection in priority order and prompt admission
+// with chunking (continuous_depth_batching/scheduler.py:101-140, 205-296,
+// 322-349; continuous_batching/scheduler_base.py:171-201, 416-545), over the
+// CDBScheduler object's own attributes and the RequestState objects it holds.
+// ---------------------------------------------------------------------------
+
+// An owned reference, released at scope exit.
+class Ref {
+ public:
+  Ref() = default;
+  explicit Ref(PyObject* p) : p_(p) {}
+  Ref(const Ref&) = delete;
+  Ref& operator=(const Ref&) = delete;
+  ~Ref() { Py_XDECREF(p_); }
+  PyObject* get() const { return p_; }
+  PyObject* release() {
+    PyObject* p = p_;
+    p_ = nullptr;
+    return p;
+  }
+  void reset(PyObject* p) {
+    Py_XDECREF(p_);
+    p_ = p;
+  }
+  explicit operator bool() const { return p_ != nullptr; }
+
+ private:
+  PyObject* p_ = nullptr;
+};
+
+constexpr long kPending = 0, kPrefilling = 1, kDecoding = 2, kFinishedStatus = 3;  // RequestStatus values
+PyObject* g_status[4];     // the RequestStatus members PENDING, PREFILLING, DECODING, FINISHED
+PyObject* g_finished;      // g_status[FINISHED]
+PyObject* g_batch_type;    // ScheduledCDBBatch(kind, requests, depth_items, num_q_tokens, max_kv_read)
+PyObject* g_future_type;   // FutureRequestState(state, has_new_token, query_length)
+
+PyObject *s_active_requests, *s_waiting_requests, *s_waiting_order, *s_block_new_requests, *s_ready_queue,
+    *s_coda_queue, *s_in_flight_ids, *s_max_num_seqs, *s_min_coda_batch_size, *s_min_free_slots, *s_safety_margin,
+    *s_kv_pressure_mode, *s_max_model_len, *s_cache, *s_max_fast_path_len, *s_slot_of_step, *s_mixed_batches,
+    *s_max_in_flight, *s_max_live, *s_max_resident, *s_resident_samples, *s_resident_sum, *s_steady_warmup,
+    *s_advance_steady, *s_block_manager, *s_num_blocks, *s_block_size, *s_allocate_blocks, *s_get_num_free_blocks,
+    *s_is_cpu_offloaded, *s_remaining_prefill, *s_tokens_to_process, *s_initial_tokens, *s_max_new_tokens,
+    *s_status, *s_popleft, *s_reserve, *s_kind_coda, *s_kind_prefill, *s_kind_recurrent;
+
+// ceil(a / b) for b > 0 and any sign of a, as Python's -(-a // b).
+long ceil_div(long a, long b) {
+  long q = a / b;
+  if (a % b > 0) ++q;
+  return q;
+}
+
+bool raise_peak(PyObject* obj, PyObject* name, long value) {
+  long cur;
+  if (!get_long(obj, name, &cur)) return false;
+  return value <= cur || set_long(obj, name, value);
+}
+
+bool add_long(PyObject* obj, PyObject* name, long delta) {
+  long cur;
+  return get_long(obj, name, &cur) && set_long(obj, name, cur + delta);
+}
+
+// The scheduler's containers and constants, read once per call.
+struct Sched {
+  PyObject* self = nullptr;  // borrowed
+  Ref active, waiting, in_flight, cache, pool;
+  long max_num_seqs = 0, block_size = 0, num_blocks = 0;
+  double safety_margin = 0.0;
+
+  bool load(PyObject* s) {
+    self = s;
+    active.reset(PyObject_GetAttr(s, s_active_requests));
+    waiting.reset(PyObject_GetAttr(s, s_waiting_requests));
+    in_flight.reset(PyObject_GetAttr(s, s_in_flight_ids));
+    cache.reset(PyObject_GetAttr(s, s_cache));
+    if (!active || !waiting || !in_flight || !cache) return false;
+    if (!PyDict_Check(active.get()) || !PyDict_Check(waiting.get()) || !PySet_Check(in_flight.get())) {
+      PyErr_SetString(PyExc_TypeError, "scheduler: active/waiting requests must be dicts, in-flight ids a set");
+      return false;
+    }
+    if (!get_long(s, s_max_num_seqs, &max_num_seqs) || !get_long(cache.get(), s_block_size, &block_size) ||
+        !get_long(cache.get(), s_num_blocks, &num_blocks))
+      return false;
+    if (block_size <= 0) {
+      PyErr_SetString(PyExc_ValueError, "scheduler: cache block_size must be positive");
+      return false;
+    }
+    Ref margin(PyObject_GetAttr(s, s_safety_margin));
+    if (!margin) return false;
+    safety_margin = PyFloat_AsDouble(margin.get());
+    if (safety_margin == -1.0 && PyErr_Occurred()) return false;
+    // The block manager is read directly when it is the tick core's own BlockPool.
+    Ref manager(PyObject_GetAttr(cache.get(), s_block_manager));
+    if (manager && PyObject_TypeCheck(manager.get(), &BlockPoolType)) pool.reset(manager.release());
+    else PyErr_Clear();
+    return true;
+  }
+
+  bool free_blocks(long* out) {
+    if (pool) {
+      *out = (long)reinterpret_cast<BlockPool*>(pool.get())->free_list->size();
+      return true;
+    }
+    Ref r(PyObject_CallMethodNoArgs(cache.get(), s_get_num_free_blocks));
+    if (!r) return false;
+    *out = PyLong_AsLong(r.get());
+    return !(*out == -1 && PyErr_Occurred());
+  }
+
+  long residency_slots() const { return std::max<long>(0, max_num_seqs - (long)PyDict_GET_SIZE(active.get())); }
+};
+
+bool types_bound() {
+  if (g_finished && g_batch_type && g_future_type) return true;
+  PyErr_SetString(PyExc_RuntimeError, "the request and scheduler types are not bound to the tick core");
+  return false;
+}
+
+// bind_request_types(RequestStatus, FutureRequestState), called where they are defined.
+PyObject* bind_request_types(PyObject*, PyObject* args) {
+  PyObject *status, *future;
+  if (!PyArg_ParseTuple(args, "OO", &status, &future)) return nullptr;
+  PyObject* members[4] = {nullptr, nullptr, nullptr, nullptr};
+  for (long v = 0; v < 4; ++v) {
+    members[v] = PyObject_CallFunction(status, "l", v);
+    if (!members[v]) {
+      for (long j = 0; j < v; ++j) Py_DECREF(members[j]);
+      return nullptr;
+    }
+  }
+  for (long v = 0; v < 4; ++v) {
+    Py_XDECREF(g_status[v]);
+    g_status[v] = members[v];
+  }
+  g_finished = g_status[kFinishedStatus];
+  Py_INCREF(future);
+  Py_XDECREF(g_future_type);
+  g_future_type = future;
+  Py_RETURN_NONE;
+}
+
+// bind_batch_type(ScheduledCDBBatch), called where it is defined.
+PyObject* bind_batch_type(PyObject*, PyObject* batch) {
+  Py_INCREF(batch);
+  Py_XDECREF(g_batch_type);
+  g_batch_type = batch;
+  Py_RETURN_NONE;
+}
+
+bool load_sched(PyObject* self, Sched& S) { return types_bound() && S.load(self); }
+
+// record_resident_sample (scheduler_base.py:315-398): the resident-set peak and mean, and
+// the steady-state window when one is being tracked.
+bool record_resident(Sched& S) {
+  const long resident = (long)PyDict_GET_SIZE(S.active.get());
+  if (!raise_peak(S.self, s_max_resident, resident) || !add_long(S.self, s_resident_samples, 1) ||
+      !add_long(S.self, s_resident_sum, resident))
+    return false;
+  Ref warmup(PyObject_GetAttr(S.self, s_steady_warmup));
+  if (!warmup) return false;
+  if (warmup.get() == Py_None) return true;
+  Ref arg(PyLong_FromLong(resident));
+  Ref r(arg ? PyObject_CallMethodOneArg(S.self, s_advance_steady, arg.get()) : nullptr);
+  return bool(r);
+}
+
+// Whether any active request is decoding (-1 on error).
+int has_decode_work(Sched& S) {
+  Py_ssize_t pos = 0;
+  PyObject *key, *state;
+  while (PyDict_Next(S.active.get(), &pos, &key, &state)) {
+    long st;
+    if (!get_long(state, s_status_field, &st)) return -1;
+    if (st == kDecoding) return 1;
+  }
+  return 0;
+}
+
+// Prefill runs when nothing decodes or the free blocks exceed the safety margin
+// (scheduler_base.py:171-201). Both tests are pure, so the cheap one goes first.
+int admit_prefill(Sched& S) {
+  long free;
+  if (!S.free_blocks(&free)) return -1;
+  if ((double)free > S.safety_margin * (double)S.num_blocks) return 1;
+  const int decoding = has_decode_work(S);
+  return decoding < 0 ? -1 : !decoding;
+}
+
+// Worst-case blocks of a request under reserve admission (utils.py:107-129).
+bool reserved_peak(PyObject* state, long max_model_len, long block_size, long* out) {
+  Ref initial(PyObject_GetAttr(state, s_initial_tokens));
+  Ref budget(initial ? PyObject_GetAttr(state, s_max_new_tokens) : nullptr);
+  if (!budget) return false;
+  const Py_ssize_t prompt = PyObject_Length(initial.get());
+  if (prompt < 0) return false;
+  long total = max_model_len;
+  if (budget.get() != Py_None) {
+    const long mnt = PyLong_AsLong(budget.get());
+    if (mnt == -1 && PyErr_Occurred()) return false;
+    total = std::min<long>((long)prompt + mnt, max_model_len);
+  }
+  *out = ceil_div(total, block_size);
+  return true;
+}
+
+// The prefill bucket (scheduler_base.py:416-460): active requests mid-prefill with no token
+// in flight, then -- unless new requests are blocked -- waiting prompts that are not swapped
+// out, in arrival order, up to the open residency slots; under reserve admission only those
+// whose worst-case blocks still fit beside the active requests' commitments.
+PyObject* prefill_bucket_of(Sched& S) {
+  Ref out(PyList_New(0));
+  if (!out) return nullptr;
+  Py_ssize_t pos = 0;
+  PyObject *key, *state;
+  while (PyDict_Next(S.active.get(), &pos, &key, &state)) {
+    long st;
+    if (!get_long(state, s_status_field, &st)) return nullptr;
+    if (st != kPrefilling) continue;
+    Ref rid(PyObject_GetAttr(state, s_request_id));
+    if (!rid) return nullptr;
+    const int busy = PySet_Contains(S.in_flight.get(), rid.get());
+    if (busy < 0 || (!busy && PyList_Append(out.get(), state))) return nullptr;
+  }
+  const int blocked = get_truth(S.self, s_block_new_requests);
+  if (blocked < 0) return nullptr;
+  if (blocked) return out.release();
+  const long limit = S.residency_slots();
+  Ref admissible(PyList_New(0));
+  if (!admissible) return nullptr;
+  if (limit > 0) {
+    Ref order(PyObject_GetAttr(S.self, s_waiting_order));
+    Ref it(order ? PyObject_GetIter(order.get()) : nullptr);
+    if (!it) return nullptr;
+    while (PyList_GET_SIZE(admissible.get()) < limit) {
+      Ref rid(PyIter_Next(it.get()));
+      if (!rid) {
+        if (PyErr_Occurred()) return nullptr;
+        break;
+      }
+      PyObject* waiting = PyDict_GetItemWithError(S.waiting.get(), rid.get());  // borrowed
+      if (!waiting) {
+        if (!PyErr_Occurred()) PyErr_SetObject(PyExc_KeyError, rid.get());
+        return nullptr;
+      }
+      const int offloaded = get_truth(waiting, s_is_cpu_offloaded);
+      if (offloaded < 0 || (!offloaded && PyList_Append(admissible.get(), waiting))) return nullptr;
+    }
+  }
+  Ref mode(PyObject_GetAttr(S.self, s_kv_pressure_mode));
+  if (!mode) return nullptr;
+  const int reserve = PyObject_RichCompareBool(mode.get(), s_reserve, Py_EQ);
+  if (reserve < 0) return nullptr;
+  if (reserve) {
+    long max_len, committed = 0, need;
+    if (!get_long(S.self, s_max_model_len, &max_len)) return nullptr;
+    pos = 0;
+    while (PyDict_Next(S.active.get(), &pos, &key, &state)) {
+      if (!reserved_peak(state, max_len, S.block_size, &need)) return nullptr;
+      committed += need;
+    }
+    Py_ssize_t fit = 0;
+    for (; fit < PyList_GET_SIZE(admissible.get()); ++fit) {
+      if (!reserved_peak(PyList_GET_ITEM(admissible.get(), fit), max_len, S.block_size, &need)) return nullptr;
+      if (committed + need > S.num_blocks) break;
+      committed += need;
+    }
+    if (PyList_SetSlice(admissible.get(), fit, PyList_GET_SIZE(admissible.get()), nullptr)) return nullptr;
+  }
+  const Py_ssize_t n = PyList_GET_SIZE(out.get());
+  if (PyList_SetSlice(out.get(), n, n, admissible.get())) return nullptr;
+  return out.release();
+}
+
+// A bucket is admitted when it holds a request mid-prefill or enough residency slots are open.
+int admit_bucket(Sched& S, PyObject* bucket) {
+  const Py_ssize_t n = PyList_GET_SIZE(bucket);
+  if (n == 0) return 0;
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    long st;
+    if (!get_long(PyList_GET_ITEM(bucket, i), s_status_field, &st)) return -1;
+    if (st == kPrefilling) return 1;
+  }
+  long min_free;
+  if (!get_long(S.self, s_min_free_slots, &min_free)) return -1;
+  return S.residency_slots() >= min_free;
+}
+
+bool mark_in_flight(Sched& S, PyObject* rid) {
+  if (PySet_Add(S.in_flight.get(), rid)) return false;
+  const long live = (long)(PyDict_GET_SIZE(S.active.get()) + PyDict_GET_SIZE(S.waiting.get()));
+  return raise_peak(S.self, s_max_in_flight, (long)PySet_GET_SIZE(S.in_flight.get())) &&
+         raise_peak(S.self, s_max_live, live);
+}
+
+// Blocks for `n` more tokens past the request's length, taken from the cache when the held
+// ones fall short (scheduler_base.py:520-531). 1 held or allocated, 0 not enough free, -1 error.
+int allocate_for(Sched& S, PyObject* state, long n) {
+  long current, held;
+  if (!get_long(state, s_position_offset, &current) || !get_long(state, s_allocated_blocks, &held)) return -1;
+  if (held * S.block_size - current >= n) return 1;
+  const long needed = ceil_div(current + n, S.block_size) - held;
+  Ref rid(PyObject_GetAttr(state, s_request_id));
+  Ref count(rid ? PyLong_FromLong(needed) : nullptr);
+  Ref offset(count ? PyLong_FromLong(held) : nullptr);
+  Ref got(offset ? PyObject_CallMethodObjArgs(S.cache.get(), s_allocate_blocks, count.get(), rid.get(),
+                                              offset.get(), nullptr)
+                 : nullptr);
+  if (!got) return -1;
+  if (got.get() == Py_None) return 0;
+  const long g = PyLong_AsLong(got.get());
+  if (g == -1 && PyErr_Occurred()) return -1;
+  return set_long(state, s_allocated_blocks, held + g) ? 1 : -1;
+}
+
+// Takes the first request_len prompt tokens of a candidate (scheduler_base.py:462-492): a
+// pending request becomes active, and one whose prompt is used up moves to decoding with
+// the rest of its prompt as the tokens to process.
+bool take_prompt_chunk(Sched& S, PyObject* state, PyObject* tokens, long request_len, PyObject* taken) {
+  const Py_ssize_t ntok = PyObject_Length(tokens);
+  long st;
+  Ref rid(PyObject_GetAttr(state, s_request_id));
+  if (ntok < 0 || !rid || !get_long(state, s_status_field, &st)) return false;
+  if (ntok <= request_len) {
+    if (st == kPending && (PyDict_SetItem(S.active.get(), rid.get(), state) || PySet_Add(taken, rid.get())))
+      return false;
+    if (st <= kPrefilling) {
+      Ref rest(PyObject_GetAttr(state, s_remaining_prefill));
+      Ref none_left(rest ? PyList_New(0) : nullptr);
+      if (!none_left || PyObject_SetAttr(state, s_tokens_to_process, rest.get()) ||
+          PyObject_SetAttr(state, s_remaining_prefill, none_left.get()) ||
+          PyObject_SetAttr(state, s_status, g_status[kDecoding]))
+        return false;
+    }
+    return true;
+  }
+  if (st == kPending && (PyDict_SetItem(S.active.get(), rid.get(), state) ||
+                         PyObject_SetAttr(state, s_status, g_status[kPrefilling]) || PySet_Add(taken, rid.get())))
+    return false;
+  Ref tail(PySequence_GetSlice(tokens, request_len, PY_SSIZE_T_MAX));
+  Ref head(tail ? PySequence_GetSlice(tokens, 0, request_len) : nullptr);
+  return head && PyObject_SetAttr(state, s_remaining_prefill, tail.get()) == 0 &&
+         PyObject_SetAttr(state, s_tokens_to_process, head.get()) == 0;
+}
+
+// One prefill batch from the candidates in order, within the token and KV-read budgets
+// (scheduler_base.py:494-545): a request whose whole remaining prompt does not fit the
+// token budget is chunked, decode-only batches of single tokens ignore the read budget,
+// and allocation failure skips a request (or ends the batch when the cache is empty and
+// the request still waits). `taken` collects the ids leaving the waiting queue.
+PyObject* fill_prefill(Sched& S, PyObject* candidates, long token_budget, long cache_budget, PyObject* taken,
+                       long* num_q_tokens, long* max_kv_read) {
+  Ref scheduled(PyList_New(0));
+  long max_fast;
+  if (!scheduled || !get_long(S.self, s_max_fast_path_len, &max_fast)) return nullptr;
+  const double margin = S.safety_margin * (double)S.num_blocks;
+  bool fast = true;
+  long tokens_left = token_budget, reads_left = cache_budget;
+  for (Py_ssize_t i = 0; i < PyList_GET_SIZE(candidates); ++i) {
+    PyObject* state = PyList_GET_ITEM(candidates, i);
+    long free;
+    if (!S.free_blocks(&free)) return nullptr;
+    if ((double)free < margin && PyList_GET_SIZE(scheduled.get()) > 0) break;
+    Ref tokens(PyObject_GetAttr(state, s_remaining_prefill));
+    if (!tokens) return nullptr;
+    const Py_ssize_t ntok = PyObject_Length(tokens.get());
+    if (ntok < 0) return nullptr;
+    long request_len = std::min<long>((long)ntok, tokens_left);
+    if (request_len == 0) continue;
+    long position;
+    if (!get_long(state, s_position_offset, &position)) return nullptr;
+    const bool eligible = request_len == 1 && position < max_fast;
+    const long read_needed = position;
+    if (!(fast && eligible) && reads_left < read_needed) continue;
+    const int got = allocate_for(S, state, request_len);
+    if (got < 0) return nullptr;
+    Ref rid(PyObject_GetAttr(state, s_request_id));
+    if (!rid) return nullptr;
+    if (!got) {
+      if (free == 0) {
+        const int waiting = PyDict_Contains(S.waiting.get(), rid.get());
+        if (waiting < 0) return nullptr;
+        if (waiting) break;
+      }
+      continue;
+    }
+    if (!take_prompt_chunk(S, state, tokens.get(), request_len, taken) || !mark_in_flight(S, rid.get()))
+      return nullptr;
+    Ref chunk(PyObject_GetAttr(state, s_tokens_to_process));
+    const Py_ssize_t taken_len = chunk ? PyObject_Length(chunk.get()) : -1;
+    if (taken_len < 0 || !get_long(state, s_position_offset, &position)) return nullptr;
+    request_len = (long)taken_len;
+    fast = fast && request_len == 1 && position < max_fast;
+    tokens_left -= request_len;
+    reads_left -= read_needed;
+    Ref rest(PyObject_GetAttr(state, s_remaining_prefill));
+    const int more = rest ? PyObject_IsTrue(rest.get()) : -1;
+    if (more < 0) return nullptr;
+    Ref future(PyObject_CallFunction(g_future_type, "OOl", state, more ? Py_False : Py_True, request_len));
+    if (!future || PyList_Append(scheduled.get(), future.get())) return nullptr;
+    PyObject* was_waiting = PyDict_GetItemWithError(S.waiting.get(), rid.get());  // borrowed
+    if (was_waiting) {
+      if (PyDict_DelItem(S.waiting.get(), rid.get()) || PySet_Add(taken, rid.get())) return nullptr;
+    } else if (PyErr_Occurred()) {
+      return nullptr;
+    }
+    if (tokens_left == 0 || (reads_left <= 0 && !fast)) break;
+  }
+  *num_q_tokens = token_budget - tokens_left;
+  *max_kv_read = cache_budget - reads_left;
+  return scheduled.release();
+}
+
+// Drops the taken ids from the waiting order: popped off the front while they lead it,
+// else by rebuilding the order without them (scheduler_base.py:503-511).
+bool drop_from_waiting_order(Sched& S, PyObject* taken) {
+  if (PySet_GET_SIZE(taken) == 0) return true;
+  Ref remaining(PySet_New(taken));
+  Ref order(remaining ? PyObject_GetAttr(S.self, s_waiting_order) : nullptr);
+  if (!order) return false;
+  while (PySet_GET_SIZE(remaining.get()) > 0) {
+    const Py_ssize_t n = PyObject_Length(order.get());
+    if (n < 0) return false;
+    if (n == 0) break;
+    Ref head(PySequence_GetItem(order.get(), 0));
+    const int lead = head ? PySet_Contains(remaining.get(), head.get()) : -1;
+    if (lead < 0) return false;
+    if (!lead) break;
+    Ref popped(PyObject_CallMethodNoArgs(order.get(), s_popleft));
+    if (!popped || PySet_Discard(remaining.get(), popped.get()) < 0) return false;
+  }
+  if (PySet_GET_SIZE(remaining.get()) == 0) return true;
+  Ref kept(PyList_New(0));
+  Ref it(kept ? PyObject_GetIter(order.get()) : nullptr);
+  if (!it) return false;
+  for (;;) {
+    Ref rid(PyIter_Next(it.get()));
+    if (!rid) {
+      if (PyErr_Occurred()) return false;
+      break;
+    }
+    const int gone = PySet_Contains(remaining.get(), rid.get());
+    if (gone < 0 || (!gone && PyList_Append(kept.get(), rid.get()))) return false;
+  }
+  Ref fresh(PyObject_CallOneArg(reinterpret_cast<PyObject*>(Py_TYPE(order.get())), kept.get()));
+  return fresh && PyObject_SetAttr(S.self, s_waiting_order, fresh.get()) == 0;
+}
+
+PyObject* make_batch(PyObject* kind, PyObject* requests, PyObject* items, long num_q_tokens, long max_kv_read) {
+  return PyObject_CallFunction(g_batch_type, "OOOll", kind, requests, items, num_q_tokens, max_kv_read);
+}
+
+// The prefill batch of this tick, or None (scheduler.py:205-234).
+PyObject* schedule_prefill_of(Sched& S, long token_budget, long cache_budget) {
+  Ref bucket(prefill_bucket_of(S));
+  if (!bucket) return nullptr;
+  const int admitted = admit_bucket(S, bucket.get());
+  if (admitted < 0) return nullptr;
+  if (!admitted) Py_RETURN_NONE;
+  Ref taken(PySet_New(nullptr));
+  if (!taken) return nullptr;
+  long num_q_tokens = 0, max_kv_read = 0;
+  Ref scheduled(fill_prefill(S, bucket.get(), token_budget, cache_budget, taken.get(), &num_q_tokens, &max_kv_read));
+  if (!scheduled || !drop_from_waiting_order(S, taken.get())) return nullptr;
+  if (PyList_GET_SIZE(scheduled.get()) == 0) Py_RETURN_NONE;
+  return make_batch(s_kind_prefill, scheduled.get(), Py_None, num_q_tokens, max_kv_read);
+}
+
+std::deque<PyObject*>* queue_attr(PyObject* self, PyObject* name, Ref& holder) {
+  holder.reset(PyObject_GetAttr(self, name));
+  if (!holder) return nullptr;
+  if (!is_queue(holder.get())) {
+    PyErr_SetString(PyExc_TypeError, "scheduler queues must be ItemQueues");
+    return nullptr;
+  }
+  return reinterpret_cast<ItemQueue*>(holder.get())->items;
+}
+
+// schedule_next(scheduler, token_budget, cache_budget, allow_coda) -> ScheduledCDBBatch | None
+// One homogeneous bucket per tick (scheduler.py:101-140): a coda batch once
+// min_coda_batch_size tokens wait, else a prefill batch when admission allows, else the
+// next recurrent batch (head item first, slot-homogeneous when required), else an
+// undersized coda flush.
+PyObject* schedule_next(PyObject*, PyObject* args) {
+  PyObject* self;
+  long token_budget, cache_budget;
+  int allow_coda;
+  if (!PyArg_ParseTuple(args, "Ollp", &self, &token_budget, &cache_budget, &allow_coda)) return nullptr;
+  Sched S;
+  if (!load_sched(self, S) || !record_resident(S)) return nullptr;
+  Ref coda_holder, ready_holder;
+  auto* coda = queue_attr(self, s_coda_queue, coda_holder);
+  auto* ready = coda ? queue_attr(self, s_ready_queue, ready_holder) : nullptr;
+  long min_coda;
+  if (!ready || !get_long(self, s_min_coda_batch_size, &min_coda)) return nullptr;
+  auto coda_batch = [&]() -> PyObject* {
+    const Py_ssize_t n = std::min<Py_ssize_t>(S.max_num_seqs, (Py_ssize_t)coda->size());
+    return pop_front_from(coda, n);
+  };
+  if (allow_coda && (long)coda->size() >= min_coda) {
+    Ref batch(coda_batch());
+    if (!batch) return nullptr;
+    if (PyList_GET_SIZE(batch.get()) > 0) return make_batch(s_kind_coda, Py_None, batch.get(), 0, 0);
+  }
+  const int admit = admit_prefill(S);
+  if (admit < 0) return nullptr;
+  if (admit) {
+    Ref prefill(schedule_prefill_of(S, token_budget, cache_budget));
+    if (!prefill) return nullptr;
+    if (prefill.get() != Py_None) return prefill.release();
+  }
+  const Py_ssize_t size = std::min<Py_ssize_t>(S.max_num_seqs, (Py_ssize_t)ready->size());
+  if (size > 0) {
+    Ref slot_of_step(PyObject_GetAttr(self, s_slot_of_step));
+    Ref batch(slot_of_step ? pop_batch_from(ready, size, slot_of_step.get()) : nullptr);
+    if (!batch || !add_long(self, s_mixed_batches, 1)) return nullptr;
+    if (PyList_GET_SIZE(batch.get()) > 0) return make_batch(s_kind_recurrent, Py_None, batch.get(), 0, 0);
+  }
+  if (allow_coda) {
+    Ref batch(coda_batch());
+    if (!batch) return nullptr;
+    if (PyList_GET_SIZE(batch.get()) > 0) return make_batch(s_kind_coda, Py_None, batch.get(), 0, 0);
+  }
+  Py_RETURN_NONE;
+}
+
+PyObject* schedule_prefill(PyObject*, PyObject* args) {
+  PyObject* self;
+  long token_budget, cache_budget;
+  if (!PyArg_ParseTuple(args, "Oll", &self, &token_budget, &cache_budget)) return nullptr;
+  Sched S;
+  if (!load_sched(self, S)) return nullptr;
+  return schedule_prefill_of(S, token_budget, cache_budget);
+}
+
+PyObject* prefill_bucket(PyObject*, PyObject* self) {
+  Sched S;
+  if (!load_sched(self, S)) return nullptr;
+  return prefill_bucket_of(S);
+}
+
+PyObject* record_resident_sample(PyObject*, PyObject* self) {
+  Sched S;
+  if (!load_sched(self, S) || !record_resident(S)) return nullptr;
+  Py_RETURN_NONE;
+}
+
+PyObject* prefill_admitted(PyObject*, PyObject* self) {
+  Sched S;
+  if (!load_sched(self, S)) return nullptr;
+  const int admit = admit_prefill(S);
+  if (admit < 0) return nullptr;
+  return PyBool_FromLong(admit);
+}
+
+PyObject* allocate_if_needed(PyObject*, PyObject* args) {
+  PyObject *self, *state;
+  long n;
+  if (!PyArg_ParseTuple(args, "OOl", &self, &state, &n)) return nullptr;
+  Sched S;
+  if (!load_sched(self, S)) return nullptr;
+  const int got = allocate_for(S, state, n);
+  if (got < 0) return nullptr;
+  return PyBool_FromLong(got);
+}
+
+// ---------------------------------------------------------------------------
+// Sampled-token bookkeeping (continuous_batching/requests.py:208-237) and the
+// coda-result walk of the engine (cdb/continuous_api.py:1378-1420).
+// ---------------------------------------------------------------------------
+PyObject* g_perf_counter;  // time.perf_counter
+PyObject *s_eos_ids, *s_stop_sequences, *s_first_token_time, *s_name;
+
+// Whether the generated tokens end with one of the request's stop sequences.
+int matches_stop_sequence(PyObject* state, PyObject* generated) {
+  Ref stops(PyObject_GetAttr(state, s_stop_sequences));
+  Ref it(stops ? PyObject_GetIter(stops.get()) : nullptr);
+  if (!it) return -1;
+  const Py_ssize_t n = PyList_GET_SIZE(generated);
+  for (;;) {
+    Ref seq(PyIter_Next(it.get()));
+    if (!seq) return PyErr_Occurred() ? -1 : 0;
+    const int nonempty = PyObject_IsTrue(seq.get());
+    if (nonempty < 0) return -1;
+    if (!nonempty) continue;
+    const Py_ssize_t len = PyObject_Length(seq.get());
+    if (len < 0) return -1;
+    if (n < len) continue;
+    Ref tail(PyList_GetSlice(generated, n - len, n));
+    const int eq = tail ? PyObject_RichCompareBool(tail.get(), seq.get(), Py_EQ) : -1;
+    if (eq) return eq;
+  }
+}
+
+// Record a sampled token on a decoding request: one fewer token in flight; the token is
+// kept (and becomes the next token to process) when it is EOS or within the length limit;
+// the request finishes on EOS, at the limit or on a stop sequence. 1 finished, 0 not, -1 error.
+int update_completion_of(PyObject* state, PyObject* token) {
+  long status, in_flight, limit;
+  if (!get_long(state, s_status_field, &status)) return -1;
+  if (status != kDecoding) {
+    Ref rid(PyObject_GetAttr(state, s_request_id));
+    Ref current(rid ? PyObject_GetAttr(state, s_status_field) : nullptr);
+    Ref name(current ? PyObject_GetAttr(current.get(), s_name) : nullptr);
+    if (name) PyErr_Format(PyExc_RuntimeError, "Cannot update request %S while status is %S", rid.get(), name.get());
+    return -1;
+  }
+  if (!get_long(state, s_tokens_in_flight, &in_flight) ||
+      !set_long(state, s_tokens_in_flight, std::max<long>(0, in_flight - 1)) ||
+      !get_long(state, s_new_tokens_limit, &limit))
+    return -1;
+  Ref eos(PyObject_GetAttr(state, s_eos_ids));
+  const int is_eos = eos ? PySequence_Contains(eos.get(), token) : -1;
+  Ref generated(is_eos >= 0 ? PyObject_GetAttr(state, s_generated_tokens) : nullptr);
+  if (!generated) return -1;
+  if (!PyList_Check(generated.get())) {
+    PyErr_SetString(PyExc_TypeError, "state.generated_tokens must be a list");
+    return -1;
+  }
+  Py_ssize_t n = PyList_GET_SIZE(generated.get());
+  if (is_eos || n < limit) {
+    Ref first(PyObject_GetAttr(state, s_first_token_time));
+    const double t = first ? PyFloat_AsDouble(first.get()) : -1.0;
+    if (!first || (t == -1.0 && PyErr_Occurred())) return -1;
+    if (t < 0) {
+      Ref now(PyObject_CallNoArgs(g_perf_counter));
+      if (!now || PyObject_SetAttr(state, s_first_token_time, now.get())) return -1;
+    }
+    Ref next(PyList_New(1));
+    if (!next || PyList_Append(generated.get(), token)) return -1;
+    Py_INCREF(token);
+    PyList_SET_ITEM(next.get(), 0, token);
+    if (PyObject_SetAttr(state, s_tokens_to_process, next.get())) return -1;
+    ++n;
+  }
+  int done = is_eos || n >= limit;
+  if (!done) done = matches_stop_sequence(state, generated.get());
+  if (done < 0) return -1;
+  if (done && PyObject_SetAttr(state, s_status, g_finished)) return -1;
+  return done;
+}
+
+PyObject* update_completion(PyObject*, PyObject* args) {
+  PyObject *state, *token;
+  if (!PyArg_ParseTuple(args, "OO", &state, &token)) return nullptr;
+  if (!g_finished) {
+    PyErr_SetString(PyExc_RuntimeError, "RequestStatus is not bound to the tick core");
+    return nullptr;
+  }
+  const int done = update_completion_of(state, token);
+  if (done < 0) return nullptr;
+  return PyBool_FromLong(done);
+}
+
+// consume_coda(items, tokens, eager) -> [(state, stage), ...]
+// A coda batch's sampled tokens, row by row: rows of finished requests are skipped; an
+// eagerly re-entered row only records its token; any other row first advances its
+// request's position. Each request that finishes is returned with stage False (to retire),
+// each unfinished non-eager one with stage True (its next decode token is to be staged),
+// in row order.
+PyObject* consume_coda(PyObject*, PyObject* args) {
+  PyObject *items, *tokens, *eager;
+  if (!PyArg_ParseTuple(args, "O!O!O", &PyList_Type, &items, &PyList_Type, &tokens, &eager)) return nullptr;
+  if (!g_finished) {
+    PyErr_SetString(PyExc_RuntimeError, "RequestStatus is not bound to the tick core");
+    return nullptr;
+  }
+  const Py_ssize_t n = PyList_GET_SIZE(items);
+  if (PyList_GET_SIZE(tokens) < n || (eager != Py_None && (!PyList_Check(eager) || PyList_GET_SIZE(eager) < n))) {
+    PyErr_SetString(PyExc_ValueError, "consume_coda: tokens and eager flags must cover every item");
+    return nullptr;
+  }
+  Ref actions(PyList_New(0));
+  if (!actions) return nullptr;
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    Ref state(PyObject_GetAttr(PyList_GET_ITEM(items, i), s_state));
+    long status;
+    if (!state || !get_long(state.get(), s_status_field, &status)) return nullptr;
+    if (status == kFinishedStatus) continue;
+    const int was_eager = eager == Py_None ? 0 : PyObject_IsTrue(PyList_GET_ITEM(eager, i));
+    if (was_eager < 0) return nullptr;
+    if (!was_eager) {
+      long position;
+      if (!get_long(state.get(), s_position_offset, &position) ||
+          !set_long(state.get(), s_position_offset, position + 1))
+        return nullptr;
+    }
+    const int done = update_completion_of(state.get(), PyList_GET_ITEM(tokens, i));
+    if (done < 0) return nullptr;
+    if (was_eager && !done) continue;
+    Ref action(Py_BuildValue("(OO)", state.get(), done ? Py_False : Py_True));
+    if (!action || PyList_Append(actions.get(), action.get())) return nullptr;
+  }
+  return actions.release();
+}
+
 PyMethodDef kMethods[] = {
     {"route_sync", route_sync, METH_VARARGS,
      "route_sync(items, flags, max_steps, histogram, backlog) -> (coda_items, refills, exits)"},
@@ -767,6 +1475,20 @@ PyMethodDef kMethods[] = {
     {"split_live", split_live, METH_VARARGS, "split_live(items, finished_status) -> (live, dead)"},
     {"select_eager", select_eager, METH_VARARGS,
      "select_eager(coda_items, block_size, allocate, item_type, token) -> (items, rows, flags)"},
+    {"bind_request_types", bind_request_types, METH_VARARGS, "bind_request_types(RequestStatus, FutureRequestState)"},
+    {"bind_batch_type", bind_batch_type, METH_O, "bind_batch_type(ScheduledCDBBatch)"},
+    {"schedule_next", schedule_next, METH_VARARGS,
+     "schedule_next(scheduler, token_budget, cache_budget, allow_coda) -> ScheduledCDBBatch | None"},
+    {"schedule_prefill", schedule_prefill, METH_VARARGS,
+     "schedule_prefill(scheduler, token_budget, cache_budget) -> ScheduledCDBBatch | None"},
+    {"prefill_bucket", prefill_bucket, METH_O, "prefill_bucket(scheduler) -> prefill candidates"},
+    {"record_resident_sample", record_resident_sample, METH_O, "record_resident_sample(scheduler)"},
+    {"prefill_admitted", prefill_admitted, METH_O, "prefill_admitted(scheduler) -> bool"},
+    {"allocate_if_needed", allocate_if_needed, METH_VARARGS,
+     "allocate_if_needed(scheduler, state, tokens) -> whether the request holds blocks for them"},
+    {"update_completion", update_completion, METH_VARARGS,
+     "update_completion(state, token) -> whether the request finished on this sampled token"},
+    {"consume_coda", consume_coda, METH_VARARGS, "consume_coda(items, tokens, eager) -> [(state, stage), ...]"},
     {nullptr, nullptr, 0, nullptr},
 };
 
@@ -785,10 +1507,36 @@ PyMODINIT_FUNC PyInit__tick(void) {
       {&s_tokens_in_flight, "tokens_in_flight"}, {&s_generated_tokens, "generated_tokens"},
       {&s_new_tokens_limit, "_new_tokens_limit"}, {&s_replay_eos_finishes, "replay_eos_finishes"},
       {&s_next_synthetic_exit_depth, "next_synthetic_exit_depth"},
+      {&s_active_requests, "active_requests"}, {&s_waiting_requests, "waiting_requests"},
+      {&s_waiting_order, "waiting_requests_order"}, {&s_block_new_requests, "block_new_requests"},
+      {&s_ready_queue, "ready_queue"}, {&s_coda_queue, "coda_queue"}, {&s_in_flight_ids, "in_flight_request_ids"},
+      {&s_max_num_seqs, "max_num_seqs"}, {&s_min_coda_batch_size, "min_coda_batch_size"},
+      {&s_min_free_slots, "min_free_slots"}, {&s_safety_margin, "safety_margin"},
+      {&s_kv_pressure_mode, "kv_pressure_mode"}, {&s_max_model_len, "max_model_len"}, {&s_cache, "cache"},
+      {&s_max_fast_path_len, "max_decode_fast_path_length"}, {&s_slot_of_step, "_slot_of_step"},
+      {&s_mixed_batches, "mixed_batches_scheduled"}, {&s_max_in_flight, "max_in_flight_requests"},
+      {&s_max_live, "max_live_requests"}, {&s_max_resident, "max_resident_requests"},
+      {&s_resident_samples, "resident_samples"}, {&s_resident_sum, "resident_sum"},
+      {&s_steady_warmup, "steady_warmup_requests"}, {&s_advance_steady, "_advance_steady_window"},
+      {&s_block_manager, "_block_manager"}, {&s_num_blocks, "num_blocks"}, {&s_block_size, "block_size"},
+      {&s_allocate_blocks, "allocate_blocks"}, {&s_get_num_free_blocks, "get_num_free_blocks"},
+      {&s_is_cpu_offloaded, "is_cpu_offloaded"}, {&s_remaining_prefill, "remaining_prefill_tokens"},
+      {&s_tokens_to_process, "tokens_to_process"}, {&s_initial_tokens, "initial_tokens"},
+      {&s_max_new_tokens, "max_new_tokens"}, {&s_status, "status"}, {&s_popleft, "popleft"},
+      {&s_reserve, "reserve"}, {&s_kind_coda, "coda"}, {&s_kind_prefill, "prefill"},
+      {&s_kind_recurrent, "recurrent"}, {&s_eos_ids, "_eos_token_ids"}, {&s_stop_sequences, "stop_sequences"},
+      {&s_first_token_time, "first_token_time"}, {&s_name, "name"},
   };
   for (const Name& nm : names) {
     *nm.slot = PyUnicode_InternFromString(nm.text);
     if (!*nm.slot) return nullptr;
+  }
+  {
+    PyObject* time_module = PyImport_ImportModule("time");
+    if (!time_module) return nullptr;
+    g_perf_counter = PyObject_GetAttrString(time_module, "perf_counter");
+    Py_DECREF(time_module);
+    if (!g_perf_counter) return nullptr;
   }
   BlockPoolType.tp_name = "_tick.BlockPool";
   BlockPoolType.tp_basicsize = sizeof(BlockPool);

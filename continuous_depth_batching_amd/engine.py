@@ -530,20 +530,20 @@ class ContinuousDepthBatchingEngine:
             self._consume_coda_result(pending)
 
     def _consume_coda_result(self, pending: PendingCodaResult) -> None:
+        """Sampled tokens of a coda batch (cdb/continuous_api.py:1378-1406).
+
+        The tick core walks the rows: finished requests are skipped, eager rows only record
+        their token, other rows advance their position first. What is left here is the
+        requests that finished (retired) and the non-eager survivors (next token staged),
+        in row order."""
+
         tokens = self.runner.consume_coda_result(pending)
         self.last_stats.coda_batches += 1
         self.last_stats.coda_tokens += len(pending.items)
-        eager = pending.eager_reentries or [False] * len(pending.items)
         new_items: list[DepthWorkItem] = []
-        for item, token, was_eager in zip(pending.items, tokens, eager):
-            state = item.state
-            if state.status == RequestStatus.FINISHED:
-                continue
-            if was_eager:
-                if state.update_and_check_completion(token):
-                    self._retire_request(state)
-                continue
-            if self._advance_after_coda(item, token):
+        for state, stage in _tick.consume_coda(pending.items, tokens, pending.eager_reentries):
+            if not stage:
+                self._retire_request(state)
                 continue
             new = self._stage_decode_token(state)
             if new is not None:
@@ -695,7 +695,7 @@ class ContinuousDepthBatchingEngine:
             self._restore_offloaded_requests()
             sched.record_resident_sample()
             did_prefill = False
-            while sched.admit_prefill(sched.has_decode_work()):
+            while sched.prefill_admitted():
                 scheduled = sched.schedule_prefill_batch(token_budget=self.cache.max_num_batched_tokens,
                                                          cache_budget=self.cache.num_pages)
                 if scheduled is None or not scheduled.requests:

@@ -15,6 +15,8 @@ import time
 from dataclasses import dataclass, field
 from enum import IntEnum
 
+from . import _tick
+
 logger = logging.getLogger("ContinuousBatchingLogger")
 
 #: Placeholder id of a token that the device has sampled but the host has not seen.
@@ -114,29 +116,14 @@ class RequestState:
         return self.tokens_in_flight > 0 and self.generated_len() + self.tokens_in_flight >= self._new_tokens_limit
 
     def update_and_check_completion(self, token_id: int) -> bool:
-        """Record a sampled token; return whether the request finished (requests.py:208-237)."""
+        """Record a sampled token; return whether the request finished (requests.py:208-237).
 
-        if self.status != RequestStatus.DECODING:
-            raise RuntimeError(f"Cannot update request {self.request_id} while status is {self.status.name}")
-        self.tokens_in_flight = max(0, self.tokens_in_flight - 1)
-        is_eos = token_id in self._eos_token_ids
-        n = self.generated_len()
-        if is_eos or n < self._new_tokens_limit:
-            if self.first_token_time < 0:
-                self.first_token_time = time.perf_counter()
-            self.generated_tokens.append(token_id)
-            self.tokens_to_process = [token_id]
-            n += 1
-        if is_eos or n >= self._new_tokens_limit or self._matches_stop_sequence():
-            self.status = RequestStatus.FINISHED
-            return True
-        return False
+        One fewer token is in flight; the token is kept (and becomes the next token to
+        process) when it is EOS or within the length limit; the request finishes on EOS, at
+        the limit or when the generated tokens end with a stop sequence. Runs in the tick
+        core, which also applies it row by row to coda results."""
 
-    def _matches_stop_sequence(self) -> bool:
-        for seq in self.stop_sequences:
-            if seq and len(self.generated_tokens) >= len(seq) and self.generated_tokens[-len(seq):] == seq:
-                return True
-        return False
+        return _tick.update_completion(self, token_id)
 
     def reset_depth_state_for_next_token(self) -> None:
         self.current_token_exit_depth = None
@@ -229,3 +216,6 @@ class DepthWorkItem:
     synthetic_exit_depth: int | None = None
     apply_exit_gate: bool = True
     hidden_slot: int | None = None
+
+
+_tick.bind_request_types(RequestStatus, FutureRequestState)

@@ -9,6 +9,10 @@ working set advancing (:142-180). Under multi-slot KV layouts a recurrent
 batch holds only items writing the same slot (:322-346). Admission, token
 budgets and block allocation follow scheduler_base.py:171-545. ``mixed_slot_launches`` lifts the
 slot rule (the kernels read a cache layer per row).
+
+The per-tick decisions run in the C++ tick core (``_tick.schedule_next`` and the
+admission functions beside it) over this object's attributes: the queues, the
+request dicts and counters stay here, where the engine and its statistics read them.
 """
 
 from __future__ import annotations
@@ -16,7 +20,6 @@ from __future__ import annotations
 import time
 from collections import deque
 from dataclasses import dataclass
-from itertools import islice
 from typing import Literal
 
 from . import _tick
@@ -112,15 +115,10 @@ class CDBScheduler:
     def has_pending_work(self) -> bool:
         return bool(self.coda_queue or self.ready_queue or self.active_requests or self.waiting_requests)
 
-    def has_decode_work(self) -> bool:
-        return any(s.status == RequestStatus.DECODING for s in self.active_requests.values())
-
     def record_resident_sample(self) -> None:
-        resident = len(self.active_requests)
-        self.max_resident_requests = max(self.max_resident_requests, resident)
-        self.resident_samples += 1
-        self.resident_sum += resident
-        self._advance_steady_window(resident)
+        """Resident-set peak and mean, and the steady-state window when one is tracked."""
+
+        _tick.record_resident_sample(self)
 
     # -- steady-state window (scheduler_base.py:315-398) --------------------------------------------------------
     @property
@@ -203,12 +201,11 @@ class CDBScheduler:
         if live > self.max_live_requests:
             self.max_live_requests = live
 
-    # -- admission (scheduler_base.py:171-201, 416-531) --------------------------------------------------------
-    def has_prefill_headroom(self) -> bool:
-        return self.cache.get_num_free_blocks() > self.safety_margin * self.cache.num_blocks
+    # -- admission (scheduler_base.py:171-201, 416-545) --------------------------------------------------------
+    def prefill_admitted(self) -> bool:
+        """Prefill may run: nothing decodes, or the free blocks exceed the safety margin."""
 
-    def admit_prefill(self, has_decode_work: bool) -> bool:
-        return not has_decode_work or self.has_prefill_headroom()
+        return _tick.prefill_admitted(self)
 
     def free_residency_slots(self) -> int:
         return max(0, self.max_num_seqs - len(self.active_requests))
@@ -235,82 +232,17 @@ class CDBScheduler:
             admitted.append(state)
         return admitted
 
-    def admit_prefill_batch(self, candidates: list[RequestState]) -> bool:
-        if not candidates:
-            return False
-        if any(s.status == RequestStatus.PREFILLING for s in candidates):
-            return True
-        return self.free_residency_slots() >= self.min_free_slots
-
-    def _prefill_admits(self, state: RequestState) -> bool:
-        return state.request_id not in self.in_flight_request_ids
-
-    def _get_waiting_candidates(self, limit: int | None = None) -> list[RequestState]:
-        fresh = (self.waiting_requests[r] for r in self.waiting_requests_order
-                 if not self.waiting_requests[r].is_cpu_offloaded)
-        return list(islice(fresh, limit))
-
     def get_prefill_bucket(self) -> list[RequestState]:
-        prefilling = [s for s in self.active_requests.values()
-                      if s.status == RequestStatus.PREFILLING and self._prefill_admits(s)]
-        if self.block_new_requests:
-            return prefilling
-        admissible = self._get_waiting_candidates(limit=self.free_residency_slots())
-        if self.kv_pressure_mode == "reserve":
-            committed = sum(reserved_peak_blocks(len(s.initial_tokens), s.max_new_tokens, self.max_model_len,
-                                                 self.cache.block_size) for s in self.active_requests.values())
-            fitting = []
-            for s in admissible:
-                need = reserved_peak_blocks(len(s.initial_tokens), s.max_new_tokens, self.max_model_len,
-                                            self.cache.block_size)
-                if committed + need > self.cache.num_blocks:
-                    break
-                committed += need
-                fitting.append(s)
-            admissible = fitting
-        return prefilling + admissible
+        """Requests mid-prefill with no token in flight, then admissible waiting prompts."""
 
-    def get_prefill_candidates(self) -> list[RequestState]:
-        candidates = self.get_prefill_bucket()
-        return candidates if self.admit_prefill_batch(candidates) else []
-
-    def _cleanup_waiting_queue(self, ids: set[str]) -> None:
-        remaining = set(ids)
-        order = self.waiting_requests_order
-        while remaining and order and order[0] in remaining:
-            remaining.discard(order.popleft())
-        if remaining:
-            self.waiting_requests_order = deque(r for r in order if r not in remaining)
+        return _tick.prefill_bucket(self)
 
     def _allocate_blocks_if_needed(self, state: RequestState, len_next_tokens: int) -> bool:
-        current = state.current_len()
-        if state.allocated_blocks * self.cache.block_size - current < len_next_tokens:
-            needed = -(-(current + len_next_tokens) // self.cache.block_size) - state.allocated_blocks
-            got = self.cache.allocate_blocks(needed, state.request_id, state.allocated_blocks)
-            if got is None:
-                return False
-            state.allocated_blocks += got
-        return True
+        return _tick.allocate_if_needed(self, state, len_next_tokens)
 
     # -- bucket selection (continuous_depth_batching/scheduler.py:101-349) ------------------------------------
     def schedule_next(self, token_budget: int, cache_budget: int, *, allow_coda: bool = True) -> ScheduledCDBBatch | None:
-        self.record_resident_sample()
-        if allow_coda and len(self.coda_queue) >= self.min_coda_batch_size:
-            batch = self._schedule_coda_batch()
-            if batch:
-                return ScheduledCDBBatch(kind="coda", depth_items=batch)
-        if self.admit_prefill(self.has_decode_work()):
-            prefill = self.schedule_prefill_batch(token_budget=token_budget, cache_budget=cache_budget)
-            if prefill is not None:
-                return prefill
-        recurrent = self._schedule_recurrent_batch()
-        if recurrent:
-            return ScheduledCDBBatch(kind="recurrent", depth_items=recurrent)
-        if allow_coda:
-            batch = self._schedule_coda_batch()
-            if batch:
-                return ScheduledCDBBatch(kind="coda", depth_items=batch)
-        return None
+        return _tick.schedule_next(self, token_budget, cache_budget, allow_coda)
 
     def enqueue_depth(self, item: DepthWorkItem, *, front: bool = False) -> None:
         if not 0 <= item.recurrent_step < self.max_recurrent_steps:
@@ -361,83 +293,9 @@ class CDBScheduler:
         self.coda_queue.extend(items)
 
     def schedule_prefill_batch(self, token_budget: int, cache_budget: int) -> ScheduledCDBBatch | None:
-        candidates = self.get_prefill_candidates()
-        if not candidates:
-            return None
-        to_remove: set[str] = set()
-        scheduled, num_q_tokens, max_kv_read = self._process_prefill_candidates(candidates, token_budget,
-                                                                                cache_budget, to_remove)
-        self._cleanup_waiting_queue(to_remove)
-        if not scheduled:
-            return None
-        return ScheduledCDBBatch(kind="prefill", requests=scheduled, num_q_tokens=num_q_tokens,
-                                 max_kv_read=max_kv_read)
+        return _tick.schedule_prefill(self, token_budget, cache_budget)
 
-    def _process_prefill_candidates(self, candidates: list[RequestState], token_budget: int, cache_budget: int,
-                                    to_remove: set[str]) -> tuple[list[FutureRequestState], int, int]:
-        scheduled: list[FutureRequestState] = []
-        decode_fast_path = True
-        margin_blocks = self.safety_margin * self.cache.num_blocks
-        original_tokens, original_cache = token_budget, cache_budget
-        for state in candidates:
-            free = self.cache.get_num_free_blocks()
-            if free < margin_blocks and scheduled:
-                break
-            tokens = state.remaining_prefill_tokens
-            request_len = min(len(tokens), token_budget)
-            if request_len == 0:
-                continue
-            eligible = request_len == 1 and state.position_offset < self.max_decode_fast_path_length
-            read_needed = state.current_len()
-            if not (decode_fast_path and eligible) and cache_budget < read_needed:
-                continue
-            if not self._allocate_blocks_if_needed(state, request_len):
-                if free == 0 and state.request_id in self.waiting_requests:
-                    break
-                continue
-            self._schedule_prefill_request(state, tokens, request_len, to_remove)
-            self._mark_request_in_flight(state.request_id)
-            request_len = len(state.tokens_to_process)
-            decode_fast_path &= request_len == 1 and state.position_offset < self.max_decode_fast_path_length
-            token_budget -= request_len
-            cache_budget -= read_needed
-            scheduled.append(FutureRequestState(state, not state.remaining_prefill_tokens, request_len))
-            if self.waiting_requests.pop(state.request_id, None) is not None:
-                to_remove.add(state.request_id)
-            if token_budget == 0 or (cache_budget <= 0 and not decode_fast_path):
-                break
-        return scheduled, original_tokens - token_budget, original_cache - cache_budget
 
-    def _schedule_prefill_request(self, state: RequestState, tokens: list[int], request_len: int,
-                                  to_remove: set[str]) -> None:
-        if len(tokens) <= request_len:
-            if state.status == RequestStatus.PENDING:
-                self.active_requests[state.request_id] = state
-                to_remove.add(state.request_id)
-            if state.status <= RequestStatus.PREFILLING:
-                state.tokens_to_process = state.remaining_prefill_tokens
-                state.remaining_prefill_tokens = []
-                state.status = RequestStatus.DECODING
-            return
-        if state.status == RequestStatus.PENDING:
-            self.active_requests[state.request_id] = state
-            state.status = RequestStatus.PREFILLING
-            to_remove.add(state.request_id)
-        state.remaining_prefill_tokens = tokens[request_len:]
-        state.tokens_to_process = tokens[:request_len]
-
-    def _schedule_recurrent_batch(self) -> list[DepthWorkItem]:
-        # The head item, then queue order; under the slot-homogeneous rule only items writing the
-        # head's KV slot, the skipped ones kept in order ahead of the rest (tick core pop_batch).
-        size = min(self.max_num_seqs, len(self.ready_queue))
-        if size == 0:
-            return []
-        batch = _tick.pop_batch(self.ready_queue, size, self._slot_of_step)
-        self.mixed_batches_scheduled += 1
-        return batch
-
-    def _schedule_coda_batch(self) -> list[DepthWorkItem]:
-        return _tick.pop_front(self.coda_queue, min(self.max_num_seqs, len(self.coda_queue)))
-
+_tick.bind_batch_type(ScheduledCDBBatch)
 
 __all__ = ["CDBScheduler", "ScheduledCDBBatch", "reserved_peak_blocks", "logger"]

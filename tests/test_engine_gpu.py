@@ -84,14 +84,18 @@ def test_config1_live_gate_last_exited(refill: bool) -> None:
     assert engine.last_stats.exit_kv_copies == sum(w.exit_copies for w in want)
 
 
-@pytest.mark.parametrize("async_batching", [False, True])
-def test_synthetic_replay_single_policy_refill(async_batching: bool) -> None:
+@pytest.mark.parametrize("async_batching,graphs", [(False, True), (True, True), (True, False)])
+def test_synthetic_replay_single_policy_refill(async_batching: bool, graphs: bool) -> None:
+    """Refill at mixed loop steps; ``graphs=False`` runs every stage eagerly (no recorded graph),
+    including the block-table updates that the recorded recurrent graph otherwise applies."""
+
     model, weights = build_model(seed=1)
     prompts, mnt = workload(seed=1, n=12, new_tokens=24)
     rng = np.random.default_rng(2)
     depths = [rng.choice(4, size=m - 1, p=[0.15, 0.25, 0.3, 0.3]).tolist() for m in mnt]
     engine = make_engine(model, synthetic_exit_replay=True, kv_policy="single", delay_gate_consumption=False,
-                         use_async_batching=async_batching, max_num_seqs=8)
+                         use_async_batching=async_batching, max_num_seqs=8, use_cuda_graph=graphs,
+                         use_cuda_graph_prefill=graphs)
     outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=None, exit_depths=depths)
     want = run_oracle(weights, prompts, mnt, kv_policy="single", exit_depths=depths)
     assert [o.generated_tokens for o in outs] == [w.tokens for w in want]

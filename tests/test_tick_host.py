@@ -17,7 +17,7 @@ import pytest
 
 from continuous_depth_batching_amd import _tick
 from continuous_depth_batching_amd.model_runner import ModelRunner
-from continuous_depth_batching_amd.requests import DepthWorkItem, RequestState
+from continuous_depth_batching_amd.requests import DepthWorkItem, RequestState, RequestStatus
 
 M = ModelRunner
 
@@ -328,3 +328,92 @@ def test_select_eager_matches_the_per_row_python(seed: int) -> None:
                        for i in items], rows, flags, _eager_snapshot(coda), budget["blocks"]))
     assert built[0] == built[1]
     assert any(built[0][2]) and not all(built[0][2])
+
+
+def _update_python(state: RequestState, token: int) -> bool:
+    """RequestState.update_and_check_completion as plain Python (requests.py:208-237)."""
+
+    if state.status != RequestStatus.DECODING:
+        raise RuntimeError(f"Cannot update request {state.request_id} while status is {state.status.name}")
+    state.tokens_in_flight = max(0, state.tokens_in_flight - 1)
+    is_eos = token in state._eos_token_ids
+    n = len(state.generated_tokens)
+    if is_eos or n < state._new_tokens_limit:
+        if state.first_token_time < 0:
+            state.first_token_time = 1.0
+        state.generated_tokens.append(token)
+        state.tokens_to_process = [token]
+        n += 1
+    stop = any(seq and len(state.generated_tokens) >= len(seq) and state.generated_tokens[-len(seq):] == seq
+               for seq in state.stop_sequences)
+    if is_eos or n >= state._new_tokens_limit or stop:
+        state.status = RequestStatus.FINISHED
+        return True
+    return False
+
+
+def _decoding_states(rng: random.Random, n: int) -> list[RequestState]:
+    states = []
+    for i in range(n):
+        state = RequestState(request_id=f"q{i}", initial_tokens=[1, 2], max_new_tokens=rng.choice([None, 2, 5]),
+                             eos_token_id=rng.choice([None, 7, [7, 9], -1]),
+                             stop_sequences=rng.choice([[], [[3, 4]], [[], [5]], [[1, 2, 3]]]))
+        state.status = RequestStatus.DECODING
+        state.generated_tokens = [rng.randrange(10) for _ in range(rng.randrange(4))]
+        state.tokens_in_flight = rng.randrange(3)
+        state.position_offset = rng.randrange(50)
+        if rng.random() < 0.3:
+            state.first_token_time = 0.5
+        if rng.random() < 0.15:
+            state.status = RequestStatus.FINISHED
+        states.append(state)
+    return states
+
+
+def _request_view(state: RequestState):
+    return (int(state.status), list(state.generated_tokens), list(state.tokens_to_process), state.tokens_in_flight,
+            state.position_offset, state.first_token_time >= 0)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_update_completion_matches_the_python(seed: int) -> None:
+    rng = random.Random(seed)
+    for case in range(60):
+        a, b = (_decoding_states(random.Random(seed * 1000 + case), 1)[0] for _ in range(2))
+        if a.status == RequestStatus.FINISHED:
+            with pytest.raises(RuntimeError, match="while status is FINISHED"):
+                _tick.update_completion(a, 1)
+            continue
+        for _step in range(6):
+            token = rng.randrange(10)
+            if a.status != RequestStatus.DECODING:
+                break
+            assert _tick.update_completion(a, token) == _update_python(b, token)
+            assert _request_view(a) == _request_view(b)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_consume_coda_matches_the_per_row_python(seed: int) -> None:
+    rng = random.Random(seed)
+    n = rng.randint(1, 24)
+    tokens = [rng.randrange(10) for _ in range(n)]
+    eager = None if seed % 4 == 0 else [rng.random() < 0.6 for _ in range(n)]
+    twins = [_decoding_states(random.Random(seed), n) for _ in range(2)]
+    items = [[DepthWorkItem(state=s, token_id=0, token_position=0, recurrent_step=0) for s in states]
+             for states in twins]
+    got = [(s.request_id, stage) for s, stage in _tick.consume_coda(items[0], tokens, eager)]
+    want = []
+    for item, token, was_eager in zip(items[1], tokens, eager or [False] * n):
+        state = item.state
+        if state.status == RequestStatus.FINISHED:
+            continue
+        if was_eager:
+            if _update_python(state, token):
+                want.append((state.request_id, False))
+            continue
+        state.position_offset += 1
+        want.append((state.request_id, not _update_python(state, token)))
+    assert got == want
+    assert [_request_view(s) for s in twins[0]] == [_request_view(s) for s in twins[1]]
+    with pytest.raises(ValueError):
+        _tick.consume_coda(items[0], tokens[:-1], eager)

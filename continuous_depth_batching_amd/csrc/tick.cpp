@@ -14,6 +14,7 @@
 //                   (continuous_depth_batching/scheduler.py:101-180, 322-346).
 //   split_live      drops work items of finished requests before a launch.
 //   select_eager    chooses a coda's eager successors (cdb/continuous_api.py:1304-1327).
+//   coda_upload     a coda launch's slot upload and its successors' hidden slots.
 //   consume_coda    a coda batch's sampled tokens: token append and finish checks
 //                   (continuous_batching/requests.py:208-237) row by row.
 //   schedule_next   the scheduler's per-tick bucket choice (coda > prefill > recurrent >
@@ -1464,6 +1465,73 @@ PyObject* consume_coda(PyObject*, PyObject* args) {
   return actions.release();
 }
 
+// add_tokens_in_flight(items): one more sampled token in flight on each item's request.
+PyObject* add_tokens_in_flight(PyObject*, PyObject* items) {
+  if (!PyList_Check(items)) {
+    PyErr_SetString(PyExc_TypeError, "items must be a list");
+    return nullptr;
+  }
+  for (Py_ssize_t i = 0; i < PyList_GET_SIZE(items); ++i) {
+    Ref state(PyObject_GetAttr(PyList_GET_ITEM(items, i), s_state));
+    if (!state || !add_long(state.get(), s_tokens_in_flight, 1)) return nullptr;
+  }
+  Py_RETURN_NONE;
+}
+
+// coda_upload(items, successors, rows, upload_addr, upload_len, free_slots, next_slot, capacity) -> next_slot
+// Fills a coda launch's int64 host upload (cdb/model_runner.py:1064-1125 stages the same
+// facts): [the items' hidden slots | per item, its successor's slot or -1 | the successors'
+// slots]. Each successor (one per listed coda row) gets a hidden slot: the most recently
+// freed first (free_slots is a LIFO list), then fresh ones from next_slot below capacity
+// (cdb/model_runner.py:1193-1203). Without successors only the items' slots are written.
+PyObject* coda_upload(PyObject*, PyObject* args) {
+  PyObject *items, *successors, *rows, *free_slots;
+  unsigned long long addr;
+  Py_ssize_t upload_len;
+  long next_slot, capacity;
+  if (!PyArg_ParseTuple(args, "O!O!O!KnO!ll", &PyList_Type, &items, &PyList_Type, &successors, &PyList_Type, &rows,
+                        &addr, &upload_len, &PyList_Type, &free_slots, &next_slot, &capacity))
+    return nullptr;
+  const Py_ssize_t n = PyList_GET_SIZE(items), k = PyList_GET_SIZE(successors);
+  if (PyList_GET_SIZE(rows) != k || n + (k ? n + k : 0) > upload_len || addr == 0) {
+    PyErr_SetString(PyExc_ValueError, "coda_upload: rows must match the successors and the upload hold them all");
+    return nullptr;
+  }
+  int64_t* upload = reinterpret_cast<int64_t*>(static_cast<uintptr_t>(addr));
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    long slot;
+    if (!get_long(PyList_GET_ITEM(items, i), s_hidden_slot, &slot)) return nullptr;
+    upload[i] = slot;
+  }
+  if (k == 0) return PyLong_FromLong(next_slot);
+  for (Py_ssize_t i = 0; i < n; ++i) upload[n + i] = -1;
+  for (Py_ssize_t j = 0; j < k; ++j) {
+    long slot;
+    const Py_ssize_t nfree = PyList_GET_SIZE(free_slots);
+    if (nfree > 0) {
+      slot = PyLong_AsLong(PyList_GET_ITEM(free_slots, nfree - 1));
+      if (slot == -1 && PyErr_Occurred()) return nullptr;
+      if (PyList_SetSlice(free_slots, nfree - 1, nfree, nullptr)) return nullptr;
+    } else {
+      if (next_slot >= capacity) {
+        PyErr_Format(PyExc_RuntimeError, "hidden-state bank exhausted (%ld slots)", capacity);
+        return nullptr;
+      }
+      slot = next_slot++;
+    }
+    const long row = PyLong_AsLong(PyList_GET_ITEM(rows, j));
+    if (row == -1 && PyErr_Occurred()) return nullptr;
+    if (row < 0 || row >= n) {
+      PyErr_Format(PyExc_ValueError, "coda_upload: successor row %ld outside the %zd coda rows", row, n);
+      return nullptr;
+    }
+    upload[n + row] = slot;
+    upload[2 * n + j] = slot;
+    if (!set_long(PyList_GET_ITEM(successors, j), s_hidden_slot, slot)) return nullptr;
+  }
+  return PyLong_FromLong(next_slot);
+}
+
 PyMethodDef kMethods[] = {
     {"route_sync", route_sync, METH_VARARGS,
      "route_sync(items, flags, max_steps, histogram, backlog) -> (coda_items, refills, exits)"},
@@ -1489,6 +1557,9 @@ PyMethodDef kMethods[] = {
     {"update_completion", update_completion, METH_VARARGS,
      "update_completion(state, token) -> whether the request finished on this sampled token"},
     {"consume_coda", consume_coda, METH_VARARGS, "consume_coda(items, tokens, eager) -> [(state, stage), ...]"},
+    {"add_tokens_in_flight", add_tokens_in_flight, METH_O, "add_tokens_in_flight(items)"},
+    {"coda_upload", coda_upload, METH_VARARGS,
+     "coda_upload(items, successors, rows, upload_addr, upload_len, free_slots, next_slot, capacity) -> next_slot"},
     {nullptr, nullptr, 0, nullptr},
 };
 

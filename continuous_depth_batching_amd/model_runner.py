@@ -165,6 +165,7 @@ class _CodaTurn:
     host_tokens: torch.Tensor  # pinned int64 greedy tokens
     event: Any
     direct: ops.CodaScratch | None = None  # one-call coda of up to CODA_DIRECT_MAX_ROWS rows
+    upload_addr: int = 0  # host_upload.data_ptr()
 
 
 class ModelRunner:
@@ -516,22 +517,17 @@ class ModelRunner:
 
         if not items:
             return PendingCodaResult(items=[], host_tokens=torch.empty(0, dtype=torch.int64))
-        for item in items:
-            item.state.tokens_in_flight += 1
+        _tick.add_tokens_in_flight(items)
         n = len(items)
         eager_items, eager_rows = successors(items) if successors is not None else ([], [])
         fused = bool(eager_items) and self.adapter.coda_writes_successor_prelude
         m = n + n + len(eager_items) if fused else n
         turn = self._coda_turn(m, n)
-        upload = turn.host_upload.numpy()
-        upload[:n] = [it.hidden_slot for it in items]
-        if fused:
-            new_slots = self.allocate_hidden_slots(len(eager_items))
-            # One upload: [coda rows' slots | each row's successor slot or -1 | the successors' slots].
-            successor = upload[n:2 * n]
-            successor[:] = -1
-            successor[eager_rows] = new_slots
-            upload[2 * n:m] = new_slots
+        # One upload: [coda rows' slots | each row's successor slot or -1 | the successors' slots],
+        # the successors taking hidden slots (LIFO free list first) in the same call.
+        self.next_hidden_slot = _tick.coda_upload(
+            items, eager_items if fused else [], eager_rows if fused else [], turn.upload_addr,
+            turn.host_upload.numel(), self.free_hidden_slots, self.next_hidden_slot, self.bank_capacity)
         direct = turn.direct if n <= ops.CODA_DIRECT_MAX_ROWS and (fused or not eager_items) else None
         with self._on_stream():
             event = turn.event
@@ -554,10 +550,7 @@ class ModelRunner:
                 if fused:
                     self.gate_state.reset(dev[2 * n:], len(eager_items))
         pending = PendingCodaResult(items=items, host_tokens=host, device_tokens=tokens, ready_event=event)
-        if fused:
-            for item, slot in zip(eager_items, new_slots):
-                item.hidden_slot = slot
-        elif eager_items:
+        if eager_items and not fused:
             self.compute_prelude_batch(eager_items, device_groups=[(pending, eager_rows)])
         if not allow_async:
             event.synchronize()
@@ -581,6 +574,7 @@ class ModelRunner:
                 dev_upload=torch.empty(cap, dtype=torch.int64, device=self.device),
                 host_tokens=self._pinned((max(rows, seqs),), torch.int64),
                 event=torch.cuda.Event())
+            turn.upload_addr = turn.host_upload.data_ptr()
             if self._coda_weights is not None:
                 turn.direct = ops.CodaScratch(self._coda_weights, self.bank, self.gate_state, turn.host_upload,
                                               turn.dev_upload, turn.host_tokens)

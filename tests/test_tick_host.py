@@ -417,3 +417,44 @@ def test_consume_coda_matches_the_per_row_python(seed: int) -> None:
     assert [_request_view(s) for s in twins[0]] == [_request_view(s) for s in twins[1]]
     with pytest.raises(ValueError):
         _tick.consume_coda(items[0], tokens[:-1], eager)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_coda_upload_matches_the_python_staging(seed: int) -> None:
+    """The coda upload and the successors' hidden slots, as the runner built them in Python
+    (LIFO free slots first, then fresh ones; cdb/model_runner.py:1193-1203)."""
+
+    rng = random.Random(seed)
+    n = rng.randint(1, 20)
+    k = rng.randint(0, n)
+    rows = sorted(rng.sample(range(n), k))
+    free = [rng.randrange(100) for _ in range(rng.randrange(6))]
+    next_slot, capacity = 100, 100 + k
+    items = [DepthWorkItem(state=RequestState(request_id=f"c{i}", initial_tokens=[1]), token_id=0,
+                           token_position=0, recurrent_step=0, hidden_slot=rng.randrange(100)) for i in range(n)]
+    succ = [DepthWorkItem(state=items[r].state, token_id=-1, token_position=1, recurrent_step=0) for r in rows]
+    upload = np.full(3 * n + 4, 77, dtype=np.int64)
+    free_c = list(free)
+    got_next = _tick.coda_upload(items, succ, rows, upload.ctypes.data, upload.size, free_c, next_slot, capacity)
+
+    want = np.full_like(upload, 77)
+    want[:n] = [it.hidden_slot for it in items]
+    free_p, nxt, slots = list(free), next_slot, []
+    for _ in range(k):
+        if free_p:
+            slots.append(free_p.pop())
+        else:
+            slots.append(nxt)
+            nxt += 1
+    if k:
+        want[n:2 * n] = -1
+        want[n + np.array(rows, dtype=np.int64)] = slots
+        want[2 * n:2 * n + k] = slots
+    assert upload.tolist() == want.tolist()
+    assert got_next == nxt and free_c == free_p
+    assert [s.hidden_slot for s in succ] == slots
+    if k:
+        with pytest.raises(RuntimeError, match="bank exhausted"):
+            _tick.coda_upload(items, succ, rows, upload.ctypes.data, upload.size, [], capacity, capacity)
+        with pytest.raises(ValueError):
+            _tick.coda_upload(items, succ, rows, upload.ctypes.data, 2 * n, [], 0, capacity)

@@ -24,6 +24,14 @@ CDB_DEVICE float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) 
 // (no branch, so surrounding loads stay batched); NaN stays NaN.
 CDB_DEVICE uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
+// Two fp32 values as one word of bf16 (lo in the low half), rounded as f32_to_bf16:
+// a single v_cvt_pk_bf16_f32 for both.
+typedef float cdb_f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 cdb_bf16x2_t __attribute__((ext_vector_type(2)));
+CDB_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((cdb_f32x2_t){lo, hi}, cdb_bf16x2_t));
+}
+
 // Round an fp32 value to the nearest bf16 and return it as fp32.
 CDB_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -87,6 +95,15 @@ template <typename T, int N> struct Vec {
     } else {
       uint32_t word = w[i >> 1];
       return (i & 1) ? __uint_as_float(word & 0xffff0000u) : __uint_as_float(word << 16);
+    }
+  }
+  // Elements i and i + 1 (i even) at once.
+  CDB_DEVICE void set_pair(int i, float a, float b) {
+    if constexpr (sizeof(T) == 4) {
+      w[i] = __float_as_uint(a);
+      w[i + 1] = __float_as_uint(b);
+    } else {
+      w[i >> 1] = pack_bf16x2(a, b);
     }
   }
   CDB_DEVICE void set(int i, float v) {

@@ -547,8 +547,8 @@ __global__ void __launch_bounds__(256) prefill_attention_bf16_kernel(PrefillPara
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       Vec<bf16_t, 4> ov;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ov.set(i, o[j][4 * a + i] * inv);
+      ov.set_pair(0, o[j][4 * a] * inv, o[j][4 * a + 1] * inv);
+      ov.set_pair(2, o[j][4 * a + 2] * inv, o[j][4 * a + 3] * inv);
       ov.store(orow + 32 * j + 8 * a + 4 * half);
     }
 }

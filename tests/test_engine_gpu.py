@@ -158,3 +158,39 @@ def test_mixed_slot_launches_last_exited_follow_the_oracle(refill: bool) -> None
     assert engine.last_stats.exit_kv_copies == sum(w.exit_copies for w in want)
     mixed = [ev for ev in engine.launch_log if ev[0] == "recurrent" and len({row[2] for row in ev[1]}) > 1]
     assert mixed, "launches must mix loop steps (and so KV slots)"
+
+
+@pytest.mark.parametrize("async_batching", [False, True])
+def test_eos_finishes_follow_the_oracle(async_batching: bool) -> None:
+    """Requests that stop on EOS mid-stream: with async batching an EOS token arrives after the
+    request's successor was already staged (eager re-entry), so the finish must cancel that
+    queued successor. The EOS ids are decoded tokens of four of the oracle's streams; greedy
+    decode is prefix-consistent, so each expected stream is the oracle's stream cut after its
+    first EOS token (with one exit depth per decoded token)."""
+
+    model, weights = build_model(seed=7)
+    prompts, mnt = workload(seed=7, n=10, new_tokens=24)
+    rng = np.random.default_rng(8)
+    depths = [rng.choice(4, size=m - 1, p=[0.15, 0.25, 0.3, 0.3]).tolist() for m in mnt]
+    free_run = run_oracle(weights, prompts, mnt, kv_policy="single", exit_depths=depths)
+    eos = sorted({free_run[r].tokens[3 + 2 * r] for r in (0, 2, 4, 6)})
+    want_tokens, want_depths = [], []
+    for out in free_run:
+        cut = next((k for k, t in enumerate(out.tokens) if t in eos), len(out.tokens) - 1)
+        want_tokens.append(out.tokens[:cut + 1])
+        want_depths.append(out.exit_depths[:cut])
+    assert sum(len(t) < m for t, m in zip(want_tokens, mnt)) >= 4
+    engine = make_engine(model, synthetic_exit_replay=True, kv_policy="single", delay_gate_consumption=False,
+                         use_async_batching=async_batching, max_num_seqs=6)
+    outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=eos, exit_depths=depths)
+    assert [o.generated_tokens for o in outs] == want_tokens
+    for o, w in zip(outs, want_depths):
+        if async_batching:
+            # A successor staged ahead of its EOS token may already have left the recurrent path
+            # (its exit recorded) before the finish cancels it, as in the reference's eager path.
+            assert o.exit_depths[:len(w)] == w
+            assert len(o.exit_depths) <= len(w) + 1
+        else:
+            assert o.exit_depths == w
+    if async_batching:
+        assert engine.last_stats.cancelled_depth_items > 0

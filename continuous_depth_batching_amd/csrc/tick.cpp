@@ -4,6 +4,8 @@
 //   route_sync      routes one recurrent launch's rows on the synchronous exit
 //                   horizon (cdb/continuous_api.py:1090-1183 with _record_exit
 //                   :1205-1223): exits go to the coda list, the rest step on.
+//   route_delayed   the same on the offset-one horizon, from each row's previous
+//                   launch's decision (cdb/continuous_api.py:1124-1141).
 //   fill_recurrent  writes one launch's packed metadata into the pinned staging
 //                   arrays (cdb/model_runner.py:704-754 assembles the same facts).
 //   BlockPool       the paged cache's block manager: FIFO free list, allocated
@@ -1340,7 +1342,7 @@ PyObject* allocate_if_needed(PyObject*, PyObject* args) {
 // coda-result walk of the engine (cdb/continuous_api.py:1378-1420).
 // ---------------------------------------------------------------------------
 PyObject* g_perf_counter;  // time.perf_counter
-PyObject *s_eos_ids, *s_stop_sequences, *s_first_token_time, *s_name;
+PyObject *s_eos_ids, *s_stop_sequences, *s_first_token_time, *s_name, *s_get;
 
 // Whether the generated tokens end with one of the request's stop sequences.
 int matches_stop_sequence(PyObject* state, PyObject* generated) {
@@ -1532,6 +1534,71 @@ PyObject* coda_upload(PyObject*, PyObject* args) {
   return PyLong_FromLong(next_slot);
 }
 
+// route_delayed(items, flags, max_steps, pending, histogram, backlog) -> (coda_items, refills, exits)
+// Routes one recurrent launch's rows on the offset-one horizon (cdb/continuous_api.py:1124-1141,
+// 1247-1280, 1699-1724): a row leaves at the last step, or when the decision its previous launch made for
+// it says so; pending maps id(item) to that (PendingFlags, row) and is updated with this
+// launch's (flags, row) for every row that steps on. Exits get the same bookkeeping as
+// route_sync; survivors advance one step. The previous launch's flags are read through
+// PendingFlags.get, which waits for them once and keeps them as a list.
+PyObject* route_delayed(PyObject*, PyObject* args) {
+  PyObject *items, *flags, *pending, *hist, *backlog;
+  long max_steps;
+  if (!PyArg_ParseTuple(args, "O!OlO!O!O", &PyList_Type, &items, &flags, &max_steps, &PyDict_Type, &pending,
+                        &PyDict_Type, &hist, &backlog))
+    return nullptr;
+  if (backlog != Py_None && !PyList_Check(backlog)) {
+    PyErr_SetString(PyExc_TypeError, "backlog must be a list or None");
+    return nullptr;
+  }
+  const Py_ssize_t n = PyList_GET_SIZE(items);
+  Ref coda(PyList_New(0)), refills(PyList_New(0)), exits(PyList_New(n));
+  if (!coda || !refills || !exits) return nullptr;
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    Py_INCREF(Py_False);
+    PyList_SET_ITEM(exits.get(), i, Py_False);
+  }
+  for (Py_ssize_t i = 0; i < n; ++i) {
+    PyObject* item = PyList_GET_ITEM(items, i);
+    long step;
+    const int apply = get_truth(item, s_apply_exit_gate);
+    Ref key(PyLong_FromVoidPtr(item));
+    if (apply < 0 || !key || !get_long(item, s_recurrent_step, &step)) return nullptr;
+    // pending.pop(id(item), None)
+    Ref previous(PyDict_GetItemWithError(pending, key.get()));
+    if (previous) {
+      Py_INCREF(previous.get());
+      if (PyDict_DelItem(pending, key.get())) return nullptr;
+    } else if (PyErr_Occurred()) {
+      return nullptr;
+    }
+    int leave = step == max_steps - 1;
+    if (!leave && apply && previous) {
+      if (!PyTuple_Check(previous.get()) || PyTuple_GET_SIZE(previous.get()) != 2) {
+        PyErr_SetString(PyExc_TypeError, "pending entries must be (flags, row) tuples");
+        return nullptr;
+      }
+      Ref decided(PyObject_CallMethodOneArg(PyTuple_GET_ITEM(previous.get(), 0), s_get,
+                                            PyTuple_GET_ITEM(previous.get(), 1)));
+      leave = decided ? PyObject_IsTrue(decided.get()) : -1;
+      if (leave < 0) return nullptr;
+    }
+    if (leave) {
+      Py_INCREF(Py_True);
+      if (PyList_SetItem(exits.get(), i, Py_True) || !record_exit(item, step, apply, hist, backlog, max_steps) ||
+          PyList_Append(coda.get(), item))
+        return nullptr;
+      continue;
+    }
+    Ref row(PyLong_FromSsize_t(i));
+    Ref entry(row ? PyTuple_Pack(2, flags, row.get()) : nullptr);
+    if (!entry || PyDict_SetItem(pending, key.get(), entry.get()) || !set_long(item, s_recurrent_step, step + 1) ||
+        PyList_Append(refills.get(), item))
+      return nullptr;
+  }
+  return Py_BuildValue("(OOO)", coda.get(), refills.get(), exits.get());
+}
+
 PyMethodDef kMethods[] = {
     {"route_sync", route_sync, METH_VARARGS,
      "route_sync(items, flags, max_steps, histogram, backlog) -> (coda_items, refills, exits)"},
@@ -1558,6 +1625,8 @@ PyMethodDef kMethods[] = {
      "update_completion(state, token) -> whether the request finished on this sampled token"},
     {"consume_coda", consume_coda, METH_VARARGS, "consume_coda(items, tokens, eager) -> [(state, stage), ...]"},
     {"add_tokens_in_flight", add_tokens_in_flight, METH_O, "add_tokens_in_flight(items)"},
+    {"route_delayed", route_delayed, METH_VARARGS,
+     "route_delayed(items, flags, max_steps, pending, histogram, backlog) -> (coda_items, refills, exits)"},
     {"coda_upload", coda_upload, METH_VARARGS,
      "coda_upload(items, successors, rows, upload_addr, upload_len, free_slots, next_slot, capacity) -> next_slot"},
     {nullptr, nullptr, 0, nullptr},
@@ -1596,7 +1665,7 @@ PyMODINIT_FUNC PyInit__tick(void) {
       {&s_max_new_tokens, "max_new_tokens"}, {&s_status, "status"}, {&s_popleft, "popleft"},
       {&s_reserve, "reserve"}, {&s_kind_coda, "coda"}, {&s_kind_prefill, "prefill"},
       {&s_kind_recurrent, "recurrent"}, {&s_eos_ids, "_eos_token_ids"}, {&s_stop_sequences, "stop_sequences"},
-      {&s_first_token_time, "first_token_time"}, {&s_name, "name"},
+      {&s_first_token_time, "first_token_time"}, {&s_name, "name"}, {&s_get, "get"},
   };
   for (const Name& nm : names) {
     *nm.slot = PyUnicode_InternFromString(nm.text);

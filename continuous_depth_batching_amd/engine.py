@@ -434,23 +434,12 @@ class ContinuousDepthBatchingEngine:
             if self.record_launches:
                 self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), self.scheduler.refill_events))
             return
-        refills = []
-        exits = []
-        for idx, item in enumerate(items):
-            # Delayed horizon: a launch's decisions route the item after its next launch.
-            step = item.recurrent_step
-            previous = self._pending_flags.pop(id(item), None)
-            should_exit = step == max_steps - 1 or (
-                item.apply_exit_gate and previous is not None and previous[0].get(previous[1]))
-            if not should_exit:
-                self._pending_flags[id(item)] = (flags, idx)
-            exits.append(should_exit)
-            if should_exit:
-                self._record_exit(item, step)
-                self.scheduler.enqueue_coda(item)
-            else:
-                item.recurrent_step = step + 1
-                refills.append(item)
+        # Delayed horizon: a launch's decisions route the item after its next launch (tick core:
+        # the previous launch's flag per row, this launch's flags kept for the survivors).
+        coda_items, refills, exits = _tick.route_delayed(
+            items, flags, max_steps, self._pending_flags, stats.exit_depth_histogram,
+            self._exit_kv_backlog if self.exit_kv_layout is not None else None)
+        self.scheduler.enqueue_coda_items(coda_items)
         if refills:
             self.scheduler.enqueue_depth_front(refills)
         self._flush_exit_kv_copies()

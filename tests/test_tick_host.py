@@ -458,3 +458,64 @@ def test_coda_upload_matches_the_python_staging(seed: int) -> None:
             _tick.coda_upload(items, succ, rows, upload.ctypes.data, upload.size, [], capacity, capacity)
         with pytest.raises(ValueError):
             _tick.coda_upload(items, succ, rows, upload.ctypes.data, 2 * n, [], 0, capacity)
+
+
+def _route_delayed_python(items, flags, max_steps, pending, hist, backlog):
+    coda, refills, exits = [], [], []
+    for idx, item in enumerate(items):
+        step = item.recurrent_step
+        previous = pending.pop(id(item), None)
+        leave = step == max_steps - 1 or (item.apply_exit_gate and previous is not None
+                                          and previous[0].get(previous[1]))
+        if not leave:
+            pending[id(item)] = (flags, idx)
+        exits.append(leave)
+        if leave:
+            if item.apply_exit_gate:
+                item.state.current_token_exit_depth = step
+                item.state.exit_depths.append(step)
+                hist[step] += 1
+            if backlog is not None and step < max_steps - 1:
+                backlog.append((item, step))
+            coda.append(item)
+        else:
+            item.recurrent_step = step + 1
+            refills.append(item)
+    return coda, refills, exits
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("with_backlog", [False, True])
+def test_route_delayed_matches_the_per_row_routing(seed: int, with_backlog: bool) -> None:
+    """Three launches in a row on the offset-one horizon: each row's exit comes from the flag
+    its previous launch wrote, and the pending map carries the survivors' flags forward."""
+
+    import torch
+
+    from continuous_depth_batching_amd.model_runner import PendingFlags
+
+    rng = random.Random(seed)
+    max_steps = 4
+    twins = [_items(random.Random(seed), 24, max_steps) for _ in range(2)]
+    pendings: list[dict] = [{}, {}]
+    hists = [Counter(), Counter()]
+    backlogs = [[], []] if with_backlog else [None, None]
+    for launch in range(3):
+        bits = [rng.random() < 0.4 for _ in range(24)]
+        flags = [PendingFlags(host=torch.tensor(bits, dtype=torch.uint8), event=None) for _ in range(2)]
+        live = [[it for it in items if it.recurrent_step < max_steps] for items in twins]
+        got = _tick.route_delayed(live[0], flags[0], max_steps, pendings[0], hists[0], backlogs[0])
+        want = _route_delayed_python(live[1], flags[1], max_steps, pendings[1], hists[1], backlogs[1])
+        assert [[it.state.request_id for it in part] for part in got[:2]] == \
+               [[it.state.request_id for it in part] for part in want[:2]]
+        assert got[2] == want[2]
+        assert _snapshot(twins[0]) == _snapshot(twins[1])
+        assert hists[0] == hists[1]
+        assert sorted((live[0].index(next(i for i in live[0] if id(i) == k)), v[1]) for k, v in pendings[0].items()) \
+            == sorted((live[1].index(next(i for i in live[1] if id(i) == k)), v[1]) for k, v in pendings[1].items())
+        if with_backlog:
+            assert [(it.state.request_id, s) for it, s in backlogs[0]] == \
+                   [(it.state.request_id, s) for it, s in backlogs[1]]
+        for part in (got[0], want[0]):  # exited rows leave; the rest step on
+            for it in part:
+                it.recurrent_step = max_steps

@@ -123,7 +123,9 @@ class GpuActivity:
 
 
 def time_decode_attention(case, split_pages: int, iters: int) -> dict:
-    """Average duration of one decode-attention call (decode kernel + split merge) on its stream."""
+    """One decode-attention call at the case's shape, as each layer of a recurrent launch makes it:
+    the rows' chunk plan is written once (``plan_ms``, timed on its own), then ``iters`` attend calls
+    (decode kernel + split merge) run from it on their own stream (``ms``)."""
 
     import torch
 
@@ -137,25 +139,30 @@ def time_decode_attention(case, split_pages: int, iters: int) -> dict:
     out = torch.empty_like(case.q)
     stream = torch.cuda.Stream()
 
-    def launch():
+    def launch(stages):
         ops.paged_decode_attention_raw(case.q, case.k_new, case.v_new, view.k_ptr, view.v_ptr, view.layer_stride,
                                        view.num_cache_layers, view.pool_blocks, case.slot_offset, 0,
                                        case.block_table, None, case.seqlens, case.rope_cos, case.rope_sin, 1,
-                                       None, None, out, ws, case.block_size, split_pages, dim ** -0.5)
+                                       None, None, out, ws, case.block_size, split_pages, dim ** -0.5,
+                                       stages=stages)
+
+    def timed(stages, n):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(n):
+            launch(stages)
+        end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) / n
 
     with torch.cuda.stream(stream):
         for _ in range(3):
-            launch()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(iters):
-            launch()
-        end.record(stream)
-    end.synchronize()
-    ms = start.elapsed_time(end) / iters
+            launch(ops.DECODE_PLAN_AND_ATTEND)
+        plan_ms = timed(ops.DECODE_PLAN, iters)
+        ms = timed(ops.DECODE_ATTEND, iters)
     nbytes = case.algorithmic_bytes()
     gbps = nbytes / (ms * 1e-3) / 1e9
-    return {"ms": ms, "bytes": nbytes, "gbps": gbps, "rows": rows, "split_pages": split_pages,
+    return {"ms": ms, "plan_ms": plan_ms, "bytes": nbytes, "gbps": gbps, "rows": rows, "split_pages": split_pages,
             "mean_context": float(case.contexts.mean())}
 
 
@@ -223,127 +230,127 @@ def decode_bytes(positions: np.ndarray, heads: int = 16, kv_heads: int = 16, dim
                + ((p + bs) // bs).sum() * 4)
 
 
-def run_weighted_decode(launches: list[np.ndarray], pool_pages: int = 32768, group: int = 32) -> dict:
+DECODE_LAYERS = 24  # layers of the Ouro-1.4B stack: each recurrent launch plans once and attends 24 times
+
+
+class LayeredDecode:
+    """Decode attention over launches the way the engine's recurrent step runs it: one chunk plan
+    per launch, then one attend per layer, each layer on its own cache layer of a pool of
+    ``DECODE_LAYERS`` layers (so every layer's pages are cold), replayed from captured graphs.
+    Each launch gets a fresh random block table over the pool's pages."""
+
+    def __init__(self, max_rows: int, max_pos: int, pool_pages: int, seed: int) -> None:
+        import torch
+
+        from continuous_depth_batching_amd import ops
+        from continuous_depth_batching_amd.workloads import rope_tables_torch
+
+        dev = torch.device("cuda")
+        self.bs, self.heads, self.dim, self.pool_pages = 16, 16, 128, pool_pages
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.pool = torch.empty((DECODE_LAYERS, 2, pool_pages * self.bs, self.heads, self.dim),
+                                dtype=torch.bfloat16, device=dev)
+        self.pool.normal_(generator=gen)
+        self.view = ops.KVPoolView(self.pool, self.bs)
+        self.q = torch.randn((max_rows, self.heads, self.dim), generator=gen, device=dev).bfloat16()
+        self.kn, self.vn = self.q.clone(), self.q.clone()
+        self.out = torch.empty_like(self.q)
+        self.cos, self.sin = rope_tables_torch(self.dim, 10000.0, max_pos + 1, torch.bfloat16, dev)
+        self.zeros = torch.zeros(max_rows, dtype=torch.int32, device=dev)
+        self.rng = np.random.default_rng(seed + 1)
+        self.dev = dev
+
+    def tensors(self, pos: np.ndarray):
+        import torch
+
+        pages = (pos.astype(np.int64) + self.bs) // self.bs
+        ids = self.rng.choice(self.pool_pages, size=int(pages.sum()), replace=False).astype(np.int32)
+        table = np.full((len(pos), int(pages.max())), -1, np.int32)
+        off = np.concatenate([[0], np.cumsum(pages)])
+        for b in range(len(pos)):
+            table[b, :pages[b]] = ids[off[b]:off[b + 1]]
+        from continuous_depth_batching_amd import ops
+
+        ws = torch.empty(ops.decode_workspace_bytes(len(pos), self.heads, self.dim, int(pos.max()) + 1, self.bs,
+                                                    ops.MIN_SPLIT_PAGES) // 4, dtype=torch.float32, device=self.dev)
+        return (torch.from_numpy(table).to(self.dev), torch.from_numpy(pos.astype(np.int32)).to(self.dev), ws)
+
+    def launch(self, table, seqlens, ws) -> None:
+        from continuous_depth_batching_amd import ops
+
+        n = seqlens.numel()
+        for layer in range(DECODE_LAYERS):
+            ops.paged_decode_attention_raw(
+                self.q[:n], self.kn[:n], self.vn[:n], self.view.k_ptr, self.view.v_ptr, self.view.layer_stride,
+                self.view.num_cache_layers, self.view.pool_blocks, self.zeros[:n], layer, table, None, seqlens,
+                self.cos, self.sin, 1, None, None, self.out[:n], ws, self.bs, ops.ADAPTIVE_SPLIT, self.dim ** -0.5,
+                stages=ops.DECODE_PLAN_AND_ATTEND if layer == 0 else ops.DECODE_ATTEND)
+
+    def time_ms(self, launches: list[np.ndarray]) -> float:
+        """Summed per-layer milliseconds (plan included, 1/24 of it per layer) of ``launches``."""
+
+        tensors = [self.tensors(pos) for pos in launches]
+        state = {"i": 0}
+
+        def call():
+            self.launch(*tensors[state["i"] % len(tensors)])
+            state["i"] += 1
+
+        state["i"] = len(tensors) - 1  # the untimed first call takes the last launch; the capture starts at 0
+        return graph_time_ms(call, len(tensors), reps=1, warm=False) * len(tensors) / DECODE_LAYERS
+
+
+def run_weighted_decode(launches: list[np.ndarray], group: int = 16) -> dict:
     """Decode attention over every recurrent launch of the workload, at each launch's own rows and
-    positions, on a cold pool: every launch gets a fresh random block table over a 4 GiB pool of
-    pages, and launches run in graphs of ``group`` calls (one call per launch, as each of the 24
-    layers of a launch repeats the same call on its own cache layer)."""
+    positions, as the engine runs it (one plan, then 24 layers on cold cache layers): summed
+    algorithmic bytes of one layer pass over summed per-layer time."""
 
     import torch
 
-    from continuous_depth_batching_amd import ops
-    from continuous_depth_batching_amd.workloads import rope_tables_torch
-
-    dev = torch.device("cuda")
-    bs, heads, dim = 16, 16, 128
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(11)
-    pool = torch.empty((1, 2, pool_pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
-    pool.normal_(generator=gen)
-    view = ops.KVPoolView(pool, bs)
-    max_rows = max(len(p) for p in launches)
-    max_pos = max(int(p.max()) for p in launches)
-    q = torch.randn((max_rows, heads, dim), generator=gen, device=dev).bfloat16()
-    kn, vn = q.clone(), q.clone()
-    out = torch.empty_like(q)
-    cos, sin = rope_tables_torch(dim, 10000.0, max_pos + 1, torch.bfloat16, dev)
-    ws = torch.empty(ops.decode_workspace_bytes(max_rows, heads, dim, max_pos + 1, bs, ops.MIN_SPLIT_PAGES) // 4,
-                     dtype=torch.float32, device=dev)
-    zeros = torch.zeros(max_rows, dtype=torch.int32, device=dev)
-    rng = np.random.default_rng(12)
+    bs = 16
+    need = max(int(((p.astype(np.int64) + bs) // bs).sum()) for p in launches)
+    bench = LayeredDecode(max(len(p) for p in launches), max(int(p.max()) for p in launches), need + 64, seed=11)
     total_ms, total_bytes = 0.0, 0
     classes: dict[str, int] = {}
     for g0 in range(0, len(launches), group):
         chunk = launches[g0:g0 + group]
-        tensors = []
-        for pos in chunk:
-            pages = (pos.astype(np.int64) + bs) // bs
-            width = int(pages.max())
-            ids = rng.choice(pool_pages, size=int(pages.sum()), replace=False).astype(np.int32)
-            table = np.full((len(pos), width), -1, np.int32)
-            off = np.concatenate([[0], np.cumsum(pages)])
-            for b in range(len(pos)):
-                table[b, :pages[b]] = ids[off[b]:off[b + 1]]
-            tensors.append((torch.from_numpy(table).to(dev), torch.from_numpy(pos.astype(np.int32)).to(dev)))
-        state = {"i": 0}
-
-        def call():
-            table, seqlens = tensors[state["i"] % len(tensors)]
-            n = seqlens.numel()
-            ops.paged_decode_attention_raw(q[:n], kn[:n], vn[:n], view.k_ptr, view.v_ptr, view.layer_stride,
-                                           view.num_cache_layers, view.pool_blocks, zeros[:n], 0, table, None,
-                                           seqlens, cos, sin, 1, None, None, out[:n], ws, bs, ops.ADAPTIVE_SPLIT,
-                                           dim ** -0.5)
-            state["i"] += 1
-
-        state["i"] = len(tensors) - 1  # the untimed first call takes the last launch; the capture starts at 0
-        total_ms += graph_time_ms(call, len(tensors), reps=1, warm=False) * len(tensors)
+        total_ms += bench.time_ms(chunk)
         for pos in chunk:
             n = len(pos)
             key = "1-16" if n <= 16 else "17-64" if n <= 64 else "65-128" if n <= 128 else "129-256"
             classes[key] = classes.get(key, 0) + 1
             total_bytes += decode_bytes(pos)
-    del pool, ws
+    del bench
     torch.cuda.empty_cache()
     gbps = total_bytes / (total_ms * 1e-3) / 1e9
     return {"launches": len(launches), "ms": round(total_ms, 2), "bytes": total_bytes, "GBps": round(gbps, 1),
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "launches_by_rows": dict(sorted(classes.items())),
-            "note": "every recurrent launch of one generate_batch of the workload, one decode-attention call each, "
-                    "cold random block tables over a 4 GiB page pool, timed from captured graphs"}
+            "note": "every recurrent launch of one generate_batch of the workload, as the recurrent step runs it: "
+                    "one chunk plan, then decode attention on each of 24 cache layers (cold pages, a random block "
+                    "table per launch); per-layer time includes 1/24 of the plan; captured graphs"}
 
 
-def time_by_rows(positions_by_rows: dict[int, np.ndarray], pool_pages: int = 32768, calls: int = 24) -> dict:
-    """Decode attention at fixed launch widths, each from a graph of ``calls`` calls that cycle
-    through cold block tables (one per call), reported per width."""
+def time_by_rows(positions_by_rows: dict[int, np.ndarray], launches_per_width: int = 4) -> dict:
+    """Decode attention at fixed launch widths, as the recurrent step runs it (one plan, 24 cold
+    cache layers), per layer, for ``launches_per_width`` launches with fresh block tables."""
 
     import torch
 
-    from continuous_depth_batching_amd import ops
-    from continuous_depth_batching_amd.workloads import rope_tables_torch
-
-    dev = torch.device("cuda")
-    bs, heads, dim = 16, 16, 128
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(13)
-    pool = torch.empty((1, 2, pool_pages * bs, heads, dim), dtype=torch.bfloat16, device=dev)
-    pool.normal_(generator=gen)
-    view = ops.KVPoolView(pool, bs)
-    rng = np.random.default_rng(14)
+    bs = 16
+    need = max(int(((p.astype(np.int64) + bs) // bs).sum()) for p in positions_by_rows.values())
+    bench = LayeredDecode(max(positions_by_rows), max(int(p.max()) for p in positions_by_rows.values()),
+                          need + 64, seed=13)
     results = {}
     for rows, pos in positions_by_rows.items():
         pos = pos.astype(np.int32)
-        pages = (pos.astype(np.int64) + bs) // bs
-        q = torch.randn((rows, heads, dim), generator=gen, device=dev).bfloat16()
-        out = torch.empty_like(q)
-        cos, sin = rope_tables_torch(dim, 10000.0, int(pos.max()) + 1, torch.bfloat16, dev)
-        ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(pos.max()) + 1, bs, ops.MIN_SPLIT_PAGES)
-                         // 4, dtype=torch.float32, device=dev)
-        seqlens = torch.from_numpy(pos).to(dev)
-        zeros = torch.zeros(rows, dtype=torch.int32, device=dev)
-        tables = []
-        for _ in range(calls):
-            ids = rng.choice(pool_pages, size=int(pages.sum()), replace=False).astype(np.int32)
-            table = np.full((rows, int(pages.max())), -1, np.int32)
-            off = np.concatenate([[0], np.cumsum(pages)])
-            for b in range(rows):
-                table[b, :pages[b]] = ids[off[b]:off[b + 1]]
-            tables.append(torch.from_numpy(table).to(dev))
-        state = {"i": 0}
-
-        def call():
-            table = tables[state["i"] % calls]
-            state["i"] += 1
-            ops.paged_decode_attention_raw(q, q, q, view.k_ptr, view.v_ptr, view.layer_stride, view.num_cache_layers,
-                                           view.pool_blocks, zeros, 0, table, None, seqlens, cos, sin, 1, None,
-                                           None, out, ws, bs, ops.ADAPTIVE_SPLIT, dim ** -0.5)
-
-        ms = graph_time_ms(call, calls, reps=1, warm=False)
+        ms = bench.time_ms([pos] * launches_per_width) / launches_per_width
         nbytes = decode_bytes(pos)
         results[str(rows)] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
                               "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                               "mean_context": round(float(pos.mean()) + 1, 1)}
-    del pool
+    del bench
     torch.cuda.empty_cache()
     return results
 
@@ -919,8 +926,10 @@ def main() -> int:
                 "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(attention["bytes"]),
                 "traffic_source": f"{TRAFFIC_RECORD}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this shape, "
                                   "scaled by a 1 GiB copy",
-                "kernel": "cdb::paged_decode_kernel<bf16,128> + decode_merge_kernel",
+                "kernel": "cdb::paged_decode_fast_kernel<bf16,128> + decode_merge_kernel (one layer's attend)",
                 "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
+                "plan_ms": round(attention["plan_ms"], 4),
+                "plan_note": "cdb::decode_plan_kernel runs once per recurrent launch for all 24 layers",
                 "shape": f"{attention['rows']} rows x 16 heads x 128, mean context {attention['mean_context']:.0f}"}
     micro = None
     if not args.no_microbench:

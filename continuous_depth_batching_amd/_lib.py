@@ -25,6 +25,8 @@ CDB_ERRORS = {
 CDB_DTYPE_F32 = 0
 CDB_DTYPE_BF16 = 1
 CDB_DECODE_SCRATCH_BYTES = 16 << 20  # include/cdb_amd.h
+CDB_DECODE_STAGE_PLAN = 1
+CDB_DECODE_STAGE_ATTEND = 2
 
 _P = c_void_p
 _I32P = c_void_p
@@ -46,6 +48,22 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
             c_int32, c_int32,  # min/max split pages (split_pages <= 0)
             c_float, c_int64, c_int64, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stream
+        ],
+    ),
+    "cdb_paged_decode_attention_staged": (
+        c_int32,
+        [
+            _P, _P, _P, _P, _P,  # q, k_new, v_new, k_pool, v_pool
+            c_int64, c_int32, c_int64,  # layer_stride, num_cache_layers, pool_blocks
+            _I32P, c_int32,  # cache_layer, cache_layer0
+            _I32P, _I32P, c_int32,  # block_table, table_row, table_width
+            _I32P,  # seqlens
+            _P, _P, c_int32, c_int32,  # rope_cos, rope_sin, rope_style, max_positions
+            _P, _P,  # q_bias, k_bias
+            _P, _P, c_int64,  # out, workspace, workspace_bytes
+            c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
+            c_int32,  # min_split_pages (split_pages <= 0)
+            c_float, c_int64, c_int64, c_int32, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stages, stream
         ],
     ),
     "cdb_paged_decode_attention_noalloc": (

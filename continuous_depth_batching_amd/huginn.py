@@ -371,14 +371,17 @@ class HuginnCDBAdapter(CDBModelAdapter):
         """Paged decode attention at the rows' positions; ``layer_of(i)`` gives (per-row offsets, base)."""
 
         cache = launch_like.cache
+        planned = [False]  # every layer of this launch serves the same rows: the first one plans their chunks
 
         def attend(i: int, w: dict, qkv: torch.Tensor) -> torch.Tensor:
             q, k, v = self._split_qkv(qkv)
             per_row, base = layer_of(i)
+            stages = ops.DECODE_ATTEND if planned[0] else ops.DECODE_PLAN_AND_ATTEND
+            planned[0] = True
             return torch.ops.cdb.paged_decode_attention(
                 q, k, v, cache.pool, per_row, base, cache.device_table, launch_like.table_rows,
                 launch_like.positions, self.rope_cos, self.rope_sin, ROPE_INTERLEAVED, w["q_bias"], w["k_bias"],
-                launch_like.workspace, cache.block_size, launch_like.split_pages, self.scale)
+                launch_like.workspace, cache.block_size, launch_like.split_pages, self.scale, stages)
 
         return attend
 

@@ -19,21 +19,24 @@ from . import _lib
 
 _DTYPE_CODES = {torch.float32: _lib.CDB_DTYPE_F32, torch.bfloat16: _lib.CDB_DTYPE_BF16}
 
-# Decode-attention KV split length in pages: ADAPTIVE_SPLIT lets every launch pick a
-# power of two in [MIN_SPLIT_PAGES, MAX_SPLIT_PAGES] from its own page count; a
-# negative value -m does the same with m as the lower bound.
+# Decode-attention KV chunk length in pages: ADAPTIVE_SPLIT uses MIN_SPLIT_PAGES (a
+# negative value -m uses m). Chunks are lengthened only when the workspace cannot
+# hold a launch's chunks. MAX_SPLIT_PAGES is passed where the C ABI still takes it.
 ADAPTIVE_SPLIT = 0
 MIN_SPLIT_PAGES = 8
 MAX_SPLIT_PAGES = 32
+
+# Stages of cdb_paged_decode_attention_staged (include/cdb_amd.h).
+DECODE_PLAN = _lib.CDB_DECODE_STAGE_PLAN
+DECODE_ATTEND = _lib.CDB_DECODE_STAGE_ATTEND
+DECODE_PLAN_AND_ATTEND = DECODE_PLAN | DECODE_ATTEND
 
 
 def decode_split_pages(rows: int) -> int:
     """The split_pages argument a decode launch of `rows` rows passes.
 
-    Always the adaptive default. A smaller lower bound for small launches was
-    measured (one 1193-token row: 17.4 -> 14.3 us) but makes a row's split -- and
-    so its rounding -- depend on the size of the launch it lands in; with one
-    bound for every launch, rows whose context stays under the bound compute
+    Always the default chunk length: a row's chunks, and so its rounding, then do
+    not depend on the size of the launch it lands in, and rows compute
     identically in any batch composition."""
 
     return ADAPTIVE_SPLIT
@@ -144,10 +147,14 @@ def paged_decode_attention_raw(
     scale: float,
     min_split_pages: int = MIN_SPLIT_PAGES,
     max_split_pages: int = MAX_SPLIT_PAGES,
+    stages: int = DECODE_PLAN_AND_ATTEND,
 ) -> torch.Tensor:
     """Launch ``cdb_paged_decode_attention`` on explicit pool pointers (no allocation).
 
-    ``split_pages <= 0`` lets the kernel size the splits within [min, max] pages.
+    ``split_pages <= 0`` uses chunks of ``min_split_pages`` pages. ``stages`` other
+    than plan-and-attend goes through ``cdb_paged_decode_attention_staged``: a
+    caller that runs the same rows (positions, table rows, cache-layer offsets)
+    through several layers plans at the first and attends at every layer.
     """
 
     num_rows, num_heads, head_dim = q.shape
@@ -183,20 +190,22 @@ def paged_decode_attention_raw(
     _require_contiguous(block_table=block_table, seqlens=seqlens, out=out, rope_cos=rope_cos, rope_sin=rope_sin,
                         q_bias=q_bias, k_bias=k_bias)
     _require_int32(cache_layer=cache_layer, block_table=block_table, table_row=table_row, seqlens=seqlens)
-    code = _lib.lib().cdb_paged_decode_attention(
-        q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_pool_ptr, v_pool_ptr,
-        layer_stride, num_cache_layers, pool_blocks,
-        _ptr(cache_layer), cache_layer0,
-        block_table.data_ptr(), _ptr(table_row), block_table.shape[1],
-        seqlens.data_ptr(),
-        _ptr(rope_cos), _ptr(rope_sin), rope_style, 0 if rope_cos is None else rope_cos.shape[0],
-        _ptr(q_bias), _ptr(k_bias),
-        out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4,
-        num_rows, num_heads, num_kv_heads, head_dim, block_size, split_pages,
-        min_split_pages, max_split_pages,
-        scale, q.stride(0), k_new.stride(0), dtype_code(q.dtype), _stream(),
-    )
-    _lib.check(code, "cdb_paged_decode_attention")
+    head = (q.data_ptr(), k_new.data_ptr(), v_new.data_ptr(), k_pool_ptr, v_pool_ptr,
+            layer_stride, num_cache_layers, pool_blocks,
+            _ptr(cache_layer), cache_layer0,
+            block_table.data_ptr(), _ptr(table_row), block_table.shape[1],
+            seqlens.data_ptr(),
+            _ptr(rope_cos), _ptr(rope_sin), rope_style, 0 if rope_cos is None else rope_cos.shape[0],
+            _ptr(q_bias), _ptr(k_bias),
+            out.data_ptr(), workspace.data_ptr(), workspace.numel() * 4,
+            num_rows, num_heads, num_kv_heads, head_dim, block_size, split_pages, min_split_pages)
+    tail = (scale, q.stride(0), k_new.stride(0), dtype_code(q.dtype))
+    if stages == DECODE_PLAN_AND_ATTEND:
+        code = _lib.lib().cdb_paged_decode_attention(*head, max_split_pages, *tail, _stream())
+        _lib.check(code, "cdb_paged_decode_attention")
+    else:
+        code = _lib.lib().cdb_paged_decode_attention_staged(*head, *tail, stages, _stream())
+        _lib.check(code, "cdb_paged_decode_attention_staged")
     return out
 
 
@@ -221,11 +230,13 @@ def paged_decode_attention(
     block_size: int,
     split_pages: int,
     scale: float,
+    stages: int = DECODE_PLAN_AND_ATTEND,
 ) -> torch.Tensor:
     """Mixed-depth paged decode attention with fused RoPE + KV append over ``kv_pool``.
 
     ``kv_pool`` is ``[num_cache_layers, 2, pool_blocks * block_size, Hkv, D]`` (keys at
     index 0 of dim 1, values at 1) and is updated in place at each row's position.
+    ``stages`` as in ``paged_decode_attention_raw``.
     """
 
     if kv_pool.dim() != 5 or kv_pool.shape[1] != 2 or not kv_pool.is_contiguous():
@@ -239,12 +250,13 @@ def paged_decode_attention(
         q, k_new, v_new, view.k_ptr, view.v_ptr, view.layer_stride, view.num_cache_layers, view.pool_blocks,
         cache_layer, cache_layer0, block_table, table_row, seqlens, rope_cos, rope_sin, rope_style,
         q_bias, k_bias, out, workspace, block_size, max(split_pages, 0), scale, min_split_pages=min_split,
+        stages=stages,
     )
 
 
 @paged_decode_attention.register_fake
 def _(q, k_new, v_new, kv_pool, cache_layer, cache_layer0, block_table, table_row, seqlens, rope_cos, rope_sin,
-      rope_style, q_bias, k_bias, workspace, block_size, split_pages, scale):
+      rope_style, q_bias, k_bias, workspace, block_size, split_pages, scale, stages=DECODE_PLAN_AND_ATTEND):
     return torch.empty_like(q)
 
 

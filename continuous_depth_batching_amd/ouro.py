@@ -324,10 +324,12 @@ class OuroCDBAdapter(CDBModelAdapter):
             q = qkv[:, :q_w].view(rows, self.num_heads, hd)
             k = qkv[:, q_w:q_w + kv_w].view(rows, self.num_kv_heads, hd)
             v = qkv[:, q_w + kv_w:].view(rows, self.num_kv_heads, hd)
+            # Every layer serves the same rows: the first one plans their chunks.
             return torch.ops.cdb.paged_decode_attention(
                 q, k, v, cache.pool, launch.slot_offset, li, cache.device_table, launch.table_rows,
                 launch.positions, self.rope_cos, self.rope_sin, 1, None, None, launch.workspace,
-                cache.block_size, launch.split_pages, self.scale)
+                cache.block_size, launch.split_pages, self.scale,
+                ops.DECODE_PLAN_AND_ATTEND if li == 0 else ops.DECODE_ATTEND)
 
         hidden = self._layer_stack(x, residual, attend)
         torch.ops.cdb.scatter_rows_(launch.bank, launch.bank_slots, hidden)

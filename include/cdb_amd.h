@@ -36,10 +36,13 @@ enum {
 enum { CDB_DTYPE_F32 = 0, CDB_DTYPE_BF16 = 1 };
 
 /* Bytes of decode workspace for num_rows rows whose new-token positions are
- * all < max_seqlen when splits are at least split_pages pages long: a
- * 256-byte-aligned int32 header of num_rows + 2 entries, then fp32 split
- * partials. A smaller workspace (but not smaller than the header) is legal: the
- * kernel then lengthens splits until they fit. Returns -1 on bad input. */
+ * all < max_seqlen with chunks of split_pages pages: an int32 header of
+ * num_rows + 2 entries padded to 256 bytes and 1 KiB of work-queue counters
+ * (kept at zero between calls by the kernels themselves), then per chunk a
+ * 64-byte descriptor and an
+ * fp32 partial of num_heads * (head_dim + 2) floats. A smaller workspace is
+ * legal as long as it holds the header and one chunk per row: the plan then
+ * lengthens the chunks until they fit. Returns -1 on bad input. */
 int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, int32_t head_dim, int32_t max_seqlen,
                                          int32_t block_size, int32_t split_pages);
 
@@ -67,11 +70,13 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
  * q_stride / kv_stride: elements between consecutive rows of q and of
  * k_new/v_new (0 = dense), so q, k and v may be column slices of one fused
  * QKV projection output.
- * Context is split into chunks of split_pages pages processed in parallel; with
- * split_pages <= 0 the kernel picks a power of two in [min_split_pages,
- * max_split_pages] from the launch's total pages so the work fills the GPU.
- * Rows with several chunks are merged by a second kernel on the same stream.
- * Returns CDB_ERR_CAPACITY when workspace_bytes cannot hold the header. */
+ * Each row's context is cut into chunks of split_pages pages (min_split_pages
+ * when split_pages <= 0; max_split_pages is not used and kept for the ABI),
+ * processed in parallel and merged in chunk order, so a row's output does not
+ * depend on which other rows share the launch. Only a workspace too small for
+ * the launch's chunks lengthens them.
+ * Returns CDB_ERR_CAPACITY when workspace_bytes cannot hold the header and one
+ * chunk per row. */
 int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
                                int64_t layer_stride, int32_t num_cache_layers, int64_t pool_blocks,
                                const int32_t* cache_layer, int32_t cache_layer0, const int32_t* block_table,
@@ -83,6 +88,31 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t min_split_pages, int32_t max_split_pages, float scale,
                                int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
 
+/* Stages of cdb_paged_decode_attention_staged. */
+enum { CDB_DECODE_STAGE_PLAN = 1, CDB_DECODE_STAGE_ATTEND = 2 };
+
+/* cdb_paged_decode_attention in two stages, for a batch whose rows run through
+ * several layers with the same positions (seqlens), table rows (table_row) and
+ * cache-layer offsets (cache_layer), as the reference's recurrent stage runs its
+ * rows through every layer of the loop block (continuous_api.py:1171-1183,
+ * ouro/modeling_ouro.py:407-428). CDB_DECODE_STAGE_PLAN writes the chunk plan
+ * of those rows into the workspace; CDB_DECODE_STAGE_ATTEND runs attention and
+ * the merge from the plan last written to this workspace, which must describe
+ * the same rows (only cache_layer0, q/k/v, the pools and out may differ).
+ * stages = PLAN | ATTEND is cdb_paged_decode_attention. Arguments and errors as
+ * cdb_paged_decode_attention; CDB_ERR_SHAPE for any other stages value. */
+int cdb_paged_decode_attention_staged(const void* q, const void* k_new, const void* v_new, void* k_pool,
+                                      void* v_pool, int64_t layer_stride, int32_t num_cache_layers,
+                                      int64_t pool_blocks, const int32_t* cache_layer, int32_t cache_layer0,
+                                      const int32_t* block_table, const int32_t* table_row, int32_t table_width,
+                                      const int32_t* seqlens, const float* rope_cos, const float* rope_sin,
+                                      int32_t rope_style, int32_t max_positions, const void* q_bias,
+                                      const void* k_bias, void* out, void* workspace, int64_t workspace_bytes,
+                                      int32_t num_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t block_size, int32_t split_pages, int32_t min_split_pages, float scale,
+                                      int64_t q_stride, int64_t kv_stride, int32_t dtype, int32_t stages,
+                                      hipStream_t stream);
+
 /* No counterpart in the reference. cdb_paged_decode_attention for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc. Same arguments and results without the workspace: the split header and partials
@@ -91,8 +121,9 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
  * scratch must start at zero: each call writes its header and partials before reading them.
  * Every call on one GPU shares that GPU's array, so calls that overlap on one GPU (two streams,
  * or two threads) race; serialize them. Returns CDB_ERR_CAPACITY when the header plus one
- * partial per row, num_rows * num_heads * (head_dim + 2) floats, exceeds the scratch (at
- * 16 heads x 128: more than 2000 rows); a smaller surplus only lengthens the splits. */
+ * chunk per row (a 64-byte descriptor and num_heads * (head_dim + 2) floats) exceeds the
+ * scratch (at 16 heads x 128: more than 2000 rows); a smaller surplus only lengthens the
+ * chunks. */
 #define CDB_DECODE_SCRATCH_BYTES ((int64_t)16 << 20)
 int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const void* v_new, void* k_pool,
                                        void* v_pool, int64_t layer_stride, int32_t num_cache_layers,

@@ -40,10 +40,12 @@ def test_binding_covers_every_declared_symbol() -> None:
 
 def test_workspace_size_query_without_gpu() -> None:
     lib = _lib.lib()
-    # A 256-byte header (split size + split prefix of 4 rows), then ceil(100 / 32) + 1 splits
-    # per row of (D + 2) floats per head.
-    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 256 + 4 * 5 * 16 * 130 * 4
-    assert lib.cdb_paged_decode_workspace_bytes(100, 16, 128, 100, 16, 2) == 512 + 100 * 5 * 16 * 130 * 4
+    # A header (chunk size + chunk prefix of the rows, padded to 256 bytes, then 1 KiB of item-queue
+    # counters), then ceil(100 / 32) + 1 chunks per row, each a 64-byte descriptor and (D + 2) floats
+    # per head.
+    per_chunk = 64 + 16 * 130 * 4
+    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 256 + 1024 + 4 * 5 * per_chunk
+    assert lib.cdb_paged_decode_workspace_bytes(100, 16, 128, 100, 16, 2) == 512 + 1024 + 100 * 5 * per_chunk
     assert lib.cdb_paged_decode_workspace_bytes(-1, 16, 128, 100, 16, 2) == -1
 
 
@@ -71,14 +73,35 @@ def test_decode_argument_errors_without_gpu() -> None:
     assert call(num_rows=0) == _lib.CDB_OK
     assert call(q=None) == _lib.CDB_ERR_NULL
     assert call(workspace=None) == _lib.CDB_ERR_NULL
-    assert call(workspace_bytes=255) == _lib.CDB_ERR_CAPACITY  # smaller than the split header
+    assert call(workspace_bytes=255) == _lib.CDB_ERR_CAPACITY  # smaller than the chunk header
+    per_chunk = 64 + 16 * 130 * 4
+    assert call(workspace_bytes=1280 + 3 * per_chunk) == _lib.CDB_ERR_CAPACITY  # 3 chunks for 4 rows
     assert call(block_size=24) == _lib.CDB_ERR_SHAPE
     assert call(num_kv_heads=5) == _lib.CDB_ERR_SHAPE
-    assert call(min_split_pages=3) == _lib.CDB_ERR_SHAPE
+    assert call(min_split_pages=0) == _lib.CDB_ERR_SHAPE
     assert call(head_dim=80) == _lib.CDB_ERR_UNSUPPORTED
     assert call(dtype=7) == _lib.CDB_ERR_UNSUPPORTED
     assert call(rope_cos=None) == _lib.CDB_ERR_NULL
     assert call(q_stride=100) == _lib.CDB_ERR_SHAPE
+
+
+def test_staged_decode_argument_errors_without_gpu() -> None:
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("runs only where no device exists: the stand-in addresses must never reach a kernel")
+    lib = _lib.lib()
+
+    def call(stages, **kw):
+        args = _decode_args(**kw)
+        del args[30]  # max_split_pages: the staged entry does not take it
+        return lib.cdb_paged_decode_attention_staged(*args[:-1], stages, args[-1])
+
+    assert call(_lib.CDB_DECODE_STAGE_PLAN, num_rows=0) == _lib.CDB_OK
+    for bad in (0, 4, -1, 7):
+        assert call(bad) == _lib.CDB_ERR_SHAPE
+    assert call(_lib.CDB_DECODE_STAGE_ATTEND, q=None) == _lib.CDB_ERR_NULL
+    assert call(_lib.CDB_DECODE_STAGE_PLAN, workspace_bytes=255) == _lib.CDB_ERR_CAPACITY
 
 
 def test_table_update_argument_errors_without_gpu() -> None:

@@ -167,3 +167,69 @@ def test_out_of_range_row_is_flagged_nan_and_writes_nothing() -> None:
     want, want_pool = run_oracle(case)
     np.testing.assert_allclose(got[ok], want[ok], atol=2e-5)
     np.testing.assert_array_equal(got_pool, want_pool)
+
+
+def _device_case(case):
+    from continuous_depth_batching_amd import ops
+
+    dev = torch.device("cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    dt = TORCH_DTYPE[case.dtype]
+    pool = t(case.kv_pool).to(dt).contiguous()
+    tensors = dict(q=t(case.q).to(dt), k=t(case.k_new).to(dt), v=t(case.v_new).to(dt), pool=pool,
+                   layer=t(case.cache_layer), table=t(case.block_table), seqlens=t(case.seqlens),
+                   cos=t(case.rope[0]), sin=t(case.rope[1]))
+    rows, heads, dim = case.q.shape
+    ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(case.seqlens.max()) + 1, case.block_size,
+                                                ops.MIN_SPLIT_PAGES) // 4, dtype=torch.float32, device=dev)
+    return tensors, ws
+
+
+def _attend(case, d, ws, rows, cache_layer0=0, stages=None):
+    """Decode attention over the batch rows `rows` (indices into the case) through table_row."""
+    from continuous_depth_batching_amd import ops
+
+    idx = torch.as_tensor(rows, dtype=torch.long, device="cuda")
+    view = ops.KVPoolView(d["pool"], case.block_size)
+    q, k, v = d["q"][idx].contiguous(), d["k"][idx].contiguous(), d["v"][idx].contiguous()
+    out = torch.empty_like(q)
+    ops.paged_decode_attention_raw(
+        q, k, v, view.k_ptr, view.v_ptr, view.layer_stride, view.num_cache_layers, view.pool_blocks,
+        d["layer"][idx].contiguous(), cache_layer0, d["table"], idx.to(torch.int32), d["seqlens"][idx].contiguous(),
+        d["cos"], d["sin"], case.rope_style, None, None, out, ws, case.block_size, ops.ADAPTIVE_SPLIT, case.scale,
+        **({} if stages is None else {"stages": stages}))
+    return out
+
+
+def test_row_output_is_bit_identical_in_any_batch_composition() -> None:
+    # A row's chunks and their merge order depend only on the row: alone, inside the
+    # full batch, or inside a shuffled half of it, its output is the same to the bit.
+    case = make_case(seed=31, num_rows=96, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1500,
+                     rope_style=1, dtype="bf16", padding_rows=3)
+    d, ws = _device_case(case)
+    full = _attend(case, d, ws, list(range(96)))
+    rng = np.random.default_rng(3)
+    half = rng.permutation(96)[:48].tolist()
+    sub = _attend(case, d, ws, half)
+    torch.cuda.synchronize()
+    assert torch.equal(sub, full[half])
+    for r in (0, int(np.argmax(case.seqlens)), 50):
+        alone = _attend(case, d, ws, [r])
+        assert torch.equal(alone[0], full[r])
+
+
+def test_plan_once_then_attend_per_layer_matches_planning_every_layer() -> None:
+    from continuous_depth_batching_amd import ops
+
+    case = make_case(seed=32, num_rows=40, num_heads=16, num_kv_heads=16, head_dim=128, max_context=900,
+                     rope_style=1, dtype="bf16", num_layers=6)
+    d, ws = _device_case(case)
+    d["layer"] = d["layer"] % 4  # offsets 0..3 over 6 cache layers: bases 0, 1 and 2 are all in range
+    rows = list(range(40))
+    staged = [_attend(case, d, ws, rows, layer, ops.DECODE_PLAN_AND_ATTEND if layer == 0 else ops.DECODE_ATTEND)
+              for layer in (0, 1, 2)]
+    fresh = [_attend(case, d, ws, rows, layer) for layer in (0, 1, 2)]
+    torch.cuda.synchronize()
+    for a, b in zip(staged, fresh):
+        assert torch.equal(a, b)
+    assert not torch.equal(staged[0], staged[1])  # the layers really differ

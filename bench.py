@@ -455,6 +455,8 @@ def measured_traffic(algorithmic_bytes: int) -> int | None:
     record = json.loads(path.read_text())
     if int(record.get("algorithmic_bytes_per_call", -1)) != int(algorithmic_bytes):
         return None
+    if not str(record.get("kernels", "")).startswith("paged_decode_fast_kernel"):
+        return None  # counted on another form of the kernel
     return int(record["traffic_bytes_per_call"])
 
 

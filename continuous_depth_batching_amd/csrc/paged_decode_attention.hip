@@ -45,6 +45,7 @@
 // bytes, then int32 descriptors [capacity][8], then fp32 partials
 // [capacity, H, D + 2] (unnormalized accumulator, running max, running sum).
 
+#include <algorithm>
 #include <mutex>
 #include <utility>
 #include <vector>
@@ -183,6 +184,8 @@ CDB_DEVICE int length_key(int tokens) { return min((tokens + 31) >> 5, kLengthKe
 
 __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(DecodeParams P) {
   __shared__ int row_pos[kMaxRowsLds];           // position, or -1 for a row without chunks
+  __shared__ int row_trow[kMaxRowsLds];          // block-table row
+  __shared__ int row_layer[kMaxRowsLds];         // cache-layer offset
   __shared__ int chunk_prefix[kMaxRowsLds + 1];  // chunks of rows before b (partial slots)
   __shared__ int full_prefix[kMaxRowsLds + 1];   // full chunks of rows before b
   __shared__ int key_next[kLengthKeys];          // next free descriptor of each last-chunk length
@@ -195,6 +198,8 @@ __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(DecodeParams 
     const int p = P.seqlens[b];
     const int trow = P.table_row ? P.table_row[b] : b;
     row_pos[b] = position_in_range(P, p) && trow >= 0 ? p : -1;
+    row_trow[b] = trow;
+    row_layer[b] = P.cache_layer ? P.cache_layer[b] : 0;
   }
   if (tid < kLengthKeys) key_next[tid] = 0;
   __syncthreads();
@@ -245,8 +250,8 @@ __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(DecodeParams 
     const int b = lo;
     const int p = row_pos[b];
     const int n = chunk_prefix[b + 1] - chunk_prefix[b];
-    const int trow = P.table_row ? P.table_row[b] : b;
-    const int layer = P.cache_layer ? P.cache_layer[b] : 0;
+    const int trow = row_trow[b];
+    const int layer = row_layer[b];
     {
       const int c = ci - chunk_prefix[b];
       const bool last = c == n - 1;
@@ -526,7 +531,7 @@ CDB_DEVICE float score(const QueryReg<T, D>& q, float scale_log2, const Vec<T, D
 // v_perm.
 template <typename T, int D>
 CDB_DEVICE void attend_step(const QueryReg<T, D>& q, float scale_log2, const Vec<T, D / 16> (&kv)[4],
-                            const Vec<T, D / 16> (&vv)[4], const bool (&valid)[4], float& m, float& l, float* acc) {
+                            Vec<T, D / 16> (&vv)[4], const bool (&valid)[4], float& m, float& l, float* acc) {
   constexpr int C = D / 16;
   constexpr bool kBf16 = sizeof(T) == 2;
   float sc[4];
@@ -537,12 +542,12 @@ CDB_DEVICE void attend_step(const QueryReg<T, D>& q, float scale_log2, const Vec
   }
   const float m_new = fmaxf(m, fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
   if (m_new == -INFINITY) return;
-  // A masked token's value words are zeroed, so its zero weight never meets a NaN.
-  uint32_t vw[4][Vec<T, C>::kWords];
+  // A masked token's value words are zeroed (in place: the buffer is consumed
+  // here), so its zero weight never meets a NaN.
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
 #pragma unroll
-    for (int w = 0; w < Vec<T, C>::kWords; ++w) vw[u][w] = valid[u] ? vv[u].w[w] : 0u;
+    for (int w = 0; w < Vec<T, C>::kWords; ++w) vv[u].w[w] = valid[u] ? vv[u].w[w] : 0u;
   }
   const float alpha = exp2f(m - m_new);
   l *= alpha;
@@ -556,7 +561,7 @@ CDB_DEVICE void attend_step(const QueryReg<T, D>& q, float scale_log2, const Vec
       const uint32_t pk = pack_bf16x2(p0, p1);
 #pragma unroll
       for (int w = 0; w < C / 2; ++w) {
-        const uint32_t a = vw[u][w], b = vw[u + 1][w];
+        const uint32_t a = vv[u].w[w], b = vv[u + 1].w[w];
         acc[2 * w] = dot2_bf16(pk, __builtin_amdgcn_perm(b, a, 0x05040100u), acc[2 * w]);       // (a.lo, b.lo)
         acc[2 * w + 1] = dot2_bf16(pk, __builtin_amdgcn_perm(b, a, 0x07060302u), acc[2 * w + 1]);  // (a.hi, b.hi)
       }
@@ -567,7 +572,7 @@ CDB_DEVICE void attend_step(const QueryReg<T, D>& q, float scale_log2, const Vec
       const float pu = exp2f(sc[u] - m_new);
       l += pu;
 #pragma unroll
-      for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, __uint_as_float(vw[u][i]), acc[i]);
+      for (int i = 0; i < C; ++i) acc[i] = fmaf(pu, __uint_as_float(vv[u].w[i]), acc[i]);
     }
   }
   m = m_new;
@@ -1094,34 +1099,13 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
   }
 }
 
-// Merge the chunk partials of every (row, head) whose row has more than one
-// chunk, in chunk order; one wave per (row, head). Rows without chunks get zeros
-// (padding rows) or NaN (rows out of range), and multi-chunk rows whose cache
-// layer is missing get NaN. Lane s holds chunk s's (max, sum) so the global max
-// and the denominator are wave reductions; the accumulators are read eight
-// chunks at a time so their loads are in flight together.
+// The merge of one (row, head): chunk c's partial (unnormalized accumulator of
+// D floats, then its max and sum) starts at part + c * stride. Lane s holds
+// chunk s's (max, sum) so the global max and the denominator are wave
+// reductions; the accumulators are read eight chunks at a time so their loads
+// are in flight together.
 template <typename T, int D>
-__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
-  const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  // The decode kernel before this one has drained the item queues: reset them for the next call.
-  if (blockIdx.x == 0 && threadIdx.x < kQueues) P.counters[threadIdx.x * kCounterStride] = 0;
-  if (w >= P.num_rows * P.num_heads) return;
-  const int b = w / P.num_heads;
-  const int h = w - b * P.num_heads;
-  const int first = P.header[1 + b];
-  const int nsplit = P.header[2 + b] - first;
-  if (nsplit == 1) return;  // stored by the decode kernel
-  T* out_row = static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D;
-  const bool live = nsplit > 1 && first >= 0 && first + (int64_t)nsplit <= P.capacity &&
-                    layer_in_range(P, P.cache_layer ? P.cache_layer[b] : 0);
-  if (!live) {
-    const float fill = nsplit == 0 && P.seqlens[b] < 0 ? 0.f : __builtin_nanf("");
-    for (int d = lane; d < D; d += 64) Elem<T>::store(out_row + d, fill);
-    return;
-  }
-  const int64_t stride = (int64_t)P.num_heads * (D + 2);
-  const float* part = P.partial + (int64_t)first * stride + (int64_t)h * (D + 2);
+CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int lane, T* out_row) {
   const int d0 = lane, d1 = lane + 64;
   float run_m = -INFINITY, den = 0.f, num0 = 0.f, num1 = 0.f;
   for (int base = 0; base < nsplit; base += 64) {
@@ -1169,6 +1153,34 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
   if (d1 < D) Elem<T>::store(out_row + d1, num1 * inv);
 }
 
+// Merge the chunk partials of every (row, head) whose row has more than one
+// chunk, in chunk order; one wave per (row, head). Rows without chunks get zeros
+// (padding rows) or NaN (rows out of range), and multi-chunk rows whose cache
+// layer is missing get NaN.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) decode_merge_kernel(DecodeParams P) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // The decode kernel before this one has drained the item queues: reset them for the next call.
+  if (blockIdx.x == 0 && threadIdx.x < kQueues) P.counters[threadIdx.x * kCounterStride] = 0;
+  if (w >= P.num_rows * P.num_heads) return;
+  const int b = w / P.num_heads;
+  const int h = w - b * P.num_heads;
+  const int first = P.header[1 + b];
+  const int nsplit = P.header[2 + b] - first;
+  if (nsplit == 1) return;  // stored by the decode kernel
+  T* out_row = static_cast<T*>(P.out) + ((int64_t)b * P.num_heads + h) * D;
+  const bool live = nsplit > 1 && first >= 0 && first + (int64_t)nsplit <= P.capacity &&
+                    layer_in_range(P, P.cache_layer ? P.cache_layer[b] : 0);
+  if (!live) {
+    const float fill = nsplit == 0 && P.seqlens[b] < 0 ? 0.f : __builtin_nanf("");
+    for (int d = lane; d < D; d += 64) Elem<T>::store(out_row + d, fill);
+    return;
+  }
+  const int64_t stride = (int64_t)P.num_heads * (D + 2);
+  merge_chunks<T, D>(P.partial + (int64_t)first * stride + (int64_t)h * (D + 2), stride, nsplit, lane, out_row);
+}
+
 }  // namespace cdb
 
 using namespace cdb;
@@ -1214,8 +1226,14 @@ int64_t bytes_per_chunk(int64_t num_heads, int64_t head_dim) {
   return kDescBytes + num_heads * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
+// The persistent grid is at most what is resident at once, and no larger than
+// the launch can have items for: rows x ceil(table_width / chunk_pages) chunks
+// (fewer when the plan lengthens chunks) times the heads, one wave per item.
 int launch_persistent(DecodeKernel kernel, const DecodeParams& P, int num_cus, hipStream_t stream) {
-  const int grid = num_cus * resident_blocks_per_cu(kernel);
+  const int64_t chunks = std::min<int64_t>((int64_t)P.num_rows * ((P.table_width + P.chunk_pages - 1) / P.chunk_pages),
+                                           P.capacity);
+  const int64_t wanted = (chunks * P.num_heads + 3) / 4;
+  const int grid = (int)std::max<int64_t>(1, std::min<int64_t>(wanted, (int64_t)num_cus * resident_blocks_per_cu(kernel)));
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, stream, P);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }

@@ -1099,6 +1099,138 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
   }
 }
 
+// The fast form for small launches (at most kDeepRows rows): with the few
+// items of such a launch a wave takes at most about one item, so occupancy does
+// not matter and latency does. Each wave keeps kDeepSteps - 1 steps of K/V in
+// flight (four register buffers, 2 waves per SIMD) instead of one, and takes
+// its items without cross-item prefetch. A chunk is computed exactly as in
+// paged_decode_fast_kernel (same steps in the same order, same masking, same
+// new-token and slot merge), so a row's result does not depend on the form.
+constexpr int kDeepRows = 16;
+constexpr int kDeepSteps = 4;
+
+template <typename T, int D, int R>
+__global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams P) {
+  constexpr int C = Layout<D>::kChunk;
+  const int lane = threadIdx.x & 63;
+  const int slot = lane >> 4;
+  const int chunk = lane & 15;
+  const int H = P.num_heads;
+  const int kv_group = H / P.num_kv_heads;
+  const int nwaves = gridDim.x * 4;
+  const int chunks = *(const const_int32*)(P.header + 1 + P.num_rows);
+  const int n_items = (int)min((int64_t)chunks, P.capacity) * H;
+  for (int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6)); item < n_items; item += nwaves) {
+    const FastItem cur = make_fast_item(P, load_fast_desc(P, item / H), item % H);
+    const Item& c = cur.it;
+    const int kvh = c.h / kv_group;
+    const int steps = (c.t_end - c.t_begin + 15) >> 4;  // wave steps of cached tokens, 0..8
+    const bool append = c.last && c.live;
+    uint32_t lane_off[4];
+    fast_lane_offsets<T, D>(P, kvh, slot, chunk, lane_off);
+
+    // Query, new token and angles first; then the first steps, all in flight together.
+    Pending<T, D> pend;
+    issue_pending<T, D, R>(P, c, chunk, pend);
+    Angles<D> ang;
+    load_angles<D, R>(P, c.p, chunk, ang);
+    Vec<T, C> kbuf[kDeepSteps][4], vbuf[kDeepSteps][4];
+    bool vl[kDeepSteps][4];
+#pragma unroll
+    for (int st = 0; st < kDeepSteps - 1; ++st) load_fast_step<T, D>(P, cur, st, lane_off, slot, kbuf[st], vbuf[st], vl[st]);
+
+    QueryReg<T, D> q;
+    Vec<T, C> kn, vn;
+    {
+      const T* q_bias = static_cast<const T*>(P.q_bias);
+      const T* k_bias = static_cast<const T*>(P.k_bias);
+      float rot[C];
+      rotate_raw<T, D, R>(pend.q, ang, q_bias ? q_bias + (int64_t)c.h * D : nullptr, chunk, rot);
+      make_query<T, D>(P, rot, q);
+      if (append) {
+        rotate_raw<T, D, R>(pend.k, ang, k_bias ? k_bias + (int64_t)kvh * D : nullptr, chunk, rot);
+#pragma unroll
+        for (int i = 0; i < C; i += 2) kn.set_pair(i, rot[i], rot[i + 1]);
+        vn = pend.v;
+      }
+    }
+
+    float m = -INFINITY, l = 0.f;
+    float acc[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int st = 0; st < kChunkPagesFast; ++st) {
+      if (st >= steps) break;
+      const int ahead = st + kDeepSteps - 1;
+      if (ahead < kChunkPagesFast)
+        load_fast_step<T, D>(P, cur, ahead, lane_off, slot, kbuf[ahead % kDeepSteps], vbuf[ahead % kDeepSteps],
+                             vl[ahead % kDeepSteps]);
+      attend_step<T, D>(q, P.scale_log2, kbuf[st % kDeepSteps], vbuf[st % kDeepSteps], vl[st % kDeepSteps], m, l,
+                        acc);
+    }
+
+    if (append) {
+      // The new token: append its rotated key and its value, then attend to it from registers.
+      const int p = c.p;
+      const int rel = (p >> 4) - (c.t_begin >> 4);  // page of p inside the chunk, 0..7
+      int new_blk = -1;
+#pragma unroll
+      for (int j = 0; j < kChunkPagesFast; ++j)
+        if (j == rel) new_blk = cur.blk[j];
+      if (slot == 0 && c.h % kv_group == 0 && new_blk >= 0) {
+        const int64_t off = (((int64_t)new_blk << 4) + (p & 15)) * ((int64_t)P.num_kv_heads * D) +
+                            (int64_t)kvh * D + chunk * C;
+        kn.store(pool_layer<T>(P.k_pool, P, c) + off);
+        vn.store(pool_layer<T>(P.v_pool, P, c) + off);
+      }
+      const float dot = score<T, D>(q, P.scale_log2, kn);
+      if (slot == 0) {
+        const float m_new = fmaxf(m, dot);
+        const float alpha = exp2f(m - m_new);
+        const float pn = exp2f(dot - m_new);
+        l = l * alpha + pn;
+#pragma unroll
+        for (int i = 0; i < C; ++i) acc[i] = fmaf(pn, vn.get(i), acc[i] * alpha);
+        m = m_new;
+      }
+    }
+
+    // Merge the four slots of the wave (lanes 16 apart hold the same chunk).
+    float m_all = fmaxf(m, shfl_xor_f32(m, 16));
+    m_all = fmaxf(m_all, shfl_xor_f32(m_all, 32));
+    const float f = (m == -INFINITY) ? 0.f : exp2f(m - m_all);
+    l *= f;
+#pragma unroll
+    for (int i = 0; i < C; ++i) acc[i] *= f;
+    l += shfl_xor_f32(l, 16);
+    l += shfl_xor_f32(l, 32);
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      acc[i] += shfl_xor_f32(acc[i], 16);
+      acc[i] += shfl_xor_f32(acc[i], 32);
+    }
+    if (slot == 0) {
+      if (c.single) {
+        T* out_row = static_cast<T*>(P.out) + ((int64_t)c.b * H + c.h) * D;
+        const float inv = c.live ? 1.f / l : __builtin_nanf("");
+        Vec<T, C> o;
+#pragma unroll
+        for (int i = 0; i < C; i += 2) o.set_pair(i, acc[i] * inv, acc[i + 1] * inv);
+        o.store(out_row + chunk * C);
+      } else if (c.live) {
+        float* part = P.partial + ((int64_t)c.partial * H + c.h) * (D + 2);
+#pragma unroll
+        for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
+        if (chunk == 0) {
+          part[D] = m_all;
+          part[D + 1] = l;
+        }
+      }
+    }
+  }
+}
+
 // The merge of one (row, head): chunk c's partial (unnormalized accumulator of
 // D floats, then its max and sum) starts at part + c * stride. Lane s holds
 // chunk s's (max, sum) so the global max and the denominator are wave
@@ -1253,8 +1385,9 @@ int launch_decode(const DecodeParams& P, int stages, int num_cus, hipStream_t st
     if (hipGetLastError() != hipSuccess) return CDB_ERR_HIP;
   }
   if (!(stages & CDB_DECODE_STAGE_ATTEND)) return CDB_OK;
-  const int rc = fast_form(P) ? launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream)
-                              : launch_persistent(paged_decode_kernel<T, D, R>, P, num_cus, stream);
+  const int rc = !fast_form(P)              ? launch_persistent(paged_decode_kernel<T, D, R>, P, num_cus, stream)
+                 : P.num_rows <= kDeepRows ? launch_persistent(paged_decode_deep_kernel<T, D, R>, P, num_cus, stream)
+                                           : launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream);
   if (rc != CDB_OK) return rc;
   const int64_t waves = (int64_t)P.num_rows * P.num_heads;
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, P);

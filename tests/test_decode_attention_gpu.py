@@ -233,3 +233,55 @@ def test_plan_once_then_attend_per_layer_matches_planning_every_layer() -> None:
     for a, b in zip(staged, fresh):
         assert torch.equal(a, b)
     assert not torch.equal(staged[0], staged[1])  # the layers really differ
+
+
+def _expected_plan(case, chunk_tokens: int):
+    """The chunk plan restated on the host: per row its chunks of chunk_tokens tokens (the last
+    one ends at the new token), a descriptor per chunk (row | last flag, token range, position,
+    partial slot, chunks in the row, table row, cache-layer offset, the chunk's 8 block ids), full
+    chunks first in row order, then last chunks by decreasing ceil(tokens / 32)."""
+
+    bs = case.block_size
+    width = case.block_table.shape[1]
+    full, last = [], []
+    prefix = [0]
+    for b, p in enumerate(case.seqlens.tolist()):
+        n = (p + chunk_tokens) // chunk_tokens if 0 <= p < width * bs else 0
+        for c in range(n):
+            t0 = c * chunk_tokens
+            is_last = c == n - 1
+            page0 = t0 // bs
+            ids = [int(case.block_table[b, page0 + j]) if page0 + j < width else -1 for j in range(8)]
+            desc = [b | (1 << 30 if is_last else 0), t0, p if is_last else t0 + chunk_tokens, p,
+                    prefix[-1] + c, n, b, int(case.cache_layer[b])] + ids
+            (last if is_last else full).append(desc)
+        prefix.append(prefix[-1] + n)
+    key = lambda d: min((d[3] + 1 - d[1] + 31) // 32, 63)
+    return prefix, full, last, key
+
+
+def test_plan_descriptors_match_a_host_restatement() -> None:
+    from continuous_depth_batching_amd import ops
+
+    case = make_case(seed=33, num_rows=40, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1300,
+                     rope_style=1, dtype="bf16", padding_rows=2)
+    width = case.block_table.shape[1]
+    case.seqlens[5] = width * case.block_size  # one row past its table: no chunks
+    d, ws = _device_case(case)
+    d["seqlens"] = torch.from_numpy(case.seqlens).cuda()
+    ws.fill_(float("nan"))
+    rows = list(range(40))
+    _attend(case, d, ws, rows, stages=ops.DECODE_PLAN)
+    torch.cuda.synchronize()
+    words = ws.view(torch.int32).cpu().numpy()
+    chunk_tokens = ops.MIN_SPLIT_PAGES * case.block_size
+    prefix, full, last, key = _expected_plan(case, chunk_tokens)
+    assert words[0] == chunk_tokens
+    np.testing.assert_array_equal(words[1:42], prefix)
+    header_ints = (((40 + 2) * 4 + 255) // 256 * 256 + 1024) // 4
+    got = words[header_ints:header_ints + 16 * (len(full) + len(last))].reshape(-1, 16).tolist()
+    assert got[:len(full)] == full  # full chunks in row order
+    tail = got[len(full):]
+    # Last chunks by decreasing length key; within a key the order is free.
+    assert [key(x) for x in tail] == sorted((key(x) for x in last), reverse=True)
+    assert sorted(map(tuple, tail)) == sorted(map(tuple, last))

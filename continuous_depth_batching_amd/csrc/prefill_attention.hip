@@ -389,7 +389,7 @@ __global__ void __launch_bounds__(256) prefill_attention_bf16_kernel(PrefillPara
     }
   };
   // Softmax of a block's (masked) scores into bf16 P^T operands, in eight
-  // branch-free stages that the next block's score MFMAs are interleaved with.
+  // branch-free stages.
   // The running max moves (by a select) only when the block's max exceeds it by
   // more than 2^kRescaleSlack; the accumulator rescale that then follows is the
   // caller's (rare) branch.

@@ -1103,9 +1103,8 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
   }
 }
 
-// The fast form for small launches (at most kDeepRows rows): with the few
-// items of such a launch a wave takes one or two items, so latency matters more
-// than occupancy. Each wave keeps kDeepSteps - 1 steps of K/V in
+// The fast form for small launches (at most kDeepRows rows): such a launch
+// gives a wave one to four items, so latency matters more than occupancy. Each wave keeps kDeepSteps - 1 steps of K/V in
 // flight (four register buffers, 2 waves per SIMD) instead of one, and takes
 // its items without cross-item prefetch. A chunk is computed exactly as in
 // paged_decode_fast_kernel (same steps in the same order, same masking, same

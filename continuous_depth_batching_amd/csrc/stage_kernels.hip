@@ -332,7 +332,7 @@ __global__ void __launch_bounds__(kThreads) argmax_kernel(const T* logits, int64
 // rules; huginn/exit_gates.py:33-40 latent difference).
 //
 // kind 0 (hazard gate): logit = R(h . w + bias), written to signal[b].
-// kind 1 (latent difference): signal = R(||h - prev|| / max(||h||, 1e-9)),
+// kind 1 (latent difference): signal = R(||h - prev|| / max(||h||, R(1e-9))),
 //   computed from rounded elementwise differences.
 // The per-token policy state (cdf, survival in fp64; pending signal) lives in
 // arrays indexed by state_index[b] (the token's hidden slot). Then:
@@ -407,7 +407,8 @@ __global__ void __launch_bounds__(kThreads) exit_gate_kernel(GateParams P) {
     signal = Elem<T>::round(acc + b);
   } else {
     const float num = Elem<T>::round(sqrtf(acc));
-    const float den = fmaxf(Elem<T>::round(sqrtf(acc2)), 1e-9f);
+    // clamp_min(1e-9) on a model-dtype norm: the bound is itself in the model dtype.
+    const float den = fmaxf(Elem<T>::round(sqrtf(acc2)), Elem<T>::round(1e-9f));
     signal = Elem<T>::round(num / den);
   }
   Elem<T>::store(static_cast<T*>(P.signal) + row, signal);

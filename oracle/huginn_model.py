@@ -54,8 +54,15 @@ def huginn_rope_tables(head_dim: int, theta: float, max_positions: int) -> tuple
 
 class HuginnOracle:
     def __init__(self, weights: dict[str, np.ndarray], *, n_embd: int, n_heads: int, n_prelude: int, n_core: int,
-                 n_coda: int, rope_base: float, eps: float, dtype: str = "f32", max_positions: int = 4096) -> None:
+                 n_coda: int, rope_base: float, eps: float, dtype: str = "f32", max_positions: int = 4096,
+                 accumulate: str = "f32") -> None:
+        """``accumulate`` is the dot-product precision of the projections ("f32", like the GPU
+        GEMMs, or "f64"); their results are rounded to ``dtype`` either way, so the two settings
+        are two valid implementations whose spread is the size of accumulation-order noise."""
+
         self.w = {k: np.asarray(v, dtype=np.float32) for k, v in weights.items()}
+        self.acc = np.float64 if accumulate == "f64" else np.float32
+        self._w64: dict[int, np.ndarray] = {}
         self.E, self.H = n_embd, n_heads
         self.D = n_embd // n_heads
         self.n_prelude, self.n_core, self.n_coda = n_prelude, n_core, n_coda
@@ -67,7 +74,12 @@ class HuginnOracle:
 
     # -- pieces ------------------------------------------------------------------------------------------------
     def _mm(self, x: np.ndarray, weight: np.ndarray) -> np.ndarray:
-        return self.rnd(np.asarray(x, np.float32) @ weight.T)
+        if self.acc is np.float32:
+            return self.rnd(np.asarray(x, np.float32) @ weight.T)
+        wide = self._w64.get(id(weight))
+        if wide is None:
+            wide = self._w64[id(weight)] = weight.astype(np.float64)
+        return self.rnd((np.asarray(x, np.float64) @ wide.T).astype(np.float32))
 
     def _norm(self, x: np.ndarray, name: str) -> np.ndarray:
         return rmsnorm(x, self.w[name], self.eps, self.dtype)
@@ -136,11 +148,12 @@ class HuginnOracle:
         return self._mm(hidden[None, :], self.w["lm_head.weight"])[0]
 
     def latent_diff(self, state: np.ndarray, prev: np.ndarray) -> float:
-        """R(R(||R(s - p)||) / max(R(||s||), 1e-9)) (huginn/exit_gates.py:33-40 on model-dtype tensors)."""
+        """R(R(||R(s - p)||) / max(R(||s||), R(1e-9))) (huginn/exit_gates.py:33-40 on model-dtype tensors)."""
 
         d = self.rnd(state.astype(np.float32) - prev.astype(np.float32)).astype(np.float64)
         num = self.rnd(np.array([np.sqrt((d * d).sum())], np.float32))[0]
-        den = max(float(self.rnd(np.array([np.sqrt((state.astype(np.float64) ** 2).sum())], np.float32))[0]), 1e-9)
+        floor = float(self.rnd(np.array([1e-9], np.float32))[0])
+        den = max(float(self.rnd(np.array([np.sqrt((state.astype(np.float64) ** 2).sum())], np.float32))[0]), floor)
         return float(self.rnd(np.array([num / den], np.float32))[0])
 
     # -- request-level ---------------------------------------------------------------------------------------------
@@ -157,7 +170,13 @@ class HuginnOracle:
 
     def generate(self, prompt: list[int], max_new_tokens: int, *, max_steps: int, kv_policy: str = "single",
                  exit_depths: list[int] | None = None, threshold: float | None = None, min_steps: int = 1,
-                 delayed: bool = False, eos_token_id: int | None = None) -> HuginnOracleOutput:
+                 delayed: bool = False, eos_token_id: int | None = None, forced_tokens: list[int] | None = None,
+                 hidden_trace: list | None = None) -> HuginnOracleOutput:
+        """Greedy CDB decode of one request. ``forced_tokens`` feeds the given tokens back instead
+        of the oracle's own (teacher forcing; ``tokens`` still records the oracle's argmax), and
+        ``hidden_trace`` collects (decode token index j >= 1, loop step, recurrent state after the
+        step)."""
+
         num_slots = {"single": 1, "depth_indexed": max_steps, "last_exited": max_steps}[kv_policy]
 
         def slot_of(step: int) -> int:
@@ -168,6 +187,8 @@ class HuginnOracle:
         h = self.prefill_hidden(prompt, kv, steps=max_steps, slot_of=slot_of, num_slots=num_slots)
         token = int(np.argmax(self.logits(h[-1])))
         out = HuginnOracleOutput(tokens=[token])
+        if forced_tokens is not None:
+            token = forced_tokens[0]
         pos = len(prompt)
         while len(out.tokens) < max_new_tokens and token != eos_token_id:
             k_idx = len(out.tokens) - 1
@@ -181,6 +202,8 @@ class HuginnOracle:
             for step in range(max_steps):
                 prev = state
                 state = self.core_step(state, injection, kv, slot_of(step), p)
+                if hidden_trace is not None:
+                    hidden_trace.append((k_idx + 1, step, state[0].copy()))
                 if step == max_steps - 1:
                     break
                 if depth is not None:
@@ -209,5 +232,7 @@ class HuginnOracle:
             h = self.coda(state, kv, num_slots, p)
             token = int(np.argmax(self.logits(h[0])))
             out.tokens.append(token)
+            if forced_tokens is not None:
+                token = forced_tokens[len(out.tokens) - 1]
             pos += 1
         return out

@@ -78,7 +78,9 @@ def latent_diff(hidden: np.ndarray, prev: np.ndarray, dtype: str) -> np.ndarray:
     rnd = rounder(dtype)
     d = rnd(np.asarray(hidden, np.float32) - np.asarray(prev, np.float32))
     num = rnd(np.sqrt((d.astype(np.float64) ** 2).sum(-1)).astype(np.float32))
-    den = np.maximum(rnd(np.sqrt((np.asarray(hidden, np.float64) ** 2).sum(-1)).astype(np.float32)), np.float32(1e-9))
+    # clamp_min(1e-9) on a model-dtype norm clamps to the model-dtype value of 1e-9.
+    floor = rnd(np.array([1e-9], np.float32))[0]
+    den = np.maximum(rnd(np.sqrt((np.asarray(hidden, np.float64) ** 2).sum(-1)).astype(np.float32)), floor)
     return rnd((num / den).astype(np.float32))
 
 

@@ -102,3 +102,70 @@ def test_latent_difference_is_relative_l2() -> None:
     prev = np.array([[0.0, 4.0]], np.float32)
     assert stage.latent_diff(h, prev, "f32")[0] == pytest.approx(3.0 / 5.0)
     assert stage.latent_diff(h, h, "f32")[0] == 0.0
+
+
+def _torch_latent_diff(h: np.ndarray, p: np.ndarray) -> np.ndarray:
+    """huginn/exit_gates.py:33-40 run by torch on bf16 tensors."""
+
+    th, tp = torch.from_numpy(h).bfloat16(), torch.from_numpy(p).bfloat16()
+    return ((th - tp).norm(dim=-1) / th.norm(dim=-1).clamp_min(1e-9)).float().numpy()
+
+
+@pytest.mark.parametrize("scale", [1e-3, 1.0, 30.0])
+def test_latent_difference_bf16_equals_torch_bf16(scale: float) -> None:
+    """The bf16 rounding points R(R(||R(h - p)||) / max(R(||h||), R(1e-9))) are torch's own.
+    On 3000 rows 5280 wide (Huginn-0125's state), the oracle equals the reference's
+    expression evaluated by torch on bf16 tensors on all but at most 0.1% of rows. There
+    torch's fp32 sum of squares and the oracle's fp64 one fall on either side of a bf16
+    rounding boundary of a norm: one bf16 step in a norm, at most two in the signal. A dropped
+    rounding point (e.g. no R() after the subtraction) differs on most rows."""
+
+    from oracle.huginn_model import HuginnOracle
+
+    rng = np.random.default_rng(int(scale * 1000))
+    h = round_bf16((rng.standard_normal((3000, 5280)) * scale).astype(np.float32))
+    rel = rng.uniform(0.0, 0.5, (3000, 1)).astype(np.float32)
+    p = round_bf16(h + (rng.standard_normal(h.shape) * scale).astype(np.float32) * rel)
+    p[:40] = h[:40]  # converged rows: signal 0
+    want = _torch_latent_diff(h, p)
+    got = stage.latent_diff(h, p, "bf16")
+    differ = got != want
+    assert differ.sum() <= 3, differ.sum()
+    assert np.all(np.abs(got - want)[differ] <= np.abs(want[differ]) * 2.0 ** -6 * 1.0001)
+    assert np.all(got[:40] == 0.0)
+    # The same expression with the subtraction left unrounded: most rows differ.
+    loose = np.sqrt(((h.astype(np.float64) - p) ** 2).sum(-1)) / np.sqrt((h.astype(np.float64) ** 2).sum(-1))
+    assert np.mean(round_bf16(loose.astype(np.float32))[40:] != want[40:]) > 0.05
+    # The model oracle's per-row restatement equals the batched one.
+    rows = HuginnOracle.latent_diff.__get__(type("O", (), {"rnd": staticmethod(round_bf16)})())
+    for i in range(0, 3000, 97):
+        assert rows(h[i], p[i]) == got[i]
+
+
+def test_latent_difference_bf16_zero_state_clamps_in_bf16() -> None:
+    """An all-zero state: torch clamps the bf16 norm to bf16(1e-9), not to fp32 1e-9."""
+
+    h = np.zeros((3, 64), np.float32)
+    p = round_bf16(np.random.default_rng(5).standard_normal((3, 64)).astype(np.float32))
+    want = _torch_latent_diff(h, p)
+    np.testing.assert_array_equal(stage.latent_diff(h, p, "bf16"), want)
+    assert want[0] != np.float32(round_bf16(np.array([np.linalg.norm(p[0]) / 1e-9], np.float32))[0])
+
+
+@pytest.mark.parametrize("scale", [1.0, 4.0, 20.0])
+def test_silu_mul_bf16_against_torch_bf16(scale: float) -> None:
+    """R(R(silu(g)) * u) on bf16 inputs against F.silu(g) * u on bf16 tensors
+    (ouro/modeling_ouro.py:167-169). The oracle takes silu in float64 and rounds
+    once to fp32, then to bf16; torch computes silu in fp32. The two agree on all but
+    a few in a million values (a double rounding at a bf16 midpoint), and those differ
+    by one bf16 step."""
+
+    rng = np.random.default_rng(int(scale))
+    gu = round_bf16((rng.standard_normal((2000, 1024)) * scale).astype(np.float32))
+    g, u = torch.from_numpy(gu).bfloat16().chunk(2, dim=-1)
+    want = (torch.nn.functional.silu(g) * u).float().numpy()
+    got = stage.silu_mul(gu, "bf16")
+    differ = got != want
+    assert differ.sum() <= 5, differ.sum()
+    step = np.abs(want) * 2.0 ** -7 + 1e-30
+    assert np.all(np.abs(got - want)[differ] <= step[differ] * 1.0001)

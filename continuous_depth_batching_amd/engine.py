@@ -32,6 +32,7 @@ from typing import Any, Callable
 import torch
 
 from .cache import CacheFullError, PagedKVCache
+from .decode_staging import DecodeStaging
 from .offloading import OffloadingManager
 from .config import ContinuousDepthBatchingConfig, validate_cache_size_request
 from .exit_policy import ExitPolicy
@@ -147,7 +148,7 @@ class ContinuousDepthBatchingEngine:
     last_stats: ContinuousDepthBatchingStats = field(default_factory=ContinuousDepthBatchingStats)
     pending_coda_results: deque = field(default_factory=deque)
     pending_prefill_results: deque = field(default_factory=deque)
-    stalled_decoders: dict = field(default_factory=dict)
+    staging: DecodeStaging | None = None
     finished_outputs: dict = field(default_factory=dict)
     # Schedule-parity hooks. ``record_launches`` logs every launch with the state it reads:
     #   ("prefill",   ((request_id, start_position, query_length, has_new_token), ...))
@@ -206,9 +207,10 @@ class ContinuousDepthBatchingEngine:
         offloading_manager = OffloadingManager(cache, scheduler, cfg.cpu_offload_space,
                                                allow_recompute_fallback=not copies_exit_kv(cfg.kv_policy),
                                                swap_factory=runner.make_kv_swap_pool)
+        staging = DecodeStaging(cache, cfg.kv_pressure_mode, offloading_manager.preempt_request)
         return cls(model=model, cdb_config=cfg, cache=cache, scheduler=scheduler, runner=runner,
                    model_adapter=adapter, exit_policy=exit_policy, exit_kv_layout=exit_kv_layout,
-                   offloading_manager=offloading_manager)
+                   offloading_manager=offloading_manager, staging=staging)
 
     # -- public API (continuous_api.py:378-452) -----------------------------------------------------------------
     @torch.no_grad()
@@ -259,7 +261,7 @@ class ContinuousDepthBatchingEngine:
         self.last_stats = ContinuousDepthBatchingStats()
         self.pending_coda_results.clear()
         self.pending_prefill_results.clear()
-        self.stalled_decoders.clear()
+        self.staging.clear()
         self.finished_outputs.clear()
         self._exit_kv_backlog.clear()
         self._pending_flags.clear()
@@ -267,50 +269,76 @@ class ContinuousDepthBatchingEngine:
 
     # -- refill loop (continuous_api.py:503-606) ----------------------------------------------------------------
     def _run_scheduler_loop(self) -> None:
+        """Scheduler ticks until every request finished and every staged result was taken in.
+
+        A tick takes in the results that have landed (waiting for them when nothing else is
+        pending), puts restored and parked decoders back into the loop, then launches the one
+        bucket ``schedule_next`` picks. A tick that gets no bucket instead waits for a staged
+        result, takes a parked decoder's KV away, or reports a dead end."""
+
         sched = self.scheduler
         while sched.has_pending_work() or self.pending_coda_results or self.pending_prefill_results:
-            self._consume_ready_prefill_results(block=not sched.has_pending_work())
-            self._consume_ready_coda_results(block=not sched.has_pending_work())
-            if not sched.has_pending_work():
+            self._take_landed_results()
+            if not sched.has_pending_work():  # what landed finished the last request, or nothing is left
                 continue
-            # Restores go first, so the prefill gate below sees them; they already hold a block for
-            # their pending token. Restored and restaged decoders share one prelude launch.
-            restored = self._restore_offloaded_requests()
-            resumed = [item for state in restored if (item := self._stage_decode_token(state)) is not None]
-            resumed += self._restage_stalled_decoders()
-            self._prelude_and_enqueue_depth(resumed, site="resumed", front=True)
-            stats = self.last_stats
-            stats.scheduler_ticks += 1
-            pending_codas = len(self.pending_coda_results)
-            if pending_codas:
-                stats.coda_suppressed_ticks += 1
-            scheduled = sched.schedule_next(token_budget=self.cache.max_num_batched_tokens,
-                                            cache_budget=self.cache.num_pages,
-                                            allow_coda=pending_codas < CODA_PIPELINE_DEPTH)
-            if (pending_codas >= CODA_PIPELINE_DEPTH and sched.coda_queue
-                    and (scheduled is None or len(sched.coda_queue) >= sched.min_coda_batch_size)):
-                stats.coda_pipeline_blocked_ticks += 1
-            if scheduled is None:
-                if self.pending_prefill_results:
-                    self._consume_ready_prefill_results(block=True)
-                    continue
-                if self.pending_coda_results:
-                    self._consume_ready_coda_results(block=True)
-                    continue
-                if self.stalled_decoders:
-                    # Nothing else can run and no stalled decoder can allocate: yield one request's KV.
-                    self._preempt_stalled_decoder()
-                    continue
-                self._raise_scheduler_stall()
-            if scheduled.kind == "prefill":
-                self._run_prefill_batch(scheduled)
-            elif scheduled.kind == "coda":
-                self._stage_coda_batch(scheduled.depth_items or [])
+            self._resume_decoders()
+            batch = self._pick_batch()
+            if batch is None:
+                self._unblock()
             else:
-                self._run_mixed_recurrent_batch(scheduled.depth_items or [])
-        self._consume_ready_prefill_results(block=True)
-        self._consume_ready_coda_results(block=True)
+                self._launch(batch)
+        self._take_landed_results(wait=True)
         self._finish_stats()
+
+    def _take_landed_results(self, *, wait: bool = False) -> None:
+        """Prefill results first: a request's first token (prefill) comes before its second (coda).
+        Each kind is waited for when ``wait`` is set or the scheduler has nothing else pending."""
+
+        idle = lambda: wait or not self.scheduler.has_pending_work()
+        self._consume_ready_prefill_results(block=idle())
+        self._consume_ready_coda_results(block=idle())
+
+    def _resume_decoders(self) -> None:
+        """Swapped-out requests whose KV came back, then parked decoders, share one prelude launch
+        at the head of the depth queue. Restores run first so that the prefill gate of this tick
+        sees them; they already hold the block of their pending token."""
+
+        items = [item for state in self._restore_offloaded_requests()
+                 if (item := self.staging.stage(state)) is not None]
+        items += self.staging.retry_parked()
+        self._prelude_and_enqueue_depth(items, site="resumed", front=True)
+
+    def _pick_batch(self) -> ScheduledCDBBatch | None:
+        stats, sched = self.last_stats, self.scheduler
+        stats.scheduler_ticks += 1
+        in_flight = len(self.pending_coda_results)
+        stats.coda_suppressed_ticks += in_flight > 0
+        coda_open = in_flight < CODA_PIPELINE_DEPTH
+        batch = sched.schedule_next(token_budget=self.cache.max_num_batched_tokens,
+                                    cache_budget=self.cache.num_pages, allow_coda=coda_open)
+        # Count the ticks where the pipeline bound held back a coda that would have run.
+        if not coda_open and sched.coda_queue and (batch is None
+                                                    or len(sched.coda_queue) >= sched.min_coda_batch_size):
+            stats.coda_pipeline_blocked_ticks += 1
+        return batch
+
+    def _unblock(self) -> None:
+        if self.pending_prefill_results:
+            self._consume_ready_prefill_results(block=True)
+        elif self.pending_coda_results:
+            self._consume_ready_coda_results(block=True)
+        elif self.staging.parked:
+            self.staging.yield_one(len(self.scheduler.active_requests))
+        else:
+            self._raise_scheduler_stall()
+
+    def _launch(self, batch: ScheduledCDBBatch) -> None:
+        if batch.kind == "prefill":
+            self._run_prefill_batch(batch)
+        elif batch.kind == "coda":
+            self._stage_coda_batch(batch.depth_items or [])
+        else:
+            self._run_mixed_recurrent_batch(batch.depth_items or [])
 
     def _finish_stats(self) -> None:
         s = self.last_stats
@@ -346,10 +374,10 @@ class ContinuousDepthBatchingEngine:
             stats.prefill_coda_tokens += 1
             eager = False
             if (self.cdb_config.use_async_batching and not state.will_finish_on_pending_token()
-                    and self._try_allocate_one_decode_token(state)):
+                    and self.staging.reserve_row(state)):
                 eager = True
                 eager_rows.append(len(eager_flags))
-                eager_items.append(self._build_decode_item(state, token_id=TMP_TOKEN_ID))
+                eager_items.append(self.staging.work_item(state, token_id=TMP_TOKEN_ID))
             eager_flags.append(eager)
         pending.eager_entries = eager_flags
         if eager_items:
@@ -398,7 +426,7 @@ class ContinuousDepthBatchingEngine:
                 continue
             if self._advance_after_prefill(state, token):
                 continue
-            item = self._stage_decode_token(state)
+            item = self.staging.stage(state)
             if item is not None:
                 new_items.append(item)
         self._prelude_and_enqueue_depth(new_items, site="after_prefill")
@@ -506,7 +534,7 @@ class ContinuousDepthBatchingEngine:
 
         # Per row: skip a request that finishes on its pending token, else advance its position
         # and keep a KV slot for it (its last block, or a new one), then build its successor.
-        return _tick.select_eager(coda_items, self.cache.block_size, self._try_allocate_one_decode_token,
+        return _tick.select_eager(coda_items, self.cache.block_size, self.staging.reserve_row,
                                   DepthWorkItem, TMP_TOKEN_ID)
 
     def _consume_ready_coda_results(self, *, block: bool) -> None:
@@ -534,7 +562,7 @@ class ContinuousDepthBatchingEngine:
             if not stage:
                 self._retire_request(state)
                 continue
-            new = self._stage_decode_token(state)
+            new = self.staging.stage(state)
             if new is not None:
                 new_items.append(new)
         self._prelude_and_enqueue_depth(new_items, site="after_coda_staged", front=True)
@@ -556,7 +584,7 @@ class ContinuousDepthBatchingEngine:
     def _retire_request(self, state: RequestState) -> None:
         self.scheduler.record_completion(state)
         self.scheduler.finish_request(state.request_id)
-        self.stalled_decoders.pop(state.request_id, None)
+        self.staging.forget(state.request_id)
         self.finished_outputs[state.request_id] = state.to_generation_output()
         self.scheduler.block_new_requests = False
 
@@ -591,55 +619,6 @@ class ContinuousDepthBatchingEngine:
             for item in items:
                 self.scheduler.enqueue_depth(item)
 
-    def _build_decode_item(self, state: RequestState, *, token_id: int | None = None) -> DepthWorkItem:
-        state.reset_depth_state_for_next_token()
-        return DepthWorkItem(state=state, token_id=state.tokens_to_process[0] if token_id is None else token_id,
-                             token_position=state.position_offset, recurrent_step=0,
-                             synthetic_exit_depth=state.next_synthetic_exit_depth())
-
-    def _stage_decode_token(self, state: RequestState) -> DepthWorkItem | None:
-        if not state.tokens_to_process or state.tokens_to_process[0] < 0:
-            raise RuntimeError(f"Request {state.request_id} has no sampled token ready for CDB decode")
-        if self._try_allocate_one_decode_token(state):
-            self.stalled_decoders.pop(state.request_id, None)
-            return self._build_decode_item(state)
-        if self.cdb_config.kv_pressure_mode == "none":
-            raise CacheFullError(
-                f"KV cache full staging a decode block for request {state.request_id} and "
-                "kv_pressure_mode='none' does no preemption. Increase num_blocks, reduce load, or select "
-                "kv_pressure_mode='reserve'/'recompute'/'offload'.")
-        if self.cdb_config.kv_pressure_mode == "reserve":
-            raise CacheFullError(
-                f"Reserve admission over-committed the KV cache: request {state.request_id} could not "
-                "allocate a decode block. This is a bug in reservation accounting.")
-        self.stalled_decoders[state.request_id] = state
-        return None
-
-    def _restage_stalled_decoders(self) -> list[DepthWorkItem]:
-        items: list[DepthWorkItem] = []
-        for state in list(self.stalled_decoders.values()):
-            item = self._stage_decode_token(state)
-            if item is None:
-                break
-            items.append(item)
-        return items
-
-    def _preempt_stalled_decoder(self) -> None:
-        """Yield one stalled decoder's KV so the rest of the batch drains (continuous_api.py:1625-1652).
-
-        Only a stalled request sits at a clean token boundary. The victim is the one with the
-        fewest computed tokens, ties going to the most recent staller."""
-
-        if len(self.scheduler.active_requests) <= 1:
-            request_id = next(iter(self.stalled_decoders))
-            raise CacheFullError(
-                f"A single request's KV cache does not fit: request {request_id} could not allocate "
-                "a decode block and no other request can be preempted (increase num_blocks or reduce "
-                "max_model_len).")
-        request_id = min(reversed(self.stalled_decoders), key=lambda r: self.stalled_decoders[r].current_len())
-        state = self.stalled_decoders.pop(request_id)
-        self.offloading_manager.preempt_request(request_id, state)
-
     def _restore_offloaded_requests(self) -> list[RequestState]:
         """Re-admit swapped-out requests and copy their KV back before any launch reads it
         (continuous_api.py:1490-1505)."""
@@ -651,29 +630,23 @@ class ContinuousDepthBatchingEngine:
             self.offloading_manager.restore_scheduled_requests(restored)
         return restored
 
-    def _try_allocate_one_decode_token(self, state: RequestState) -> bool:
-        current = state.current_len()
-        if state.allocated_blocks * self.cache.block_size - current >= 1 and state.allocated_blocks > 0:
-            return True
-        needed = -(-(current + 1) // self.cache.block_size) - state.allocated_blocks
-        got = self.cache.allocate_blocks(needed, state.request_id, state.allocated_blocks)
-        if got is None:
-            return False
-        state.allocated_blocks += got
-        return True
-
     def _raise_scheduler_stall(self) -> None:
-        candidates = self.scheduler.get_prefill_bucket()
-        if not candidates:
-            raise CacheFullError("The CDB scheduler could place no work and has nothing in flight")
-        state = candidates[0]
-        n = min(len(state.remaining_prefill_tokens), self.cache.max_num_batched_tokens)
-        needed = -(-(state.current_len() + n) // self.cache.block_size) - state.allocated_blocks
-        if not self.cache.will_allocation_be_successful(needed, state.allocated_blocks):
-            raise CacheFullError(f"KV cache full: request {state.request_id} needs {needed} blocks for its next "
-                                 f"prefill chunk, {self.cache.get_num_free_blocks()} are free")
-        raise RuntimeError(f"No request could be scheduled: request {state.request_id} reads "
-                           f"{state.current_len()} KV tokens, exceeding the cache budget of {self.cache.num_pages}")
+        """A tick with no bucket, no staged result and no parked decoder: nothing will change, so
+        the leading prefill candidate names the cause (cdb/continuous_api.py:1450-1488)."""
+
+        waiting = self.scheduler.get_prefill_bucket()
+        if not waiting:
+            raise CacheFullError("scheduler dead end: no bucket, nothing in flight and no prompt waiting")
+        head = waiting[0]
+        chunk = min(len(head.remaining_prefill_tokens), self.cache.max_num_batched_tokens)
+        blocks = self.cache.block_size
+        missing = (head.current_len() + chunk + blocks - 1) // blocks - head.allocated_blocks
+        if not self.cache.will_allocation_be_successful(missing, head.allocated_blocks):
+            raise CacheFullError(f"prompt chunk of request {head.request_id} does not fit: it needs {missing} more "
+                                 f"KV blocks and {self.cache.get_num_free_blocks()} are free, with no decoding "
+                                 "request left to free any")
+        raise RuntimeError(f"request {head.request_id} cannot be scheduled: its {head.current_len()} KV tokens "
+                           f"exceed the cache budget of {self.cache.num_pages} tokens")
 
     # -- no-refill baseline (continuous_api.py:608-944, synchronous wave form) ----------------------------------
     def _run_no_refill_loop(self) -> None:
@@ -694,16 +667,16 @@ class ContinuousDepthBatchingEngine:
             cohort = [s for s in sched.active_requests.values()
                       if s.status == RequestStatus.DECODING and s.tokens_to_process and s.tokens_to_process[0] >= 0]
             cohort = cohort[: self.cdb_config.max_num_seqs]
-            items = [item for s in cohort if (item := self._stage_decode_token(s)) is not None]
+            items = [item for s in cohort if (item := self.staging.stage(s)) is not None]
             if not items:
                 if not did_prefill:
-                    if self.stalled_decoders:
-                        # No wave can run and no stalled decoder can allocate: yield one request's KV.
-                        self._preempt_stalled_decoder()
+                    if self.staging.parked:
+                        # No wave can run and no parked decoder can allocate: take one's KV away.
+                        self.staging.yield_one(len(sched.active_requests))
                         continue
                     if sched.has_pending_work():
-                        raise CacheFullError("No-refill loop stalled with pending work: the KV cache cannot "
-                                             "admit any waiting request and no decode work is ready")
+                        raise CacheFullError("no-refill wave dead end: no waiting prompt fits the KV cache "
+                                             "and no decode token is ready")
                 continue
             self._record_prelude("wave_cohort", len(items))
             self.runner.compute_prelude_batch(items)

@@ -145,7 +145,7 @@ def test_recurrent_metadata_rows_and_padding() -> None:
         state.status = RequestStatus.DECODING
         state.tokens_to_process = [idx + 1]
         engine.scheduler.active_requests[state.request_id] = state
-        item = engine._stage_decode_token(state)
+        item = engine.staging.stage(state)
         assert item is not None
         items.append(item)
     items[2].recurrent_step = 2

@@ -392,11 +392,11 @@ class HuginnCDBAdapter(CDBModelAdapter):
         def attend(i: int, w: dict, qkv: torch.Tensor) -> torch.Tensor:
             layer = layer_of(i)
             q, k, v = self._split_qkv(qkv)  # strided column slices: the kernel reads them in place
-            q_rot = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-            ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
-                                  self.rope_cos, self.rope_sin, ROPE_INTERLEAVED, w["q_bias"], w["k_bias"])
-            out = torch.empty_like(q_rot)
-            ops.prefill_attention_launch(q_rot, cache.view, layer, cache.device_table, launch, out, self.scale)
+            q_rot = torch.ops.cdb.rope_kv_write(q, k, v, cache.pool, layer, cache.block_size, launch.write_rows,
+                                                launch.positions, self.rope_cos, self.rope_sin, ROPE_INTERLEAVED,
+                                                w["q_bias"], w["k_bias"])
+            out = ops.prefill_attention_launch(q_rot, cache.pool, layer, cache.block_size, cache.device_table, launch,
+                                               self.scale)
             return out.view(tokens, self.num_heads, self.head_dim)
 
         return attend
@@ -476,10 +476,10 @@ class HuginnCDBAdapter(CDBModelAdapter):
         torch.ops.cdb.scatter_rows_(launch.bank, launch.bank_slots, state)
         g = launch.gate
         if g.enabled:
-            ops.exit_gate_raw(state, prev, None, None, g.signal, g.state, launch.bank_slots, g.steps, g.synthetic,
-                              g.flags, rows, kind=ops.GATE_LATENT_DIFF, rule=g.rule, delayed=False,
-                              round_hazard=g.round_hazard, min_steps=g.min_steps, max_steps=g.max_steps,
-                              threshold=g.threshold)
+            torch.ops.cdb.exit_gate(state, prev, None, None, g.signal, g.state.cdf, g.state.survival,
+                                    g.state.pending, launch.bank_slots, g.steps, g.synthetic, g.flags, rows,
+                                    ops.GATE_LATENT_DIFF, g.rule, False, g.round_hazard, g.min_steps, g.max_steps,
+                                    g.threshold)
 
     def _coda_hidden(self, state: torch.Tensor, attend) -> torch.Tensor:
         """ln_f -> coda blocks -> ln_f (huginn/modeling_huginn.py:456-463)."""

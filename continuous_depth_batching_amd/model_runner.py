@@ -678,10 +678,11 @@ class ModelRunner:
             return
         slots = [self.layout.slot_for_step(s) for s in exit_steps]
         with self._on_stream():
-            ops.exit_kv_copy_raw(self.cache.view, self._to_device(np.asarray(rows, dtype=np.int64), torch.int64),
-                                 self._to_device(np.asarray(slots, dtype=np.int32), torch.int32), len(rows),
-                                 layer_base=self.layout.core_base, core_layers=self.layout.num_core_layers,
-                                 num_slots=self.layout.slots_per_layer)
+            torch.ops.cdb.exit_kv_copy(self.cache.pool, self.cache.block_size,
+                                       self._to_device(np.asarray(rows, dtype=np.int64), torch.int64),
+                                       self._to_device(np.asarray(slots, dtype=np.int32), torch.int32), len(rows),
+                                       self.layout.core_base, self.layout.num_core_layers,
+                                       self.layout.slots_per_layer)
 
     # -- KV swap (offload pressure mode) -------------------------------------------------------------------------
     def make_kv_swap_pool(self, num_host_blocks: int) -> KvSwapPool:

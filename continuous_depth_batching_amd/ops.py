@@ -21,10 +21,9 @@ _DTYPE_CODES = {torch.float32: _lib.CDB_DTYPE_F32, torch.bfloat16: _lib.CDB_DTYP
 
 # Decode-attention KV chunk length in pages: ADAPTIVE_SPLIT uses MIN_SPLIT_PAGES (a
 # negative value -m uses m). Chunks are lengthened only when the workspace cannot
-# hold a launch's chunks. MAX_SPLIT_PAGES is passed where the C ABI still takes it.
+# hold a launch's chunks.
 ADAPTIVE_SPLIT = 0
 MIN_SPLIT_PAGES = 8
-MAX_SPLIT_PAGES = 32
 
 # Stages of cdb_paged_decode_attention_staged (include/cdb_amd.h).
 DECODE_PLAN = _lib.CDB_DECODE_STAGE_PLAN
@@ -146,7 +145,6 @@ def paged_decode_attention_raw(
     split_pages: int,
     scale: float,
     min_split_pages: int = MIN_SPLIT_PAGES,
-    max_split_pages: int = MAX_SPLIT_PAGES,
     stages: int = DECODE_PLAN_AND_ATTEND,
 ) -> torch.Tensor:
     """Launch ``cdb_paged_decode_attention`` on explicit pool pointers (no allocation).
@@ -201,7 +199,7 @@ def paged_decode_attention_raw(
             num_rows, num_heads, num_kv_heads, head_dim, block_size, split_pages, min_split_pages)
     tail = (scale, q.stride(0), k_new.stride(0), dtype_code(q.dtype))
     if stages == DECODE_PLAN_AND_ATTEND:
-        code = _lib.lib().cdb_paged_decode_attention(*head, max_split_pages, *tail, _stream())
+        code = _lib.lib().cdb_paged_decode_attention(*head, *tail, _stream())
         _lib.check(code, "cdb_paged_decode_attention")
     else:
         code = _lib.lib().cdb_paged_decode_attention_staged(*head, *tail, stages, _stream())
@@ -860,6 +858,30 @@ def exit_gate_raw(hidden: torch.Tensor, prev: torch.Tensor | None, weight: torch
     _lib.check(code, "cdb_exit_gate")
 
 
+@torch.library.custom_op("cdb::exit_gate", mutates_args=("signal", "cdf", "survival", "pending", "exit_flags"),
+                        device_types="cuda")
+def exit_gate(hidden: torch.Tensor, prev: torch.Tensor | None, weight: torch.Tensor | None, bias: torch.Tensor | None,
+              signal: torch.Tensor, cdf: torch.Tensor, survival: torch.Tensor, pending: torch.Tensor,
+              state_index: torch.Tensor, steps: torch.Tensor, synthetic_depth: torch.Tensor | None,
+              exit_flags: torch.Tensor, rows: int, kind: int, rule: int, delayed: bool, round_hazard: bool,
+              min_steps: int, max_steps: int, threshold: float | None) -> None:
+    """The exit gate of one recurrent launch's first ``rows`` rows (cdb/adapters/ouro.py:286-291,
+    cdb/exit_policy.py:150-169, huginn/exit_gates.py:33-40): the gate signal per row (``kind``
+    GATE_HAZARD: the bf16 Linear(E, 1) logit; GATE_LATENT_DIFF: the relative L2 change against
+    ``prev``), the per-token policy state (``cdf``, ``survival``, ``pending``, indexed by
+    ``state_index``) and one exit byte per row in ``exit_flags``, all updated in place."""
+
+    exit_gate_raw(hidden, prev, weight, bias, signal, GateState(cdf=cdf, survival=survival, pending=pending),
+                  state_index, steps, synthetic_depth, exit_flags, rows, kind=kind, rule=rule, delayed=delayed,
+                  round_hazard=round_hazard, min_steps=min_steps, max_steps=max_steps, threshold=threshold)
+
+
+@exit_gate.register_fake
+def _(hidden, prev, weight, bias, signal, cdf, survival, pending, state_index, steps, synthetic_depth, exit_flags,
+      rows, kind, rule, delayed, round_hazard, min_steps, max_steps, threshold):
+    return None
+
+
 def exit_kv_copy_raw(view: KVPoolView, rows: torch.Tensor, exit_slot: torch.Tensor, n: int, *, layer_base: int,
                      core_layers: int, num_slots: int) -> None:
     """Copy each exiting token's exit-slot KV into its deeper slots (copy-on-exit layout)."""
@@ -874,6 +896,23 @@ def exit_kv_copy_raw(view: KVPoolView, rows: torch.Tensor, exit_slot: torch.Tens
                                        pool.shape[4], rows.data_ptr(), exit_slot.data_ptr(), n, layer_base,
                                        core_layers, num_slots, dtype_code(pool.dtype), _stream())
     _lib.check(code, "cdb_exit_kv_copy")
+
+
+@torch.library.custom_op("cdb::exit_kv_copy", mutates_args=("kv_pool",), device_types="cuda")
+def exit_kv_copy(kv_pool: torch.Tensor, block_size: int, rows: torch.Tensor, exit_slot: torch.Tensor, n: int,
+                 layer_base: int, core_layers: int, num_slots: int) -> None:
+    """Exit-KV propagation under a copy-on-exit KV layout (cdb/continuous_api.py:1225-1245,
+    cdb/cache.py:99-113): token i's K/V row ``rows[i]`` of cache layer
+    ``layer_base + exit_slot[i] * core_layers + l`` is copied to every deeper slot's layer, for all
+    core layers l, in ``kv_pool`` [num_cache_layers, 2, pool_rows, Hkv, D]."""
+
+    exit_kv_copy_raw(KVPoolView(kv_pool, block_size), rows, exit_slot, n, layer_base=layer_base,
+                     core_layers=core_layers, num_slots=num_slots)
+
+
+@exit_kv_copy.register_fake
+def _(kv_pool, block_size, rows, exit_slot, n, layer_base, core_layers, num_slots):
+    return None
 
 
 def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: torch.Tensor, view: KVPoolView,
@@ -906,6 +945,28 @@ def rope_kv_write_raw(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_out: 
         0 if rope_cos is None else rope_cos.shape[0], _ptr(q_bias), _ptr(k_bias), tokens, num_heads,
         num_kv_heads, head_dim, q.stride(0), k.stride(0), dtype_code(q.dtype), _stream())
     _lib.check(code, "cdb_rope_kv_write")
+
+
+@torch.library.custom_op("cdb::rope_kv_write", mutates_args=("kv_pool",), device_types="cuda")
+def rope_kv_write(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_pool: torch.Tensor, layer: int,
+                  block_size: int, rows: torch.Tensor, positions: torch.Tensor, rope_cos: torch.Tensor | None,
+                  rope_sin: torch.Tensor | None, rope_style: int, q_bias: torch.Tensor | None,
+                  k_bias: torch.Tensor | None) -> torch.Tensor:
+    """RoPE + KV append of a prefill chunk's T tokens (cb/cache.py:284-318 with the write indices
+    of cb/cache_manager.py:190-213; ouro/modeling_ouro.py:179-204, huginn/modeling_huginn.py:178-196
+    and its qk_bias): token t's rotated key and its value go to pool row ``rows[t]`` of cache layer
+    ``layer`` in ``kv_pool`` [num_cache_layers, 2, pool_rows, Hkv, D]; returns the rotated queries
+    [T, H, D]. q, k and v may be column slices of one fused QKV output."""
+
+    q_rot = q.new_empty(q.shape)
+    rope_kv_write_raw(q, k, v, q_rot, KVPoolView(kv_pool, block_size), layer, rows, positions, rope_cos, rope_sin,
+                      rope_style, q_bias, k_bias)
+    return q_rot
+
+
+@rope_kv_write.register_fake
+def _(q, k, v, kv_pool, layer, block_size, rows, positions, rope_cos, rope_sin, rope_style, q_bias, k_bias):
+    return q.new_empty(q.shape)
 
 
 PREFILL_TILE = 128
@@ -1058,18 +1119,57 @@ def prefill_attention_split_raw(q: torch.Tensor, view: KVPoolView, layer: int, b
     _lib.check(code, "cdb_prefill_attention_split")
 
 
-def prefill_attention_launch(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor, launch,
-                             out: torch.Tensor, scale: float) -> None:
+@torch.library.custom_op("cdb::prefill_attention", mutates_args=(), device_types="cuda")
+def prefill_attention(q: torch.Tensor, kv_pool: torch.Tensor, layer: int, block_size: int,
+                      block_table: torch.Tensor, table_row: torch.Tensor, cu_q: torch.Tensor, past: torch.Tensor,
+                      tile_seq: torch.Tensor, tile_q0: torch.Tensor, scale: float) -> torch.Tensor:
+    """Causal varlen prefill attention over [past | new] through the block table
+    (cb/prefill_graph.py:265-309, flash_attn_varlen_func): sequence s's queries
+    q[cu_q[s]:cu_q[s + 1]] sit at positions past[s]... and attend over the K/V of cache layer
+    ``layer`` in ``kv_pool``, read through block-table row table_row[s]. Tiles of 128 queries are
+    listed by (tile_seq, tile_q0) (prefill_tiles). Returns [T, H, D]."""
+
+    out = q.new_empty(q.shape)
+    prefill_attention_raw(q, KVPoolView(kv_pool, block_size), layer, block_table, table_row, cu_q, past, tile_seq,
+                          tile_q0, out, scale)
+    return out
+
+
+@prefill_attention.register_fake
+def _(q, kv_pool, layer, block_size, block_table, table_row, cu_q, past, tile_seq, tile_q0, scale):
+    return q.new_empty(q.shape)
+
+
+@torch.library.custom_op("cdb::prefill_attention_split", mutates_args=("partials",), device_types="cuda")
+def prefill_attention_split(q: torch.Tensor, kv_pool: torch.Tensor, layer: int, block_size: int,
+                            block_table: torch.Tensor, table_row: torch.Tensor, cu_q: torch.Tensor,
+                            past: torch.Tensor, items: torch.Tensor, merges: torch.Tensor, num_slots: int,
+                            partials: torch.Tensor, scale: float) -> torch.Tensor:
+    """cdb::prefill_attention with long tiles' key ranges split over workgroups and merged
+    (prefill_split_work): ``partials`` is scratch of at least prefill_partial_bytes(num_slots)."""
+
+    out = q.new_empty(q.shape)
+    prefill_attention_split_raw(q, KVPoolView(kv_pool, block_size), layer, block_table, table_row, cu_q, past,
+                                items, merges, num_slots, partials, out, scale)
+    return out
+
+
+@prefill_attention_split.register_fake
+def _(q, kv_pool, layer, block_size, block_table, table_row, cu_q, past, items, merges, num_slots, partials, scale):
+    return q.new_empty(q.shape)
+
+
+def prefill_attention_launch(q: torch.Tensor, kv_pool: torch.Tensor, layer: int, block_size: int,
+                             block_table: torch.Tensor, launch, scale: float) -> torch.Tensor:
     """Prefill attention of one layer for a prefill launch (model_adapter.PrefillLaunch): the
     split work list when the launch carries one, else its whole tiles."""
 
     if launch.split_items is not None:
-        prefill_attention_split_raw(q, view, layer, block_table, launch.table_rows, launch.cu_q, launch.past,
-                                    launch.split_items, launch.split_merges, launch.split_slots, launch.partials,
-                                    out, scale)
-    else:
-        prefill_attention_raw(q, view, layer, block_table, launch.table_rows, launch.cu_q, launch.past,
-                              launch.tile_seq, launch.tile_q0, out, scale)
+        return torch.ops.cdb.prefill_attention_split(q, kv_pool, layer, block_size, block_table, launch.table_rows,
+                                                     launch.cu_q, launch.past, launch.split_items,
+                                                     launch.split_merges, launch.split_slots, launch.partials, scale)
+    return torch.ops.cdb.prefill_attention(q, kv_pool, layer, block_size, block_table, launch.table_rows, launch.cu_q,
+                                           launch.past, launch.tile_seq, launch.tile_q0, scale)
 
 
 def prefill_attention_raw(q: torch.Tensor, view: KVPoolView, layer: int, block_table: torch.Tensor,

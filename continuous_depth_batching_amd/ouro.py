@@ -336,9 +336,9 @@ class OuroCDBAdapter(CDBModelAdapter):
         g = launch.gate
         if g.enabled:
             kind, w, b = self.gate_params()
-            ops.exit_gate_raw(hidden, None, w, b, g.signal, g.state, launch.bank_slots, g.steps, g.synthetic,
-                              g.flags, rows, kind=kind, rule=g.rule, delayed=False, round_hazard=g.round_hazard,
-                              min_steps=g.min_steps, max_steps=g.max_steps, threshold=g.threshold)
+            torch.ops.cdb.exit_gate(hidden, None, w, b, g.signal, g.state.cdf, g.state.survival, g.state.pending,
+                                    launch.bank_slots, g.steps, g.synthetic, g.flags, rows, kind, g.rule, False,
+                                    g.round_hazard, g.min_steps, g.max_steps, g.threshold)
 
     def prefill(self, launch: PrefillLaunch) -> torch.Tensor:
         cache = launch.cache
@@ -356,12 +356,10 @@ class OuroCDBAdapter(CDBModelAdapter):
                 q = qkv[:, :q_w].view(tokens, self.num_heads, hd)
                 k = qkv[:, q_w:q_w + kv_w].view(tokens, self.num_kv_heads, hd)
                 v = qkv[:, q_w + kv_w:].view(tokens, self.num_kv_heads, hd)
-                q_rot = torch.empty((tokens, self.num_heads, hd), dtype=qkv.dtype, device=qkv.device)
-                ops.rope_kv_write_raw(q, k, v, q_rot, cache.view, layer, launch.write_rows, launch.positions,
-                                      self.rope_cos, self.rope_sin, 1, None, None)
-                out = torch.empty_like(q_rot)
-                ops.prefill_attention_launch(q_rot, cache.view, layer, cache.device_table, launch, out, self.scale)
-                return out
+                q_rot = torch.ops.cdb.rope_kv_write(q, k, v, cache.pool, layer, cache.block_size, launch.write_rows,
+                                                    launch.positions, self.rope_cos, self.rope_sin, 1, None, None)
+                return ops.prefill_attention_launch(q_rot, cache.pool, layer, cache.block_size, cache.device_table,
+                                                    launch, self.scale)
 
             hidden = self._layer_stack(x, residual, attend)
         last = torch.ops.cdb.gather_rows(hidden, launch.last_index)

@@ -46,7 +46,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _P, _P,  # q_bias, k_bias
             _P, _P, c_int64,  # out, workspace, workspace_bytes
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
-            c_int32, c_int32,  # min/max split pages (split_pages <= 0)
+            c_int32,  # min_split_pages (split_pages <= 0)
             c_float, c_int64, c_int64, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stream
         ],
     ),
@@ -78,7 +78,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
             _P, _P,  # q_bias, k_bias
             _P,  # out
             c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # rows, H, Hkv, D, block_size, split_pages
-            c_int32, c_int32,  # min/max split pages (split_pages <= 0)
+            c_int32,  # min_split_pages (split_pages <= 0)
             c_float, c_int64, c_int64, c_int32, _P,  # scale, q_stride, kv_stride, dtype, stream
         ],
     ),

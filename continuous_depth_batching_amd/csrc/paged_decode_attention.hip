@@ -84,6 +84,7 @@ struct DecodeParams {
   void* out;                    // [B, H, D]
   int32_t* header;              // [B + 2]: chunk tokens, then the chunk prefix over rows
   int32_t* counters;            // [kQueues * kCounterStride]: per-XCD item queues of the fast form
+  int32_t* arrivals;            // [B * H]: chunks of each (row, head) finished in the current deep-form call
   int32_t* desc;                // [capacity][kDescInts]
   float* partial;               // [capacity, H, D + 2]
   int64_t layer_stride;         // elements between cache layers
@@ -96,6 +97,7 @@ struct DecodeParams {
   int32_t num_cache_layers;     // valid cache layers are [0, num_cache_layers)
   int64_t pool_blocks;          // valid block ids are [0, pool_blocks)
   int64_t capacity;             // chunks the workspace holds (descriptors and partials)
+  int32_t self_merge;           // deep form: merge and fill in the decode kernel (no merge launch)
   float scale_log2;             // softmax scale * log2(e)
 };
 
@@ -239,6 +241,7 @@ __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(DecodeParams 
   for (int b = tid; b <= B; b += kPlanThreads) P.header[1 + b] = chunk_prefix[b];
   if (tid == 0) P.header[0] = chunk_tokens;
   if (tid < kQueues) P.counters[tid * kCounterStride] = 0;
+  for (int i = tid; i < B * P.num_heads; i += kPlanThreads) P.arrivals[i] = 0;
   // One thread per chunk (in partial-slot order): a long row's descriptors are written in parallel.
   const int total_chunks = chunk_prefix[B];
   for (int ci = tid; ci < total_chunks; ci += kPlanThreads) {
@@ -280,6 +283,7 @@ __global__ void __launch_bounds__(kPlanThreads) decode_plan_kernel(DecodeParams 
 // at use so that two items (the current and the next) stay cheap to hold.
 struct Item {
   int b, h, t_begin, t_end, p, partial, trow, layer;
+  int nsplit;               // chunks of the row (0 for a descriptor no plan could have written)
   bool last, single, live;  // live: the row's cache layer exists in this call
 };
 
@@ -310,6 +314,7 @@ CDB_DEVICE Item make_item(const DecodeParams& P, const RawDesc& r, int h) {
   it.p = r.a.w;
   it.partial = r.b.x;
   const int nsplit = r.b.y;
+  it.nsplit = nsplit;
   it.single = nsplit == 1;
   it.h = h;
   const int layer_offset = r.b.w;
@@ -323,7 +328,7 @@ CDB_DEVICE Item make_item(const DecodeParams& P, const RawDesc& r, int h) {
                     it.partial < P.capacity;
   it.live = sane && layer_in_range(P, layer_offset);
   if (!sane) {
-    it.b = it.p = it.partial = 0;
+    it.b = it.p = it.partial = it.nsplit = 0;
     it.single = it.last = false;
   }
   it.t_end = it.live ? t_end : it.t_begin;
@@ -920,11 +925,14 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
   // Items in the plan's longest-first order: wave w takes items w, w + W, ...
   // for its static rounds (no coordination); the remaining items, the tail of
   // the launch, go to whichever wave asks first, from the queue of
-  // its workgroup's XCD (queue x holds tail items x, x + 8, ...). A wave asks
+  // its workgroup's XCD (queue x of n holds tail items x, x + n, ...). A wave asks
   // when it starts its last static item, so the request's round trip overlaps
   // that item's stream, and waves that stream faster take more of the tail.
   const int nwaves = gridDim.x * 4;
-  const int queue = blockIdx.x % kQueues;
+  // A grid of fewer than kQueues workgroups uses only as many queues as it has
+  // workgroups, so every queue that holds tail items is drained.
+  const int nqueues = min((int)gridDim.x, kQueues);
+  const int queue = blockIdx.x % nqueues;
   int32_t* const counter = P.counters + queue * kCounterStride;
   const auto grab = [&]() {
     int k = 0;
@@ -972,9 +980,10 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
     auto know_next = [&]() {
       if (next_known) return;
       next_known = true;
-      next = static_next ? wave_id + round * nwaves
-                         : has_tail ? tail_base + uniform(ticket) * kQueues + queue : n_items;
-      has_next = next < n_items;
+      // A negative ticket (queue counters that no plan reset) selects no item.
+      const int t = static_next || !has_tail ? -1 : uniform(ticket);
+      next = static_next ? wave_id + round * nwaves : t >= 0 ? tail_base + t * nqueues + queue : n_items;
+      has_next = next >= 0 && next < n_items;
       d_next = load_fast_desc(P, has_next ? next / H : 0);
     };
     const Item& c = cur.it;
@@ -1111,6 +1120,63 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
 // new-token and slot merge), so a row's result does not depend on the form.
 constexpr int kDeepRows = 120;  // the deep form measured faster than the fast form up to 120 rows
 constexpr int kDeepSteps = 4;
+// Deep-form launches of at most this many rows merge in the decode kernel. Against the merge
+// launch (same box, per layer): 0.7-1.4 us faster from 1 to 32 rows, even at 48, 1.3-1.6 us slower
+// at 96-120 rows, where the last arrivers' count and coherent reads outlast a separate launch.
+constexpr int kSelfMergeRows = 48;
+
+template <typename T, int D, bool kCoherent = false>
+CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int lane, T* out_row);
+
+// Agent-coherent float accesses: the eight XCDs' L2s do not share dirty lines, and these go to
+// the point where all of them agree (sc1), without writing back or invalidating a whole L2.
+CDB_DEVICE void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+CDB_DEVICE float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The deep form merges without a launch of its own. Every item of a multi-chunk row stores its
+// partial with agent-coherent stores, waits until they are performed, and counts itself in its
+// (row, head)'s arrival counter (a vector atomic, coherent across the XCDs). The wave that arrives
+// last reads the row's partials with agent-coherent loads, merges them in chunk order with the
+// merge launch's own arithmetic (so a row's output does not depend on the form), and resets the
+// counter for the next call.
+template <typename T, int D>
+CDB_DEVICE void finish_row_head(const DecodeParams& P, const Item& c, int lane) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are performed
+  int32_t* const counter = P.arrivals + (int64_t)c.b * P.num_heads + c.h;
+  int ticket = 0;
+  if (lane == 0) ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (uniform(ticket) != c.nsplit - 1) return;
+  asm volatile("" ::: "memory");  // no partial load moves above the arrival count
+  T* out_row = static_cast<T*>(P.out) + ((int64_t)c.b * P.num_heads + c.h) * D;
+  const int first = P.header[1 + c.b];
+  if (c.live && first >= 0 && first + (int64_t)c.nsplit <= P.capacity) {
+    const int64_t stride = (int64_t)P.num_heads * (D + 2);
+    merge_chunks<T, D, true>(P.partial + (int64_t)first * stride + (int64_t)c.h * (D + 2), stride, c.nsplit,
+                             lane, out_row);
+  } else {
+    for (int d = lane; d < D; d += 64) Elem<T>::store(out_row + d, __builtin_nanf(""));
+  }
+  if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Output of the rows that have no chunks, which the merge launch fills in the other forms: zeros
+// for padding rows, NaN for rows whose position is out of range. Wave w takes (row, head) pairs
+// w, w + W, ...
+template <typename T, int D>
+CDB_DEVICE void fill_chunkless_rows(const DecodeParams& P, int wave_id, int nwaves, int lane) {
+  const int H = P.num_heads;
+  for (int pr = wave_id; pr < P.num_rows * H; pr += nwaves) {
+    const int b = pr / H;
+    if (P.header[2 + b] != P.header[1 + b]) continue;
+    const float fill = P.seqlens[b] < 0 ? 0.f : __builtin_nanf("");
+    T* out_row = static_cast<T*>(P.out) + (int64_t)pr * D;
+    for (int d = lane; d < D; d += 64) Elem<T>::store(out_row + d, fill);
+  }
+}
 
 template <typename T, int D, int R>
 __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams P) {
@@ -1123,7 +1189,8 @@ __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams 
   const int nwaves = gridDim.x * 4;
   const int chunks = *(const const_int32*)(P.header + 1 + P.num_rows);
   const int n_items = (int)min((int64_t)chunks, P.capacity) * H;
-  for (int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6)); item < n_items; item += nwaves) {
+  const int wave_id = uniform(blockIdx.x * 4 + (threadIdx.x >> 6));
+  for (int item = wave_id; item < n_items; item += nwaves) {
     const FastItem cur = make_fast_item(P, load_fast_desc(P, item / H), item % H);
     const Item& c = cur.it;
     const int kvh = c.h / kv_group;
@@ -1223,15 +1290,26 @@ __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams 
         o.store(out_row + chunk * C);
       } else if (c.live) {
         float* part = P.partial + ((int64_t)c.partial * H + c.h) * (D + 2);
+        if (P.self_merge) {
 #pragma unroll
-        for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
-        if (chunk == 0) {
-          part[D] = m_all;
-          part[D + 1] = l;
+          for (int i = 0; i < C; ++i) store_coherent(part + chunk * C + i, acc[i]);
+          if (chunk == 0) {
+            store_coherent(part + D, m_all);
+            store_coherent(part + D + 1, l);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
+          if (chunk == 0) {
+            part[D] = m_all;
+            part[D + 1] = l;
+          }
         }
       }
     }
+    if (P.self_merge && !c.single && c.nsplit > 1) finish_row_head<T, D>(P, c, lane);
   }
+  if (P.self_merge) fill_chunkless_rows<T, D>(P, wave_id, nwaves, lane);
 }
 
 // The merge of one (row, head): chunk c's partial (unnormalized accumulator of
@@ -1239,8 +1317,9 @@ __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams 
 // chunk s's (max, sum) so the global max and the denominator are wave
 // reductions; the accumulators are read eight chunks at a time so their loads
 // are in flight together.
-template <typename T, int D>
+template <typename T, int D, bool kCoherent>
 CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int lane, T* out_row) {
+  const auto ld = [](const float* p) { return kCoherent ? load_coherent(p) : *p; };
   const int d0 = lane, d1 = lane + 64;
   float run_m = -INFINITY, den = 0.f, num0 = 0.f, num1 = 0.f;
   for (int base = 0; base < nsplit; base += 64) {
@@ -1252,8 +1331,8 @@ CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int 
       for (int j = 0; j < 8; ++j) {
         const bool ok = s0 + j < cnt;
         const float* ps = chunk_part + (int64_t)(s0 + j) * stride;
-        a0[j] = ok && d0 < D ? ps[d0] : 0.f;
-        a1[j] = ok && d1 < D ? ps[d1] : 0.f;
+        a0[j] = ok && d0 < D ? ld(ps + d0) : 0.f;
+        a1[j] = ok && d1 < D ? ld(ps + d1) : 0.f;
       }
     };
     // The first eight chunks' accumulators are read with the (max, sum) pairs, so
@@ -1261,8 +1340,8 @@ CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int 
     load_group(0);
     float ms = -INFINITY, ls = 0.f;
     if (lane < cnt) {
-      ms = chunk_part[lane * stride + D];
-      ls = chunk_part[lane * stride + D + 1];
+      ms = ld(chunk_part + lane * stride + D);
+      ls = ld(chunk_part + lane * stride + D + 1);
     }
     const float new_m = fmaxf(run_m, wave_max(ms));
     const float keep = run_m == -INFINITY ? 0.f : exp2f(run_m - new_m);
@@ -1354,8 +1433,13 @@ int ilog2_exact(int x) {
   return r;
 }
 
+// Workspace: the header (chunk tokens, chunk prefix over rows), the queue counters, the
+// arrival counters (one per row and head), each 256-byte aligned; then descriptors and partials.
 int64_t counters_offset(int64_t num_rows) { return ((num_rows + 2) * 4 + 255) / 256 * 256; }
-int64_t header_bytes(int64_t num_rows) { return counters_offset(num_rows) + kQueues * kCounterStride * 4; }
+int64_t arrivals_offset(int64_t num_rows) { return counters_offset(num_rows) + kQueues * kCounterStride * 4; }
+int64_t header_bytes(int64_t num_rows, int64_t num_heads) {
+  return arrivals_offset(num_rows) + (num_rows * num_heads * 4 + 255) / 256 * 256;
+}
 
 int64_t bytes_per_chunk(int64_t num_heads, int64_t head_dim) {
   return kDescBytes + num_heads * (head_dim + 2) * (int64_t)sizeof(float);
@@ -1388,10 +1472,13 @@ int launch_decode(const DecodeParams& P, int stages, int num_cus, hipStream_t st
     if (hipGetLastError() != hipSuccess) return CDB_ERR_HIP;
   }
   if (!(stages & CDB_DECODE_STAGE_ATTEND)) return CDB_OK;
-  const int rc = !fast_form(P)              ? launch_persistent(paged_decode_kernel<T, D, R>, P, num_cus, stream)
-                 : P.num_rows <= kDeepRows ? launch_persistent(paged_decode_deep_kernel<T, D, R>, P, num_cus, stream)
-                                           : launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream);
+  const bool deep = fast_form(P) && P.num_rows <= kDeepRows;
+  const int rc = !fast_form(P) ? launch_persistent(paged_decode_kernel<T, D, R>, P, num_cus, stream)
+                 : deep        ? launch_persistent(paged_decode_deep_kernel<T, D, R>, P, num_cus, stream)
+                               : launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream);
   if (rc != CDB_OK) return rc;
+  // A self-merging deep launch has merged and filled every row; the others end with the merge launch.
+  if (deep && P.self_merge) return CDB_OK;
   const int64_t waves = (int64_t)P.num_rows * P.num_heads;
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, P);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
@@ -1451,7 +1538,7 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
     return -1;
   const int64_t split_tokens = (int64_t)split_pages * block_size;
   const int64_t max_splits = (max_seqlen + split_tokens - 1) / split_tokens + 1;
-  return header_bytes(num_rows) + (int64_t)num_rows * max_splits * bytes_per_chunk(num_heads, head_dim);
+  return header_bytes(num_rows, num_heads) + (int64_t)num_rows * max_splits * bytes_per_chunk(num_heads, head_dim);
 }
 
 int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
@@ -1462,9 +1549,8 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t rope_style, int32_t max_positions, const void* q_bias, const void* k_bias,
                                void* out, void* workspace, int64_t workspace_bytes, int32_t num_rows,
                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                               int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages, float scale,
+                               int32_t split_pages, int32_t min_split_pages, float scale,
                                int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream) {
-  (void)max_split_pages;
   return decode_attention(q, k_new, v_new, k_pool, v_pool, layer_stride, num_cache_layers, pool_blocks, cache_layer,
                           cache_layer0, block_table, table_row, table_width, seqlens, rope_cos, rope_sin, rope_style,
                           max_positions, q_bias, k_bias, out, workspace, workspace_bytes, num_rows, num_heads,
@@ -1499,15 +1585,14 @@ int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const v
                                        int32_t rope_style, int32_t max_positions, const void* q_bias,
                                        const void* k_bias, void* out, int32_t num_rows, int32_t num_heads,
                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                       int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages,
+                                       int32_t split_pages, int32_t min_split_pages,
                                        float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype,
                                        hipStream_t stream) {
-  (void)max_split_pages;
   if (num_rows == 0) return CDB_OK;
   if (num_rows < 0 || num_heads <= 0 || head_dim <= 0) return CDB_ERR_SHAPE;
   // The plan lengthens chunks until they fit, down to one chunk per row: the scratch must hold
   // the header and one descriptor and partial per row.
-  const int64_t need = header_bytes(num_rows) + (int64_t)num_rows * bytes_per_chunk(num_heads, head_dim);
+  const int64_t need = header_bytes(num_rows, num_heads) + (int64_t)num_rows * bytes_per_chunk(num_heads, head_dim);
   if (need > CDB_DECODE_SCRATCH_BYTES) return CDB_ERR_CAPACITY;
   void* ws = nullptr;
   const int rc = scratch_address(&ws);
@@ -1550,7 +1635,7 @@ int decode_attention(const void* q, const void* k_new, const void* v_new, void* 
   // Split-half rotation pairs chunk c with chunk c ^ 8, i.e. D/2 = 8 chunks.
   if (rope_style == 1 && (head_dim / 16) * 8 != head_dim / 2) return CDB_ERR_UNSUPPORTED;
   if (num_cache_layers <= 0 || pool_blocks <= 0 || layer_stride < 0) return CDB_ERR_SHAPE;
-  const int64_t header = header_bytes(num_rows);
+  const int64_t header = header_bytes(num_rows, num_heads);
   const int64_t capacity = workspace_bytes > header ? (workspace_bytes - header) / bytes_per_chunk(num_heads, head_dim) : 0;
   // One chunk per row must fit; the item index (chunk * heads) must fit an int.
   if (capacity < num_rows) return CDB_ERR_CAPACITY;
@@ -1562,6 +1647,7 @@ int decode_attention(const void* q, const void* k_new, const void* v_new, void* 
   P.q_bias = q_bias; P.k_bias = k_bias; P.out = out;
   P.header = static_cast<int32_t*>(workspace);
   P.counters = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + counters_offset(num_rows));
+  P.arrivals = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + arrivals_offset(num_rows));
   P.capacity = capacity < ((int64_t)1 << 31) / num_heads ? capacity : ((int64_t)1 << 31) / num_heads - 1;
   P.desc = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + header);
   P.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + header + capacity * kDescBytes);
@@ -1574,6 +1660,7 @@ int decode_attention(const void* q, const void* k_new, const void* v_new, void* 
   P.rope_style = rope_style; P.max_positions = max_positions;
   P.num_cache_layers = num_cache_layers; P.pool_blocks = pool_blocks;
   P.scale_log2 = scale * 1.4426950408889634f;
+  P.self_merge = num_rows <= kSelfMergeRows;
 
   if (g_num_cus == 0) {
     int dev = 0;

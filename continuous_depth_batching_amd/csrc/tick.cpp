@@ -1506,6 +1506,16 @@ PyObject* coda_upload(PyObject*, PyObject* args) {
     upload[i] = slot;
   }
   if (k == 0) return PyLong_FromLong(next_slot);
+  // Every successor row is checked before any hidden slot is taken, so a bad row leaves the
+  // free list and the slot counter as they were.
+  for (Py_ssize_t j = 0; j < k; ++j) {
+    const long row = PyLong_AsLong(PyList_GET_ITEM(rows, j));
+    if (row == -1 && PyErr_Occurred()) return nullptr;
+    if (row < 0 || row >= n) {
+      PyErr_Format(PyExc_ValueError, "coda_upload: successor row %ld outside the %zd coda rows", row, n);
+      return nullptr;
+    }
+  }
   for (Py_ssize_t i = 0; i < n; ++i) upload[n + i] = -1;
   for (Py_ssize_t j = 0; j < k; ++j) {
     long slot;
@@ -1522,11 +1532,6 @@ PyObject* coda_upload(PyObject*, PyObject* args) {
       slot = next_slot++;
     }
     const long row = PyLong_AsLong(PyList_GET_ITEM(rows, j));
-    if (row == -1 && PyErr_Occurred()) return nullptr;
-    if (row < 0 || row >= n) {
-      PyErr_Format(PyExc_ValueError, "coda_upload: successor row %ld outside the %zd coda rows", row, n);
-      return nullptr;
-    }
     upload[n + row] = slot;
     upload[2 * n + j] = slot;
     if (!set_long(PyList_GET_ITEM(successors, j), s_hidden_slot, slot)) return nullptr;

@@ -71,8 +71,7 @@ int64_t cdb_paged_decode_workspace_bytes(int32_t num_rows, int32_t num_heads, in
  * k_new/v_new (0 = dense), so q, k and v may be column slices of one fused
  * QKV projection output.
  * Each row's context is cut into chunks of split_pages pages (min_split_pages
- * when split_pages <= 0; max_split_pages is not used and kept for the ABI),
- * processed in parallel and merged in chunk order, so a row's output does not
+ * when split_pages <= 0), processed in parallel and merged in chunk order, so a row's output does not
  * depend on which other rows share the launch. Only a workspace too small for
  * the launch's chunks lengthens them.
  * Returns CDB_ERR_CAPACITY when workspace_bytes cannot hold the header and one
@@ -85,7 +84,7 @@ int cdb_paged_decode_attention(const void* q, const void* k_new, const void* v_n
                                int32_t max_positions, const void* q_bias, const void* k_bias, void* out,
                                void* workspace, int64_t workspace_bytes, int32_t num_rows, int32_t num_heads,
                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t split_pages,
-                               int32_t min_split_pages, int32_t max_split_pages, float scale,
+                               int32_t min_split_pages, float scale,
                                int64_t q_stride, int64_t kv_stride, int32_t dtype, hipStream_t stream);
 
 /* Stages of cdb_paged_decode_attention_staged. */
@@ -133,7 +132,7 @@ int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const v
                                        int32_t rope_style, int32_t max_positions, const void* q_bias,
                                        const void* k_bias, void* out, int32_t num_rows, int32_t num_heads,
                                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                       int32_t split_pages, int32_t min_split_pages, int32_t max_split_pages,
+                                       int32_t split_pages, int32_t min_split_pages,
                                        float scale, int64_t q_stride, int64_t kv_stride, int32_t dtype,
                                        hipStream_t stream);
 

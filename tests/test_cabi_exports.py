@@ -41,11 +41,12 @@ def test_binding_covers_every_declared_symbol() -> None:
 def test_workspace_size_query_without_gpu() -> None:
     lib = _lib.lib()
     # A header (chunk size + chunk prefix of the rows, padded to 256 bytes, then 1 KiB of item-queue
-    # counters), then ceil(100 / 32) + 1 chunks per row, each a 64-byte descriptor and (D + 2) floats
-    # per head.
+    # counters, then one arrival counter per row and head, padded to 256 bytes), then
+    # ceil(100 / 32) + 1 chunks per row, each a 64-byte descriptor and (D + 2) floats per head.
     per_chunk = 64 + 16 * 130 * 4
-    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 256 + 1024 + 4 * 5 * per_chunk
-    assert lib.cdb_paged_decode_workspace_bytes(100, 16, 128, 100, 16, 2) == 512 + 1024 + 100 * 5 * per_chunk
+    assert lib.cdb_paged_decode_workspace_bytes(4, 16, 128, 100, 16, 2) == 256 + 1024 + 256 + 4 * 5 * per_chunk
+    assert lib.cdb_paged_decode_workspace_bytes(100, 16, 128, 100, 16, 2) == \
+        512 + 1024 + 6400 + 100 * 5 * per_chunk
     assert lib.cdb_paged_decode_workspace_bytes(-1, 16, 128, 100, 16, 2) == -1
 
 
@@ -58,7 +59,7 @@ def _decode_args(**over):
                 table_row=None, table_width=8, seqlens=fake, rope_cos=fake, rope_sin=fake, rope_style=1,
                 max_positions=128, q_bias=None, k_bias=None, out=fake, workspace=fake, workspace_bytes=1 << 20,
                 num_rows=4, num_heads=16, num_kv_heads=16, head_dim=128, block_size=16, split_pages=0,
-                min_split_pages=2, max_split_pages=64, scale=0.088, q_stride=0, kv_stride=0, dtype=1, stream=None)
+                min_split_pages=2, scale=0.088, q_stride=0, kv_stride=0, dtype=1, stream=None)
     args.update(over)
     return list(args.values())
 
@@ -75,7 +76,7 @@ def test_decode_argument_errors_without_gpu() -> None:
     assert call(workspace=None) == _lib.CDB_ERR_NULL
     assert call(workspace_bytes=255) == _lib.CDB_ERR_CAPACITY  # smaller than the chunk header
     per_chunk = 64 + 16 * 130 * 4
-    assert call(workspace_bytes=1280 + 3 * per_chunk) == _lib.CDB_ERR_CAPACITY  # 3 chunks for 4 rows
+    assert call(workspace_bytes=1536 + 3 * per_chunk) == _lib.CDB_ERR_CAPACITY  # 3 chunks for 4 rows
     assert call(block_size=24) == _lib.CDB_ERR_SHAPE
     assert call(num_kv_heads=5) == _lib.CDB_ERR_SHAPE
     assert call(min_split_pages=0) == _lib.CDB_ERR_SHAPE
@@ -94,7 +95,6 @@ def test_staged_decode_argument_errors_without_gpu() -> None:
 
     def call(stages, **kw):
         args = _decode_args(**kw)
-        del args[30]  # max_split_pages: the staged entry does not take it
         return lib.cdb_paged_decode_attention_staged(*args[:-1], stages, args[-1])
 
     assert call(_lib.CDB_DECODE_STAGE_PLAN, num_rows=0) == _lib.CDB_OK

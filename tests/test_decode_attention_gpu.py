@@ -178,7 +178,9 @@ def _device_case(case):
     pool = t(case.kv_pool).to(dt).contiguous()
     tensors = dict(q=t(case.q).to(dt), k=t(case.k_new).to(dt), v=t(case.v_new).to(dt), pool=pool,
                    layer=t(case.cache_layer), table=t(case.block_table), seqlens=t(case.seqlens),
-                   cos=t(case.rope[0]), sin=t(case.rope[1]))
+                   cos=t(case.rope[0]), sin=t(case.rope[1]),
+                   q_bias=None if case.q_bias is None else t(case.q_bias).to(dt),
+                   k_bias=None if case.k_bias is None else t(case.k_bias).to(dt))
     rows, heads, dim = case.q.shape
     ws = torch.empty(ops.decode_workspace_bytes(rows, heads, dim, int(case.seqlens.max()) + 1, case.block_size,
                                                 ops.MIN_SPLIT_PAGES) // 4, dtype=torch.float32, device=dev)
@@ -196,7 +198,8 @@ def _attend(case, d, ws, rows, cache_layer0=0, stages=None):
     ops.paged_decode_attention_raw(
         q, k, v, view.k_ptr, view.v_ptr, view.layer_stride, view.num_cache_layers, view.pool_blocks,
         d["layer"][idx].contiguous(), cache_layer0, d["table"], idx.to(torch.int32), d["seqlens"][idx].contiguous(),
-        d["cos"], d["sin"], case.rope_style, None, None, out, ws, case.block_size, ops.ADAPTIVE_SPLIT, case.scale,
+        d["cos"], d["sin"], case.rope_style, d["q_bias"], d["k_bias"], out, ws, case.block_size, ops.ADAPTIVE_SPLIT,
+        case.scale,
         **({} if stages is None else {"stages": stages}))
     return out
 
@@ -204,7 +207,8 @@ def _attend(case, d, ws, rows, cache_layer0=0, stages=None):
 def test_row_output_is_bit_identical_in_any_batch_composition() -> None:
     # A row's chunks and their merge order depend only on the row: alone, inside the
     # full batch, or inside a shuffled half of it, its output is the same to the bit.
-    # 160 rows run the persistent fast form; 80 rows and single rows the deep form.
+    # 160 rows run the persistent fast form and the merge launch; 80 rows the deep form and
+    # the merge launch; 30 rows and single rows the deep form merging in the decode kernel.
     case = make_case(seed=31, num_rows=160, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1500,
                      rope_style=1, dtype="bf16", padding_rows=3)
     d, ws = _device_case(case)
@@ -212,11 +216,66 @@ def test_row_output_is_bit_identical_in_any_batch_composition() -> None:
     rng = np.random.default_rng(3)
     half = rng.permutation(160)[:80].tolist()
     sub = _attend(case, d, ws, half)
+    few = _attend(case, d, ws, half[:30])
     torch.cuda.synchronize()
     assert torch.equal(sub, full[half])
+    assert torch.equal(few, full[half[:30]])
     for r in (0, int(np.argmax(case.seqlens)), 50):
         alone = _attend(case, d, ws, [r])
         assert torch.equal(alone[0], full[r])
+
+
+def test_huginn_shape_row_output_is_bit_identical_in_any_batch_composition() -> None:
+    # The same at Huginn-0125's attention shape (55 heads x 96, interleaved RoPE with q/k
+    # bias): 150 rows run the persistent fast form, 75 rows and single rows the deep form.
+    case = make_case(seed=34, num_rows=150, num_heads=55, num_kv_heads=55, head_dim=96, max_context=700,
+                     rope_style=2, dtype="bf16", padding_rows=2, qk_bias=True)
+    d, ws = _device_case(case)
+    full = _attend(case, d, ws, list(range(150)))
+    half = np.random.default_rng(4).permutation(150)[:75].tolist()
+    sub = _attend(case, d, ws, half)
+    few = _attend(case, d, ws, half[:30])
+    torch.cuda.synchronize()
+    assert torch.equal(sub, full[half])
+    assert torch.equal(few, full[half[:30]])
+    for r in (1, int(np.argmax(case.seqlens)), 70):
+        assert torch.equal(_attend(case, d, ws, [r])[0], full[r])
+
+
+FAST_FORM_SHAPES = {
+    # name: (dtype, heads, kv_heads, head_dim, rope_style, qk_bias)
+    "f32-mha-16x128": ("f32", 16, 16, 128, 1, False),
+    "bf16-gqa-8x4x64": ("bf16", 8, 4, 64, 1, False),
+    "bf16-huginn-55x96": ("bf16", 55, 55, 96, 2, True),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(FAST_FORM_SHAPES))
+def test_fast_form_above_120_rows_against_the_oracle(shape: str) -> None:
+    """136 rows (more than the deep form's 120, so the persistent fast form with its XCD tail
+    queues, cross-item prefetch and LDS stash runs) against the float64 oracle, with padding
+    rows, one row past its block table and one row at a cache layer outside the pool: those
+    two get NaN and write nothing, every other row is within the bar and its appended K/V row
+    is bit-identical to the oracle's."""
+
+    dtype, heads, kv_heads, dim, rope_style, bias = FAST_FORM_SHAPES[shape]
+    case = make_case(seed=35 + dim, num_rows=136, num_heads=heads, num_kv_heads=kv_heads, head_dim=dim,
+                     max_context=420, rope_style=rope_style, dtype=dtype, padding_rows=5, qk_bias=bias)
+    width = case.block_table.shape[1]
+    case.seqlens[7] = width * case.block_size  # one past its table
+    case.cache_layer[11] = case.kv_pool.shape[0]  # one past the pool's cache layers
+    got, got_pool = run_hip(case, 0)
+    assert np.isnan(got[7]).all() and np.isnan(got[11]).all()
+    case.seqlens[7] = case.seqlens[11] = -1  # as padding for the oracle: no write, no output
+    want, want_pool = run_oracle(case)
+    live = case.seqlens >= 0
+    err = np.abs(got[live] - want[live])
+    max_tol, mean_tol = TOL[dtype]
+    assert np.isfinite(got[live]).all()
+    assert err.max() <= max_tol, f"max err {err.max()}"
+    assert err.mean() <= mean_tol, f"mean err {err.mean()}"
+    assert np.all(got[-5:] == 0.0)
+    np.testing.assert_array_equal(got_pool, want_pool)
 
 
 def test_plan_once_then_attend_per_layer_matches_planning_every_layer() -> None:
@@ -279,7 +338,7 @@ def test_plan_descriptors_match_a_host_restatement() -> None:
     prefix, full, last, key = _expected_plan(case, chunk_tokens)
     assert words[0] == chunk_tokens
     np.testing.assert_array_equal(words[1:42], prefix)
-    header_ints = (((40 + 2) * 4 + 255) // 256 * 256 + 1024) // 4
+    header_ints = (((40 + 2) * 4 + 255) // 256 * 256 + 1024 + 40 * 16 * 4) // 4  # prefix, queues, arrivals
     got = words[header_ints:header_ints + 16 * (len(full) + len(last))].reshape(-1, 16).tolist()
     assert got[:len(full)] == full  # full chunks in row order
     tail = got[len(full):]

@@ -458,6 +458,12 @@ def test_coda_upload_matches_the_python_staging(seed: int) -> None:
             _tick.coda_upload(items, succ, rows, upload.ctypes.data, upload.size, [], capacity, capacity)
         with pytest.raises(ValueError):
             _tick.coda_upload(items, succ, rows, upload.ctypes.data, 2 * n, [], 0, capacity)
+        # A row outside the coda is rejected before any hidden slot is taken.
+        spare = [5, 6, 7]
+        bad_rows = rows[:-1] + [n]
+        with pytest.raises(ValueError, match="outside"):
+            _tick.coda_upload(items, succ, bad_rows, upload.ctypes.data, upload.size, spare, next_slot, capacity)
+        assert spare == [5, 6, 7]
 
 
 def _route_delayed_python(items, flags, max_steps, pending, hist, backlog):

@@ -33,7 +33,7 @@ def _args(case, tensors, out, *, workspace=None):
                    table.data_ptr(), None, table.shape[1], seqlens.data_ptr(), cos.data_ptr(), sin.data_ptr(),
                    case.rope_style, cos.shape[0], None, None, out.data_ptr()]
     ws = [] if workspace is None else [workspace.data_ptr(), workspace.numel() * 4]
-    tail = [rows, heads, k.shape[1], dim, case.block_size, 0, ops.MIN_SPLIT_PAGES, ops.MAX_SPLIT_PAGES,
+    tail = [rows, heads, k.shape[1], dim, case.block_size, 0, ops.MIN_SPLIT_PAGES,
             ctypes.c_float(case.scale), 0, 0, 1, torch.cuda.current_stream().cuda_stream]
     return common_head + ws + tail
 

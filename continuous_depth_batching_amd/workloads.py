@@ -211,3 +211,16 @@ def ouro_decode_workload(num_seqs: int = 256, vocab_size: int = 49152) -> tuple[
                                           prompt_sigma=1.0, prompt_range=(8, 2048), output_mu=5.0,
                                           output_sigma=0.8, output_range=(16, 1024), seed=1)
     return prompts, outputs, categorical_exit_trace(outputs, OURO_EXIT_PROBS, seed=2)
+
+
+def huginn_decode_workload(num_seqs: int = 128, new_tokens: int = 256,
+                           vocab_size: int = 65536) -> tuple[list[list[int]], list[int], list[list[int]]]:
+    """(prompts, max_new_tokens, 0-based exit steps) of the seeded Huginn-0125 decode workload:
+    prompts lognormal(5.0, 0.9) clipped to [8, 1024] with uniform ids, `new_tokens` new tokens
+    each, and per-token exit steps from Poisson(12) truncated to [1, 32]."""
+
+    prompts, _ = lognormal_requests(num_requests=num_seqs, vocab_size=vocab_size, prompt_mu=5.0, prompt_sigma=0.9,
+                                    prompt_range=(8, 1024), output_mu=5.0, output_sigma=0.8,
+                                    output_range=(16, 1024), seed=3)
+    outputs = [new_tokens] * num_seqs
+    return prompts, outputs, poisson_exit_trace(outputs, mean=12.0, max_steps=32, seed=4)

@@ -125,6 +125,19 @@ class OuroOracle:
     def logits(self, hidden: np.ndarray) -> np.ndarray:
         return self._mm(hidden[None, :], self._p("lm_head.weight"))[0]
 
+    def forced_logits(self, prompt: list[int], tokens: list[int], *, max_steps: int, exit_depths: list[int],
+                      kv_policy: str = "single") -> np.ndarray:
+        """[len(tokens), vocab] float64: row j is the oracle's logits for token j when the request
+        decodes ``tokens`` (teacher forcing with its replayed exit depths); row 0 comes from the
+        full-depth prefill, row j from decode token j's last loop step."""
+
+        trace: list = []
+        self.generate(prompt, len(tokens), max_steps=max_steps, kv_policy=kv_policy,
+                      exit_depths=exit_depths[: len(tokens) - 1], forced_tokens=tokens, hidden_trace=trace)
+        final = {j: h for j, _, h in trace}  # the last loop step of each token
+        return np.stack([self.logits(final[j]) for j in range(len(tokens))]).astype(np.float64)
+
+
     def prefill_hidden(self, prompt: list[int], kv: np.ndarray, *, steps: int, slot_of) -> np.ndarray:
         h = self.rnd(self._p("model.embed_tokens.weight")[np.asarray(prompt)])
         pos = np.arange(len(prompt))
@@ -206,3 +219,14 @@ class OuroOracle:
                 token = forced_tokens[len(out.tokens) - 1]
             pos += 1
         return out
+
+
+def forced_choice_stats(ref_logits: np.ndarray, chosen: list[int]) -> dict:
+    """How ``chosen`` tokens sit against teacher-forced reference logits: the fraction that are the
+    reference's argmax, and the margin (reference max logit minus the reference logit of the
+    chosen token; 0 for the argmax) at its worst and on average."""
+
+    idx = np.arange(len(chosen))
+    margins = ref_logits.max(axis=1) - ref_logits[idx, np.asarray(chosen)]
+    return {"argmax_agreement": float(np.mean(ref_logits.argmax(axis=1) == np.asarray(chosen))),
+            "max_logit_margin": float(margins.max()), "mean_logit_margin": float(margins.mean())}

@@ -96,3 +96,28 @@ def test_replayed_depths_are_recorded_and_single_slot_decodes() -> None:
     out = oracle.generate([5, 6, 7, 8], 6, max_steps=4, kv_policy="single", exit_depths=depths)
     assert out.exit_depths == depths and len(out.tokens) == 6
     torch.manual_seed(0)
+
+
+def test_forced_logits_pin_the_parity_statistics() -> None:
+    """Teacher forcing with the oracle's own greedy tokens: every row's argmax is the token that
+    follows (agreement 1, margins 0), and row 0 equals the independent torch forward's last
+    position. A planted wrong token at one step shows up as that step's margin and as one
+    disagreement."""
+
+    from oracle.ouro_model import forced_choice_stats
+
+    w = tiny_weights(seed=3, std=0.05)
+    oracle = make_oracle(w)
+    prompt = list(range(100, 112))
+    depths = [3, 1, 0, 2, 3]
+    out = oracle.generate(prompt, 6, max_steps=4, kv_policy="single", exit_depths=depths)
+    logits = oracle.forced_logits(prompt, out.tokens, max_steps=4, exit_depths=depths)
+    assert logits.shape == (6, TINY["vocab"])
+    np.testing.assert_allclose(logits[0], torch_ouro_forward(w, prompt, 4), rtol=1e-4, atol=1e-4)
+    stats = forced_choice_stats(logits, out.tokens)
+    assert stats == {"argmax_agreement": 1.0, "max_logit_margin": 0.0, "mean_logit_margin": 0.0}
+    wrong = list(out.tokens)
+    wrong[2] = int(np.argsort(logits[2])[-2])  # the runner-up at step 2
+    stats = forced_choice_stats(logits, wrong)
+    assert stats["argmax_agreement"] == 5 / 6
+    assert stats["max_logit_margin"] == float(logits[2].max() - logits[2][wrong[2]]) > 0

@@ -131,3 +131,55 @@ def test_ouro_2p6b_shape_last_exited_schedule_replay_and_exit_copies() -> None:
     assert wave.last_stats.scheduler_refills == 0
     assert wave.last_stats.exit_kv_copies == copies
     assert [out.generated_tokens for out in wave_outs] == refill_tokens
+
+
+def test_huginn_0125_workload_schedule_replay() -> None:
+    """The Huginn-0125 decode workload at its own size: 128 sequences x 256 new tokens, exit steps
+    replayed from Poisson(12) truncated to [1, 32], shared KV, refill, bf16 (huginn/modeling_huginn.py
+    through cdb/adapters/huginn.py:121-176). Every launch, exit depth, the refill count and the free
+    blocks at the end equal the schedule oracle's."""
+
+    from continuous_depth_batching_amd.huginn import HuginnConfig, build_huginn
+    from continuous_depth_batching_amd.workloads import huginn_decode_workload
+
+    cfg = HuginnConfig(block_size=2048, state_init="random", state_seed=1)
+    model = build_huginn(cfg, seed=1, dtype=torch.bfloat16, device="cuda", qk_bias_std=0.02)
+    prompts, mnt, depths = huginn_decode_workload(128, 256, cfg.vocab_size)
+    blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, mnt)) * 1.05) + 64
+    engine, outs, o = replay_and_compare(
+        model, prompts, mnt, depths, max_recurrent_steps=32, num_blocks=blocks, block_size=16, max_model_len=2048,
+        max_num_seqs=128, kv_policy="single", refill=True, synthetic_exit_replay=True,
+        delay_gate_consumption=False, kv_pressure_mode="none")
+    recurrent = [ev for ev in engine.launch_log if ev[0] == "recurrent"]
+    assert max(len(ev[1]) for ev in recurrent) == 128
+    assert max(len({row[2] for row in ev[1]}) for ev in recurrent) >= 8  # many loop steps share launches
+    assert sum(len(out.generated_tokens) for out in outs) == sum(mnt)
+    print(f"\n[huginn-0125 replay] {len(engine.launch_log)} launches, {len(recurrent)} recurrent, "
+          f"refills {engine.last_stats.scheduler_refills}", flush=True)
+    del engine, model
+    torch.cuda.empty_cache()
+
+
+def test_ouro_2p6b_512_sequence_single_kv_schedule_replay() -> None:
+    """The 512-sequence Ouro-2.6B-shape workload (48 layers looped 4 steps) with shared KV and a
+    pool sized for the batch, at its own size: every launch, exit depth, the refill count and the
+    free blocks at the end equal the schedule oracle's."""
+
+    from continuous_depth_batching_amd.ouro import build_ouro, ouro_1p4b_config
+    from continuous_depth_batching_amd.workloads import ouro_decode_workload
+
+    cfg = ouro_1p4b_config(num_hidden_layers=48)
+    model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device="cuda")
+    prompts, mnt, depths = ouro_decode_workload(512, cfg.vocab_size)
+    blocks = int(sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, mnt)) * 1.05) + 64
+    engine, outs, o = replay_and_compare(
+        model, prompts, mnt, depths, max_recurrent_steps=4, num_blocks=blocks, block_size=16, max_model_len=4096,
+        max_num_seqs=512, kv_policy="single", refill=True, synthetic_exit_replay=True,
+        delay_gate_consumption=False, kv_pressure_mode="none")
+    recurrent = [ev for ev in engine.launch_log if ev[0] == "recurrent"]
+    assert max(len(ev[1]) for ev in recurrent) > 256  # the 512-row buckets are reached
+    assert sum(len(out.generated_tokens) for out in outs) == sum(mnt)
+    print(f"\n[ouro-2.6b 512 replay] {len(engine.launch_log)} launches, {len(recurrent)} recurrent, "
+          f"refills {engine.last_stats.scheduler_refills}", flush=True)
+    del engine, model
+    torch.cuda.empty_cache()

@@ -94,6 +94,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "cdb_silu_mul": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
     "cdb_copy_rows": (c_int32, [_P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, _P]),
     "cdb_argmax": (c_int32, [_P, _P, c_int64, c_int32, c_int32, _P]),
+    "cdb_route_compact": (c_int32, [_P, _P, c_int32, _P, _P]),
     "cdb_table_updates": (c_int32, [_P, c_int64, _P, _P, _P, c_int32, _P]),
     "cdb_exit_gate": (
         c_int32,

@@ -694,6 +694,62 @@ int launch_rope_write(const RopeWriteParams& P, hipStream_t s) {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Exit routing of one recurrent launch, in launch order
+// ---------------------------------------------------------------------------
+
+// lists = [exits, stays, exit rows..., staying rows...] over the launch's rows; a row
+// whose bank slot is negative is padding and is in neither list. One workgroup: each
+// thread counts a contiguous run of rows, a scan over the runs places them.
+constexpr int kRouteThreads = 256;
+
+__global__ void __launch_bounds__(kRouteThreads) route_compact_kernel(const uint8_t* exit_flags,
+                                                                      const int64_t* bank_slots, int32_t rows,
+                                                                      int32_t* lists) {
+  __shared__ int wave_total[2][kRouteThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int per = (rows + kRouteThreads - 1) / kRouteThreads;
+  const int lo = min(tid * per, rows), hi = min(lo + per, rows);
+  int exits = 0, stays = 0;
+  for (int r = lo; r < hi; ++r) {
+    if (bank_slots[r] < 0) continue;
+    if (exit_flags[r]) ++exits; else ++stays;
+  }
+  int run_exits = exits, run_stays = stays;  // inclusive scan over the wave's runs
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int e = __shfl_up(run_exits, off, 64), s = __shfl_up(run_stays, off, 64);
+    if (lane >= off) {
+      run_exits += e;
+      run_stays += s;
+    }
+  }
+  if (lane == 63) {
+    wave_total[0][wave] = run_exits;
+    wave_total[1][wave] = run_stays;
+  }
+  __syncthreads();
+  int exit_at = run_exits - exits, stay_at = run_stays - stays, all_exits = 0, all_stays = 0;
+#pragma unroll
+  for (int w = 0; w < kRouteThreads / 64; ++w) {
+    if (w < wave) {
+      exit_at += wave_total[0][w];
+      stay_at += wave_total[1][w];
+    }
+    all_exits += wave_total[0][w];
+    all_stays += wave_total[1][w];
+  }
+  for (int r = lo; r < hi; ++r) {
+    if (bank_slots[r] < 0) continue;
+    if (exit_flags[r]) lists[2 + exit_at++] = r;
+    else lists[2 + all_exits + stay_at++] = r;
+  }
+  if (tid == 0) {
+    lists[0] = all_exits;
+    lists[1] = all_stays;
+  }
+}
+
 extern "C" {
 
 int cdb_rmsnorm_fused(const void* x, const void* residual, const void* w_a, const void* w_b, void* out_h,
@@ -771,6 +827,16 @@ int cdb_table_updates(int32_t* table, int64_t cells, const int64_t* idx, const i
   if (capacity < 0 || cells <= 0) return CDB_ERR_SHAPE;
   hipLaunchKernelGGL(table_update_kernel, dim3(grid_for(capacity)), dim3(kThreads), 0, stream, table, cells, idx, val,
                      count, capacity);
+  return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
+}
+
+int cdb_route_compact(const uint8_t* exit_flags, const int64_t* bank_slots, int32_t rows, int32_t* lists,
+                      hipStream_t stream) {
+  if (rows == 0) return CDB_OK;
+  if (!exit_flags || !bank_slots || !lists) return CDB_ERR_NULL;
+  if (rows < 0) return CDB_ERR_SHAPE;
+  hipLaunchKernelGGL(route_compact_kernel, dim3(1), dim3(kRouteThreads), 0, stream, exit_flags, bank_slots, rows,
+                     lists);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
 

@@ -4,6 +4,8 @@
 //   route_sync      routes one recurrent launch's rows on the synchronous exit
 //                   horizon (cdb/continuous_api.py:1090-1183 with _record_exit
 //                   :1205-1223): exits go to the coda list, the rest step on.
+//   route_lists     route_sync from the device's routing lists (cdb_route_compact):
+//                   the exiting rows, then the staying rows, each in launch order.
 //   route_delayed   the same on the offset-one horizon, from each row's previous
 //                   launch's decision (cdb/continuous_api.py:1124-1141).
 //   fill_recurrent  writes one launch's packed metadata into the pinned staging
@@ -177,6 +179,79 @@ PyObject* route_sync(PyObject*, PyObject* args) {
     }
   }
   PyBuffer_Release(&flags);
+  if (!ok) {
+    Py_XDECREF(coda);
+    Py_XDECREF(refills);
+    Py_XDECREF(exits);
+    return nullptr;
+  }
+  return Py_BuildValue("(NNN)", coda, refills, exits);
+}
+
+// route_lists(items, lists, max_steps, histogram, backlog) -> (coda_items, refills, exits)
+// lists = [n_exit, n_stay, exiting rows..., staying rows...] as cdb_route_compact writes it. The
+// lists must cover every row once, each in launch order; every row must apply the exit gate
+// (the device lists carry the gate's decisions only).
+PyObject* route_lists(PyObject*, PyObject* args) {
+  PyObject *items, *lists_obj, *hist, *backlog;
+  long max_steps;
+  if (!PyArg_ParseTuple(args, "O!OlO!O", &PyList_Type, &items, &lists_obj, &max_steps, &PyDict_Type, &hist,
+                        &backlog))
+    return nullptr;
+  if (backlog != Py_None && !PyList_Check(backlog)) {
+    PyErr_SetString(PyExc_TypeError, "backlog must be a list or None");
+    return nullptr;
+  }
+  Py_buffer buf;
+  if (PyObject_GetBuffer(lists_obj, &buf, PyBUF_SIMPLE) != 0) return nullptr;
+  const Py_ssize_t n = PyList_GET_SIZE(items);
+  const int32_t* lists = static_cast<const int32_t*>(buf.buf);
+  const Py_ssize_t have = buf.len / 4;
+  const int32_t n_exit = have >= 2 ? lists[0] : -1, n_stay = have >= 2 ? lists[1] : -1;
+  bool ok = n_exit >= 0 && n_stay >= 0 && n_exit + n_stay == n && have >= 2 + n;
+  // Each list strictly increasing and together a partition of the rows.
+  std::vector<uint8_t> seen(n, 0);
+  for (int32_t k = 0; ok && k < n_exit + n_stay; ++k) {
+    const int32_t r = lists[2 + k];
+    const bool rising = k == 0 || k == n_exit || r > lists[1 + k];
+    ok = r >= 0 && r < n && rising && !seen[r];
+    if (ok) seen[r] = 1;
+  }
+  if (!ok) {
+    PyBuffer_Release(&buf);
+    PyErr_SetString(PyExc_ValueError, "routing lists do not partition the launch's rows in launch order");
+    return nullptr;
+  }
+  PyObject* coda = PyList_New(0);
+  PyObject* refills = PyList_New(0);
+  PyObject* exits = PyList_New(n);
+  ok = coda && refills && exits;
+  for (Py_ssize_t i = 0; ok && i < n; ++i) {
+    Py_INCREF(Py_False);
+    PyList_SET_ITEM(exits, i, Py_False);
+  }
+  for (int32_t k = 0; ok && k < n_exit + n_stay; ++k) {
+    const int32_t r = lists[2 + k];
+    PyObject* item = PyList_GET_ITEM(items, r);
+    long step;
+    const int apply = get_truth(item, s_apply_exit_gate);
+    ok = apply >= 0 && get_long(item, s_recurrent_step, &step);
+    if (ok && !apply) {
+      PyErr_SetString(PyExc_ValueError, "device routing needs every row to apply the exit gate");
+      ok = false;
+    }
+    if (!ok) break;
+    if (k < n_exit) {
+      ok = record_exit(item, step, 1, hist, backlog, max_steps) && PyList_Append(coda, item) == 0;
+      if (ok) {
+        Py_INCREF(Py_True);
+        PyList_SetItem(exits, r, Py_True);  // releases the False it replaces
+      }
+    } else {
+      ok = set_long(item, s_recurrent_step, step + 1) && PyList_Append(refills, item) == 0;
+    }
+  }
+  PyBuffer_Release(&buf);
   if (!ok) {
     Py_XDECREF(coda);
     Py_XDECREF(refills);
@@ -1607,6 +1682,8 @@ PyObject* route_delayed(PyObject*, PyObject* args) {
 PyMethodDef kMethods[] = {
     {"route_sync", route_sync, METH_VARARGS,
      "route_sync(items, flags, max_steps, histogram, backlog) -> (coda_items, refills, exits)"},
+    {"route_lists", route_lists, METH_VARARGS,
+     "route_lists(items, lists, max_steps, histogram, backlog) -> (coda_items, refills, exits)"},
     {"fill_recurrent", fill_recurrent, METH_VARARGS,
      "fill_recurrent(items, i64, i32, table_row_of, core_base, core_layers, slot_of_step)"},
     {"enqueue_front", enqueue_front, METH_VARARGS, "enqueue_front(queue, items, max_steps, in_flight) -> refills"},

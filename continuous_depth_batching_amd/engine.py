@@ -450,11 +450,16 @@ class ContinuousDepthBatchingEngine:
         stats.recurrent_steps += len(items)
         max_steps = self.cdb_config.max_recurrent_steps
         if not self.exit_policy.delayed():
-            # Synchronous horizon: this launch's flags route its rows (the host tick core does
-            # the per-row work: exit bookkeeping, coda list, step advance of the refills).
-            coda_items, refills, exits = _tick.route_sync(
-                items, flags.wait(), max_steps, stats.exit_depth_histogram,
-                self._exit_kv_backlog if self.exit_kv_layout is not None else None)
+            # Synchronous horizon: this launch's decisions route its rows. The device lists the
+            # exiting and the staying rows in launch order; the tick core does the bookkeeping
+            # (exit depths, coda list, step advance of the staying rows).
+            backlog = self._exit_kv_backlog if self.exit_kv_layout is not None else None
+            if flags.lists is not None:
+                coda_items, refills, exits = _tick.route_lists(
+                    items, flags.routing_lists(), max_steps, stats.exit_depth_histogram, backlog)
+            else:
+                coda_items, refills, exits = _tick.route_sync(
+                    items, flags.wait(), max_steps, stats.exit_depth_histogram, backlog)
             self.scheduler.enqueue_coda_items(coda_items)
             if refills:
                 self.scheduler.enqueue_depth_front(refills)

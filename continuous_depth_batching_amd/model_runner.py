@@ -95,29 +95,43 @@ class PendingPrefillResult:
 
 @dataclass
 class PendingFlags:
-    """Exit decisions of one launch, on their way to the host."""
+    """Exit decisions of one launch, on their way to the host: one byte per row, or, when the
+    device routed the launch (cdb_route_compact), the lists [n_exit, n_stay, exiting rows,
+    staying rows] in launch order."""
 
-    host: torch.Tensor
+    host: torch.Tensor | None
     event: Any | None
+    lists: torch.Tensor | None = None
     _values: list[int] | None = None
+
+    def _landed(self) -> None:
+        if self.event is not None:
+            self.event.synchronize()
+            self.event = None
 
     def wait(self) -> np.ndarray:
         """The decision bytes, once the launch has written them (one per row, then padding)."""
 
-        if self.event is not None:
-            self.event.synchronize()
-            self.event = None
+        self._landed()
+        if self.host is None:
+            lists = self.lists.numpy()
+            flags = np.zeros(int(lists[0]) + int(lists[1]), np.uint8)
+            flags[lists[2:2 + int(lists[0])]] = 1
+            return flags
         return self.host.numpy()
+
+    def routing_lists(self) -> np.ndarray:
+        """The device's routing lists, once the launch has written them."""
+
+        self._landed()
+        return self.lists.numpy()
 
     def get(self, index: int) -> bool:
         values = self._values
         if values is None:
-            # Wait once, then read the pinned bytes as a Python list: per-row tensor
-            # indexing costs microseconds each on the routing path.
-            if self.event is not None:
-                self.event.synchronize()
-                self.event = None
-            values = self._values = self.host.tolist()
+            # Wait once, then read the bytes as a Python list: per-row tensor indexing costs
+            # microseconds each on the routing path.
+            values = self._values = self.wait().tolist()
         return bool(values[index])
 
 
@@ -156,6 +170,8 @@ class _RecurrentBucket:
     turn: int = 0
     host_flags: list[torch.Tensor] = field(default_factory=list)
     flag_events: list[Any] = field(default_factory=list)
+    dev_lists: torch.Tensor | None = None  # cdb_route_compact output of the launch
+    host_lists: list[torch.Tensor] = field(default_factory=list)
 
 
 @dataclass
@@ -182,6 +198,9 @@ class ModelRunner:
         self.cache = cache
         self.adapter = model_adapter
         self.exit_policy = exit_policy
+        # On the synchronous horizon the device routes each launch's rows (exit and stay lists in
+        # launch order); on the delayed one the host reads each row's decision a launch later.
+        self.device_routing = not exit_policy.delayed()
         self.device = cache.device
         self.dtype = model_adapter.dtype
         self.max_num_seqs = engine_config.max_num_seqs
@@ -394,6 +413,9 @@ class ModelRunner:
         b.dev_upd_val = dev_meta[base + 2 + 2 * u:total]
         b.host_flags = [self._pinned((rows,), torch.uint8) for _ in range(self.FLAG_TURNS)]
         b.flag_events = [None] * self.FLAG_TURNS
+        if self.device_routing:
+            b.dev_lists = torch.zeros(2 + rows, dtype=torch.int32, device=self.device)
+            b.host_lists = [self._pinned((2 + rows,), torch.int32) for _ in range(self.FLAG_TURNS)]
         self._buckets[rows] = b
         return b
 
@@ -425,13 +447,20 @@ class ModelRunner:
                 b.staged = torch.cuda.Event()
             b.staged.record()
             self._run_recurrent(b)
-            host_flags = b.host_flags[turn]
-            host_flags[:n].copy_(b.launch.gate.flags[:n], non_blocking=True)
+            if self.device_routing:
+                # The graph's last kernel routed the rows: one copy of the lists.
+                host_lists = b.host_lists[turn][:2 + n]
+                host_lists.copy_(b.dev_lists[:2 + n], non_blocking=True)
+                host_flags = None
+            else:
+                host_lists = None
+                host_flags = b.host_flags[turn]
+                host_flags[:n].copy_(b.launch.gate.flags[:n], non_blocking=True)
             event = b.flag_events[turn]
             if event is None:
                 event = b.flag_events[turn] = torch.cuda.Event()
             event.record()
-        return PendingFlags(host=host_flags, event=event)
+        return PendingFlags(host=host_flags, event=event, lists=host_lists)
 
     def fill_recurrent_metadata(self, items: list[DepthWorkItem], i64: np.ndarray, i32: np.ndarray) -> None:
         """Host metadata of one recurrent launch over a bucket of ``len(i64)`` rows.
@@ -484,10 +513,18 @@ class ModelRunner:
         ops.table_updates_raw(self.cache.device_table, b.dev_upd_idx, b.dev_upd_val, b.dev_upd_count,
                               self.TABLE_UPDATE_SLOTS)
 
+    def _recurrent_body(self, b: _RecurrentBucket) -> None:
+        """One recurrent launch on the device: the block-table cells it carries, the loop step with
+        its exit gate, and on the synchronous horizon the routing lists of its rows."""
+
+        self._apply_table_updates(b)
+        self.adapter.recurrent_step(b.launch)
+        if self.device_routing:
+            torch.ops.cdb.route_compact(b.launch.gate.flags, b.launch.bank_slots, b.dev_lists)
+
     def _run_recurrent(self, b: _RecurrentBucket) -> None:
         if not self.use_graphs:
-            self._apply_table_updates(b)
-            self.adapter.recurrent_step(b.launch)
+            self._recurrent_body(b)
             return
         if b.graph is not None:
             self.recurrent_graph_hits += 1
@@ -495,12 +532,10 @@ class ModelRunner:
             return
         # First use of this bucket: run it eagerly (this launch's real work), then capture.
         with gc_paused():
-            self._apply_table_updates(b)
-            self.adapter.recurrent_step(b.launch)
+            self._recurrent_body(b)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=self.stream, pool=self.graph_pool, capture_error_mode="thread_local"):
-                self._apply_table_updates(b)
-                self.adapter.recurrent_step(b.launch)
+                self._recurrent_body(b)
         b.graph = graph
         self.recurrent_graph_captures += 1
 

@@ -882,6 +882,35 @@ def _(hidden, prev, weight, bias, signal, cdf, survival, pending, state_index, s
     return None
 
 
+def route_compact_raw(exit_flags: torch.Tensor, bank_slots: torch.Tensor, lists: torch.Tensor) -> None:
+    """Launch ``cdb_route_compact`` over ``bank_slots.numel()`` rows (no allocation): ``lists``
+    int32 [2 + rows] gets [n_exit, n_stay, exiting rows, staying rows] in launch order."""
+
+    rows = bank_slots.numel()
+    if exit_flags.dtype != torch.uint8 or bank_slots.dtype != torch.int64 or lists.dtype != torch.int32:
+        raise TypeError("exit_flags uint8, bank_slots int64 and lists int32 expected")
+    if exit_flags.numel() < rows or lists.numel() < 2 + rows:
+        raise ValueError("exit_flags needs a byte per row and lists 2 + rows entries")
+    _require_cuda(exit_flags, bank_slots, lists)
+    _require_contiguous(exit_flags=exit_flags, bank_slots=bank_slots, lists=lists)
+    _lib.check(_lib.lib().cdb_route_compact(exit_flags.data_ptr(), bank_slots.data_ptr(), rows, lists.data_ptr(),
+                                            _stream()), "cdb_route_compact")
+
+
+@torch.library.custom_op("cdb::route_compact", mutates_args=("lists",), device_types="cuda")
+def route_compact(exit_flags: torch.Tensor, bank_slots: torch.Tensor, lists: torch.Tensor) -> None:
+    """Exit routing of one recurrent launch in launch order (cdb/continuous_api.py:1171-1183):
+    ``lists`` = [n_exit, n_stay, the exiting rows, the staying rows]; padding rows (negative
+    bank slot) are in neither list."""
+
+    route_compact_raw(exit_flags, bank_slots, lists)
+
+
+@route_compact.register_fake
+def _(exit_flags, bank_slots, lists):
+    return None
+
+
 def exit_kv_copy_raw(view: KVPoolView, rows: torch.Tensor, exit_slot: torch.Tensor, n: int, *, layer_base: int,
                      core_layers: int, num_slots: int) -> None:
     """Copy each exiting token's exit-slot KV into its deeper slots (copy-on-exit layout)."""

@@ -180,6 +180,17 @@ int cdb_copy_rows(const void* src, const int64_t* src_index, int64_t src_rows, v
 int cdb_table_updates(int32_t* table, int64_t cells, const int64_t* idx, const int32_t* val, const int32_t* count,
                       int32_t capacity, hipStream_t stream);
 
+/* Exit routing of one recurrent launch on the device, in launch order: writes
+ * lists = [n_exit, n_stay, the n_exit exiting rows, the n_stay staying rows], the
+ * rows being indices into the launch (exit_flags[r] != 0: row r leaves for the coda)
+ * and rows with a negative bank slot (padding) in neither list. Replaces the
+ * per-row routing pass over the launch's decisions on the synchronous horizon
+ * (cdb/continuous_api.py:1171-1183 after cdb/model_runner.py:694-699,796-821):
+ * exiting rows go to the coda queue in this order, staying rows back to the head of
+ * the depth queue in this order. lists holds 2 + rows ints. */
+int cdb_route_compact(const uint8_t* exit_flags, const int64_t* bank_slots, int32_t rows, int32_t* lists,
+                      hipStream_t stream);
+
 /* Greedy sampling: out[r] = first index of the maximum of logits[r, :vocab]
  * (torch.argmax semantics incl. NaN; cdb/model_runner.py:1062,1105). */
 int cdb_argmax(const void* logits, int64_t* out, int64_t rows, int32_t vocab, int32_t dtype, hipStream_t stream);

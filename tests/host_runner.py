@@ -166,7 +166,15 @@ class HostLoopRunner(ModelRunner):
             self.hidden[slot] += 1.0
             signal = 10.0 if step == 0 else -10.0
             flags[r] = self._decide(slot, step, synth, signal)
-        return PendingFlags(host=torch.from_numpy(flags), event=None)
+        if self.exit_policy.delayed():
+            return PendingFlags(host=torch.from_numpy(flags), event=None)
+        # The synchronous horizon routes from the lists cdb_route_compact writes: exiting rows,
+        # then staying rows, each in launch order (padding rows have a negative bank slot).
+        live = np.nonzero(i64 >= 0)[0]
+        exits = [int(r) for r in live if flags[r]]
+        stays = [int(r) for r in live if not flags[r]]
+        lists = np.array([len(exits), len(stays)] + exits + stays, np.int32)
+        return PendingFlags(host=None, event=None, lists=torch.from_numpy(lists))
 
     def _decide(self, slot: int, step: int, synth: int, signal: float) -> bool:
         p = self.exit_policy

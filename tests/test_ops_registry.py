@@ -20,6 +20,7 @@ OPERATORS = {
     "residual_rmsnorm": set(),
     "exit_gate": {"signal", "cdf", "survival", "pending", "exit_flags"},
     "exit_kv_copy": {"kv_pool"},
+    "route_compact": {"lists"},
     "gather_rows": set(),
     "scatter_rows_": {"dst"},
     "linear": set(),

@@ -425,3 +425,24 @@ def test_prefill_attention_long_prefixes(dtype: str, head_dim: int, heads: int, 
     err = np.abs(host(out_split) - want)
     assert (err <= bound).all(), (err - bound).max()
     assert err.mean() <= mean_tol, err.mean()
+
+
+@pytest.mark.parametrize("rows,live", [(1, 1), (8, 5), (256, 256), (512, 300), (1500, 1400)])
+def test_route_compact_lists_exits_then_stays_in_launch_order(rows: int, live: int) -> None:
+    """cdb_route_compact against its restatement: [n_exit, n_stay, exiting rows, staying rows],
+    each list in launch order, padding rows (negative bank slot) in neither; bit-exact."""
+
+    from continuous_depth_batching_amd import ops
+
+    rng = np.random.default_rng(rows)
+    flags = (rng.random(rows) < 0.35).astype(np.uint8)
+    slots = np.full(rows, -1, np.int64)
+    slots[:live] = rng.permutation(4 * rows)[:live]
+    lists = torch.full((2 + rows,), -7, dtype=torch.int32, device="cuda")
+    torch.ops.cdb.route_compact(dev(flags), dev(slots), lists)
+    got = lists.cpu().numpy()
+    exits = [r for r in range(rows) if slots[r] >= 0 and flags[r]]
+    stays = [r for r in range(rows) if slots[r] >= 0 and not flags[r]]
+    want = np.array([len(exits), len(stays)] + exits + stays, np.int32)
+    np.testing.assert_array_equal(got[:2 + live], want)
+    assert np.all(got[2 + live:] == -7)  # nothing written past the live rows' lists

@@ -84,6 +84,64 @@ def test_route_sync_matches_the_per_row_routing(seed: int, with_backlog: bool) -
         assert [(idx[id(i)], s) for i, s in back_a] == [(idx_b[id(i)], s) for i, s in back_b]
 
 
+def _compact_python(flags: np.ndarray, slots: np.ndarray) -> np.ndarray:
+    """cdb_route_compact restated: [n_exit, n_stay, exiting rows, staying rows], padding skipped."""
+
+    live = np.nonzero(slots >= 0)[0]
+    exit_rows = [int(r) for r in live if flags[r]]
+    stay_rows = [int(r) for r in live if not flags[r]]
+    return np.array([len(exit_rows), len(stay_rows)] + exit_rows + stay_rows, dtype=np.int32)
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("with_backlog", [False, True])
+def test_route_lists_equals_route_sync(seed: int, with_backlog: bool) -> None:
+    """Routing from the device's lists (exiting rows, then staying rows, each in launch order)
+    gives route_sync's coda list, refills, exit flags, histogram, backlog and item state."""
+
+    rng = random.Random(seed)
+    max_steps = 4
+    n = rng.randrange(1, 60)
+    items_a = _items(random.Random(seed + 200), n, max_steps)
+    items_b = _items(random.Random(seed + 200), n, max_steps)
+    for it in items_a + items_b:
+        it.apply_exit_gate = True  # the device lists carry the gate's decisions
+    rows = n + rng.randrange(0, 9)
+    flags = np.zeros(rows, dtype=np.uint8)
+    flags[:n] = [rng.random() < 0.4 for _ in range(n)]
+    flags[n:] = 1  # padding rows, skipped by their negative bank slot
+    slots = np.full(rows, -1, np.int64)
+    slots[:n] = np.arange(n)
+    lists = _compact_python(flags, slots)
+    hist_a, hist_b = Counter({2: 1}), Counter({2: 1})
+    back_a = [] if with_backlog else None
+    back_b = [] if with_backlog else None
+    got = _tick.route_lists(items_a, lists, max_steps, hist_a, back_a)
+    want = _tick.route_sync(items_b, flags, max_steps, hist_b, back_b)
+    idx = {id(it): k for k, it in enumerate(items_a)}
+    idx_b = {id(it): k for k, it in enumerate(items_b)}
+    for a, b in zip(got[:2], want[:2]):
+        assert [idx[id(i)] for i in a] == [idx_b[id(i)] for i in b]
+    assert got[2] == want[2] and all(type(e) is bool for e in got[2])
+    assert hist_a == hist_b and _snapshot(items_a) == _snapshot(items_b)
+    if with_backlog:
+        assert [(idx[id(i)], s) for i, s in back_a] == [(idx_b[id(i)], s) for i, s in back_b]
+
+
+def test_route_lists_rejects_lists_that_are_not_a_launch_order_partition() -> None:
+    items = _items(random.Random(1), 5, 4)
+    for it in items:
+        it.apply_exit_gate = True
+    # wrong total, an exit list out of order, a repeated stay, a row in both lists, a row past the launch
+    for bad in ([2, 2, 0, 3, 1, 2], [2, 3, 3, 0, 1, 2, 4], [1, 4, 0, 1, 2, 3, 3], [2, 3, 0, 1, 1, 3, 4],
+                [2, 3, 0, 5, 1, 2, 3]):
+        with pytest.raises(ValueError, match="partition"):
+            _tick.route_lists(items, np.array(bad, np.int32), 4, Counter(), None)
+    items[3].apply_exit_gate = False
+    with pytest.raises(ValueError, match="apply the exit gate"):
+        _tick.route_lists(items, np.array([2, 3, 1, 3, 0, 2, 4], np.int32), 4, Counter(), None)
+
+
 def test_route_sync_rejects_short_flags_and_bad_backlog() -> None:
     items = _items(random.Random(0), 4, 4)
     with pytest.raises(ValueError, match="fewer exit flags"):

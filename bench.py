@@ -443,11 +443,21 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, prefill_tokens:
 TRAFFIC_RECORD = "profiles/decode_attention_c2_256rows_traffic.json"
 
 
+DECODE_SOURCE = "continuous_depth_batching_amd/csrc/paged_decode_attention.hip"
+
+
+def decode_source_sha256() -> str:
+    import hashlib
+
+    return hashlib.sha256((REPO / DECODE_SOURCE).read_bytes()).hexdigest()
+
+
 def measured_traffic(algorithmic_bytes: int) -> int | None:
     """HBM bytes per decode-attention call at this shape, from the FETCH_SIZE / WRITE_SIZE
     counter runs (scaled by a plain copy of known size) recorded with the profiles. A counter
     run cannot happen inside this process, so the record is used only when it was taken on
-    this very shape (its algorithmic bytes equal this run's); otherwise the figure is null."""
+    this very shape (its algorithmic bytes equal this run's) with this very decode source (its
+    SHA-256 equals the source's now); otherwise the figure is null."""
 
     path = REPO / TRAFFIC_RECORD
     if not path.exists():
@@ -455,8 +465,8 @@ def measured_traffic(algorithmic_bytes: int) -> int | None:
     record = json.loads(path.read_text())
     if int(record.get("algorithmic_bytes_per_call", -1)) != int(algorithmic_bytes):
         return None
-    if not str(record.get("kernels", "")).startswith("paged_decode_fast_kernel"):
-        return None  # counted on another form of the kernel
+    if record.get("decode_source_sha256") != decode_source_sha256():
+        return None  # counted on another version of the kernels
     return int(record["traffic_bytes_per_call"])
 
 

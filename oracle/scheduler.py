@@ -41,9 +41,19 @@ value is the token id, each recurrent step adds one and emits the exit signal +1
 -10 after, the coda's token is round(hidden) mod vocab, and a full-depth prefill predicts
 (token + steps) mod vocab.
 
-Not modelled (the restatement raises): KV pressure (a decode block that cannot be allocated),
-preemption and offload, open-loop arrivals, pre-loop exit distributions, and the no-refill
-loop on the delayed horizon.
+KV pressure (``kv_pressure_mode`` "recompute" or "offload"; continuous_api.py:1584-1669,
+offloading_manager.py:172-314, scheduler_base.py:400-460, requests.py:82-126 of both packages): a
+decode token that cannot get its block parks its request at the token boundary; parked requests
+are retried in park order ahead of each tick's scheduling, stopping at the first that still fails;
+when no bucket can run, the parked request with the fewest tokens (the latest to park among
+equals) gives up its KV -- swapped to a host pool of ``swap_blocks`` blocks when it holds them all
+(offload), else soft-reset (prompt + generated tokens re-prefilled, the replay resumed at
+``cursor + 1``). The victim rejoins the waiting queue, and new admissions wait until a request
+finishes; swapped requests are restored first on later ticks (offload mode only), with blocks for
+their pending token.
+
+Not modelled (the restatement raises): reserve admission, open-loop arrivals, pre-loop exit
+distributions, and the no-refill loop on the delayed horizon.
 """
 
 from __future__ import annotations
@@ -79,6 +89,8 @@ class _Req:
     blocks: list[int] = field(default_factory=list)
     in_flight_tokens: int = 0
     cursor: int = 0
+    offloaded: bool = False
+    earlier: list[int] = field(default_factory=list)  # tokens generated before soft resets
 
 
 @dataclass
@@ -123,7 +135,8 @@ class ScheduleOracle:
                  synthetic_exit_replay: bool = False, exit_threshold: float | None = None,
                  rule: str = HAZARD, offset_one_signal: bool = False, min_recurrent_steps: int = 1,
                  vocab_size: int = 16, replay_eos_finishes: bool = False,
-                 replay_offset_one: bool | None = None, mixed_slot_recurrent_batches: bool = False) -> None:
+                 replay_offset_one: bool | None = None, mixed_slot_recurrent_batches: bool = False,
+                 kv_pressure_mode: str = "none", swap_blocks: int = 0) -> None:
         self.R = max_recurrent_steps
         self.num_blocks = num_blocks
         self.bs = block_size
@@ -160,6 +173,12 @@ class ScheduleOracle:
         self.delayed_replay = synthetic_exit_replay and (overlap if replay_offset_one is None else replay_offset_one)
         if not refill and (self.delayed_live or self.delayed_replay):
             raise ScheduleOracleError("the no-refill loop is restated on the synchronous horizon only")
+        if kv_pressure_mode not in ("none", "recompute", "offload"):
+            raise ScheduleOracleError(f"kv_pressure_mode {kv_pressure_mode!r} is not restated")
+        self.pressure = kv_pressure_mode
+        # Only the offload mode has a host pool; a pool without room falls back to a soft reset,
+        # which copy-on-exit layouts do not allow (offloading_manager.py:183-217).
+        self.swap_blocks = swap_blocks if kv_pressure_mode == "offload" else 0
 
     # -- slot arithmetic (kv_cache_policy.py:84-103) -----------------------------------------------------------
     def _kv_slot(self, step: int) -> int:
@@ -182,6 +201,9 @@ class ScheduleOracle:
                           [list(s) for s in (stop_sequences or [])], remaining=list(p))
                      for i, p in enumerate(prompts)]
         self.free_blocks: deque[int] = deque(range(self.num_blocks))
+        self.host_free: deque[int] = deque(range(self.swap_blocks))
+        self.host_of: dict[str, list[int]] = {}
+        self.parked: dict[str, _Req] = {}  # insertion order is park order
         self.free_slots: list[int] = []
         self.next_slot = 0
         self.waiting: dict[str, _Req] = {}
@@ -210,7 +232,7 @@ class ScheduleOracle:
             self._wave_loop()
         s = self.stats
         return {
-            "tokens": [r.generated for r in self.reqs],
+            "tokens": [r.earlier + r.generated for r in self.reqs],
             "exit_depths": [r.exit_log for r in self.reqs],
             "events": self.events,
             "trace": self.trace,
@@ -226,6 +248,8 @@ class ScheduleOracle:
                 "scheduler_ticks": s["ticks"], "fixed_depth_recurrent_steps": s["coda_tokens"] * self.R,
                 "exit_depth_histogram": dict(self.exit_hist), "prelude_tokens": dict(self.prelude_tokens),
                 "max_mixed_depths_per_batch": self.max_mixed,
+                "offload_preemptions": s["offload_preemptions"], "recompute_preemptions": s["recompute_preemptions"],
+                "restores": s["restores"],
             },
         }
 
@@ -254,6 +278,7 @@ class ScheduleOracle:
     def _retire(self, r: _Req) -> None:
         self.free_blocks.extend(r.blocks)
         r.blocks = []
+        self.parked.pop(r.rid, None)
         self.active.pop(r.rid, None)
         self.in_flight.discard(r.rid)
         if self.waiting.pop(r.rid, None) is not None:
@@ -335,12 +360,85 @@ class ScheduleOracle:
                 r.cursor += 1
         return _Item(req=r, pos=r.pos, step=0, depth=depth, value=value)
 
-    def _stage_decode(self, r: _Req) -> _Item:
+    def _stage_decode(self, r: _Req) -> _Item | None:
+        """The request's next decode item, or None when it parks for lack of a block."""
+
         if not r.to_process or r.to_process[0] < 0:
             raise ScheduleOracleError(f"{r.rid}: no sampled token to decode")
         if not self._grow_one(r):
-            raise ScheduleOracleError(f"{r.rid}: KV pressure is not modelled")
+            if self.pressure == "none":
+                raise ScheduleOracleError(f"{r.rid}: KV cache full and no pressure mode")
+            self.parked[r.rid] = r
+            return None
+        self.parked.pop(r.rid, None)
         return self._new_item(r, float(r.to_process[0]))
+
+    def _retry_parked(self) -> list[_Item]:
+        items = []
+        for r in list(self.parked.values()):
+            it = self._stage_decode(r)
+            if it is None:
+                break
+            items.append(it)
+        return items
+
+    # -- preemption and restore (continuous_api.py:1625-1652, offloading_manager.py:172-314) -----------------
+    def _yield_parked(self) -> None:
+        if len(self.active) <= 1:
+            raise ScheduleOracleError("a single request's KV does not fit the cache")
+        order = list(self.parked)
+        k = min(range(len(order)), key=lambda i: (self.parked[order[i]].pos, -i))
+        r = self.parked.pop(order[k])
+        if r.blocks and len(self.host_free) >= len(r.blocks):
+            self.host_of[r.rid] = [self.host_free.popleft() for _ in r.blocks]
+            r.offloaded = True
+            self.stats["offload_preemptions"] += 1
+        else:
+            if self.copy_on_exit:
+                raise ScheduleOracleError(f"{r.rid}: no host room and no soft reset under copy-on-exit KV")
+            # Soft reset: prompt + generated (the pending token included) re-prefilled as a new
+            # prompt, the budget reduced by as many, the replay resumed past the pending token.
+            r.earlier = r.earlier + r.generated
+            r.prompt = r.prompt + r.generated
+            r.limit -= len(r.generated)
+            r.depths = r.depths[r.cursor + 1:]
+            r.cursor = 0
+            r.generated = []
+            r.remaining = list(r.prompt)
+            r.to_process = []
+            r.pos = 0
+            r.status = "pending"
+            r.in_flight_tokens = 0
+            self.stats["recompute_preemptions"] += 1
+        self.free_blocks.extend(r.blocks)
+        r.blocks = []
+        self.active.pop(r.rid, None)
+        self.in_flight.discard(r.rid)
+        self.waiting[r.rid] = r
+        self.waiting_order.append(r.rid)
+        self.block_new = True
+
+    def _restore(self) -> list[_Req]:
+        """Swapped-out requests back into the active set, in waiting order, each with blocks for
+        its pending token; stops at the first that does not fit (scheduler_base.py:434-460)."""
+
+        if self.block_new or self.pressure != "offload":
+            return []
+        restored = []
+        for rid in list(self.waiting_order):
+            r = self.waiting[rid]
+            if not r.offloaded:
+                continue
+            if self._open_slots() == 0 or not self._grow_one(r):
+                break
+            self.active[rid] = r
+            del self.waiting[rid]
+            self.waiting_order.remove(rid)
+            self.host_free.extend(self.host_of.pop(rid))
+            r.offloaded = False
+            self.stats["restores"] += 1
+            restored.append(r)
+        return restored
 
     def _prelude(self, items: list[_Item], site: str) -> None:
         if not items:
@@ -488,8 +586,8 @@ class ScheduleOracle:
             if self._take_token(r, tok):
                 self._retire(r)
                 continue
-            if restage:
-                fresh.append(self._stage_decode(r))
+            if restage and (it := self._stage_decode(r)) is not None:
+                fresh.append(it)
         if fresh:
             self._prelude(fresh, "after_coda_staged")
             self._push_front(fresh)
@@ -527,7 +625,8 @@ class ScheduleOracle:
         bucket = [r for r in self.active.values() if r.status == "prefilling" and r.rid not in self.in_flight]
         if not self.block_new:
             limit = self._open_slots()
-            bucket += [self.waiting[rid] for rid in list(self.waiting_order)[:limit]]
+            fresh = [self.waiting[rid] for rid in self.waiting_order if not self.waiting[rid].offloaded]
+            bucket += fresh[:limit]
         if not bucket:
             return []
         if any(r.status == "prefilling" for r in bucket):
@@ -615,7 +714,8 @@ class ScheduleOracle:
             if self._take_token(r, tok):
                 self._retire(r)
                 continue
-            fresh.append(self._stage_decode(r))
+            if (it := self._stage_decode(r)) is not None:
+                fresh.append(it)
         if fresh:
             self._prelude(fresh, "after_prefill")
             for it in fresh:
@@ -627,10 +727,20 @@ class ScheduleOracle:
             self._consume_all()
             if not self._pending_work():
                 continue
+            # Restored requests, then parked ones, share one prelude at the queue head.
+            resumed = [it for r in self._restore() if (it := self._stage_decode(r)) is not None]
+            resumed += self._retry_parked()
+            if resumed:
+                self._prelude(resumed, "resumed")
+                self._push_front(resumed)
+                self._record("prelude", len(resumed), site="resumed")
             self.stats["ticks"] += 1
             self.tick = self.stats["ticks"]
             kind, payload = self._schedule_next()
             if kind is None:
+                if self.parked:
+                    self._yield_parked()
+                    continue
                 raise ScheduleOracleError("no work could be scheduled")
             if kind == "coda":
                 items = self._drop_finished(payload)
@@ -695,6 +805,7 @@ class ScheduleOracle:
     def _wave_loop(self) -> None:
         while self._pending_work():
             self.tick += 1
+            self._restore()  # restored decoders join this wave's cohort scan
             ran_prefill = False
             while self._admit_prefill():
                 packed = self._pack_prefill()
@@ -718,6 +829,9 @@ class ScheduleOracle:
                 ran_prefill = True
             ran_wave = self._wave()
             if not ran_prefill and not ran_wave:
+                if self.parked:
+                    self._yield_parked()
+                    continue
                 if not self._pending_work():
                     continue
                 raise ScheduleOracleError("no-refill loop stalled")
@@ -725,7 +839,7 @@ class ScheduleOracle:
     def _wave(self) -> bool:
         cohort = [r for r in self.active.values()
                   if r.status == "decoding" and r.to_process and r.to_process[0] >= 0][: self.cap]
-        items = [self._stage_decode(r) for r in cohort]
+        items = [it for r in cohort if (it := self._stage_decode(r)) is not None]
         if not items:
             return False
         self._prelude(items, "wave_cohort")

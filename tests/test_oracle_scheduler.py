@@ -317,3 +317,54 @@ def test_counter_identities() -> None:
     assert s["coda_tokens"] == sum(m - 1 for m in mnt)
     assert s["prefill_coda_tokens"] == len(prompts)
     assert Counter(d for ds in depths for d in ds) == Counter(s["exit_depth_histogram"])
+
+
+# -- KV pressure (test_continuous_depth_batching.py:1581-1738, test_prefill_admission.py:330-431) ----------------
+PRESSURE_PROMPTS = [[1, 2], [3, 4], [5, 6], [7, 8]]
+
+
+def _pressured(mode: str, depths, swap_blocks: int = 0, **over):
+    kw = dict(max_recurrent_steps=3, num_blocks=6, block_size=2, max_model_len=12, safety_margin=0.0,
+              synthetic_exit_replay=True, delay_gate_consumption=False, kv_pressure_mode=mode,
+              swap_blocks=swap_blocks, vocab_size=16)
+    kw.update(over)
+    return ScheduleOracle(**kw).run(PRESSURE_PROMPTS, 8, exit_depths=depths)
+
+
+@pytest.mark.parametrize("refill", [True, False])
+def test_soft_reset_at_full_depth_reproduces_the_uncontended_tokens(refill: bool) -> None:
+    """Four requests that each grow to 5 blocks on a 6-block cache: at full depth a soft-reset
+    resume (re-prefill of prompt + generated tokens) gives the tokens of an uncontended cache."""
+
+    full = [[2] * 7 for _ in range(4)]
+    calm = _pressured("none", full, num_blocks=64, refill=refill)
+    hot = _pressured("recompute", full, refill=refill)
+    assert hot["stats"]["recompute_preemptions"] > 0 and hot["stats"]["offload_preemptions"] == 0
+    assert hot["tokens"] == calm["tokens"]
+    assert hot["free_blocks_at_end"] == 6
+    assert all(len(t) == 8 for t in hot["tokens"])
+
+
+@pytest.mark.parametrize("refill", [True, False])
+def test_swap_reproduces_the_uncontended_tokens_at_any_exit_schedule(refill: bool) -> None:
+    varied = [[0, 1, 2, 1, 0, 2, 1] for _ in range(4)]
+    calm = _pressured("none", varied, num_blocks=64, refill=refill)
+    hot = _pressured("offload", varied, swap_blocks=64, refill=refill)
+    s = hot["stats"]
+    assert s["offload_preemptions"] > 0 and s["restores"] == s["offload_preemptions"]
+    assert s["recompute_preemptions"] == 0
+    assert hot["tokens"] == calm["tokens"] and hot["exit_depths"] == calm["exit_depths"]
+
+
+def test_a_full_host_pool_falls_back_to_soft_reset_unless_exits_rewrite_kv() -> None:
+    varied = [[0, 1, 2, 1, 0, 2, 1] for _ in range(4)]
+    hot = _pressured("offload", varied, swap_blocks=1)
+    assert hot["stats"]["recompute_preemptions"] > 0
+    with pytest.raises(ScheduleOracleError):
+        _pressured("offload", varied, swap_blocks=1, kv_policy="last_exited")
+
+
+def test_a_single_request_that_cannot_fit_is_an_error() -> None:
+    with pytest.raises(ScheduleOracleError, match="single request"):
+        ScheduleOracle(max_recurrent_steps=3, num_blocks=2, block_size=2, max_model_len=12, safety_margin=0.0,
+                       kv_pressure_mode="recompute").run([[1, 2]], 8)

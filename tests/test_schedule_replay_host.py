@@ -175,3 +175,125 @@ def test_mixed_slot_launches_match_the_oracle_and_keep_results(seed, policy) -> 
     _, homogeneous, _ = run_both(base, prompts, mnt, depths=depths)
     assert [o.generated_tokens for o in outs] == [o.generated_tokens for o in homogeneous]
     assert [o.exit_depths for o in outs] == [o.exit_depths for o in homogeneous]
+
+
+# -- KV pressure: parking, preemption (swap or soft reset) and restores -------------------------------------------
+PRESSURED = dict(num_blocks=8, block_size=4, max_num_batched_tokens=16, max_model_len=48, max_recurrent_steps=4,
+                 safety_margin=0.0, max_num_seqs=6, synthetic_exit_replay=True, delay_gate_consumption=False)
+
+
+def _host_pool_gib(blocks: int, **cfg) -> float:
+    """cpu_offload_space that holds exactly ``blocks`` KV blocks of this engine's cache."""
+
+    probe = make_engine(kv_pressure_mode="offload", cpu_offload_space=1.0, **cfg)
+    return (blocks * probe.offloading_manager.bytes_per_block() + 1) / 1024 ** 3
+
+
+def run_pressured(cfg: dict, prompts, mnt, depths):
+    engine = make_engine(**cfg)
+    engine.record_launches = True
+    engine.consume_all_results = True
+    outs = engine.generate_batch([list(p) for p in prompts], max_new_tokens=mnt, eos_token_id=None,
+                                 exit_depths=depths)
+    okw = {k: v for k, v in cfg.items() if k not in ("use_cuda_graph", "cpu_offload_space")}
+    want = ScheduleOracle(**okw, vocab_size=VOCAB, swap_blocks=engine.offloading_manager.num_cpu_blocks).run(
+        prompts, mnt, exit_depths=depths)
+    return engine, outs, want
+
+
+PRESSURE_CASES = {"recompute": ("recompute", 0), "offload": ("offload", 64), "offload-small-pool": ("offload", 2)}
+
+
+@pytest.mark.parametrize("seed", range(4))
+@pytest.mark.parametrize("use_async", [False, True])
+@pytest.mark.parametrize("refill", [True, False])
+@pytest.mark.parametrize("case", sorted(PRESSURE_CASES))
+def test_replay_schedule_matches_under_kv_pressure(seed, use_async, refill, case) -> None:
+    """An over-subscribed cache (8 blocks of 4 tokens for 10 requests of up to 22 tokens): every
+    launch, every preemption's effect on the queues and blocks, and the tokens equal the oracle's,
+    with decoders parked and retried, the least-computed one preempted, swapped to a host pool
+    when it holds its blocks (restored first on later ticks) and soft-reset otherwise."""
+
+    mode, pool = PRESSURE_CASES[case]
+    prompts, mnt, depths = workload(seed + 40, 10, 4)
+    cfg = dict(PRESSURED, refill=refill, use_async_batching=use_async, kv_pressure_mode=mode)
+    if pool:
+        cfg["cpu_offload_space"] = _host_pool_gib(pool, **PRESSURED)
+    engine, outs, want = run_pressured(cfg, prompts, mnt, depths)
+    assert_same_schedule(engine, outs, want)
+    om, ws = engine.offloading_manager, want["stats"]
+    assert om.num_offload_preemptions == ws["offload_preemptions"]
+    assert om.num_recompute_preemptions == ws["recompute_preemptions"]
+    assert om.num_restores == ws["restores"]
+
+
+def test_pressure_replays_exercise_every_preemption_path() -> None:
+    """Across the seeds above, each case preempts, the small pool both swaps and soft-resets, and
+    swapped requests come back."""
+
+    seen = {case: [0, 0, 0] for case in PRESSURE_CASES}
+    for case, (mode, pool) in PRESSURE_CASES.items():
+        for seed in range(4):
+            prompts, mnt, depths = workload(seed + 40, 10, 4)
+            cfg = dict(PRESSURED, refill=True, use_async_batching=True, kv_pressure_mode=mode)
+            if pool:
+                cfg["cpu_offload_space"] = _host_pool_gib(pool, **PRESSURED)
+            _, _, want = run_pressured(cfg, prompts, mnt, depths)
+            s = want["stats"]
+            seen[case] = [a + b for a, b in zip(seen[case], (s["offload_preemptions"], s["recompute_preemptions"],
+                                                              s["restores"]))]
+    assert seen["recompute"][1] > 0 and seen["recompute"][0] == 0
+    assert seen["offload"][0] > 0 and seen["offload"][1] == 0 and seen["offload"][2] == seen["offload"][0]
+    assert seen["offload-small-pool"][0] > 0 and seen["offload-small-pool"][1] > 0
+
+
+@pytest.mark.parametrize("mistake", ["first_parked_victim", "soft_reset_keeps_cursor", "restore_after_prompts"])
+def test_the_pressure_comparison_catches_a_planted_mistake(monkeypatch, mistake) -> None:
+    """A plausible preemption mistake, planted in the oracle, must make the comparison fail: the
+    first parked request as the victim instead of the least-computed one, a soft reset that
+    replays the pending token's depth again, restores that wait behind fresh prompts."""
+
+    import oracle.scheduler as sched
+
+    case = "offload" if mistake == "restore_after_prompts" else "recompute"
+    if mistake == "first_parked_victim":
+        original = sched.ScheduleOracle._yield_parked
+
+        def first(self):
+            rid = next(iter(self.parked))
+            keep = {k: v for k, v in self.parked.items()}
+            self.parked = {rid: keep[rid]}  # the restated rule then has one candidate
+            original(self)
+            self.parked = {k: v for k, v in keep.items() if k != rid}
+        monkeypatch.setattr(sched.ScheduleOracle, "_yield_parked", first)
+    elif mistake == "soft_reset_keeps_cursor":
+        original = sched.ScheduleOracle._yield_parked
+
+        def keep_cursor(self):
+            before = {rid: (r.depths, r.cursor) for rid, r in self.parked.items()}
+            original(self)
+            for rid, (depths, cursor) in before.items():
+                r = self.waiting.get(rid)
+                if r is not None and r.status == "pending" and not r.offloaded:
+                    r.depths = depths[cursor:]
+        monkeypatch.setattr(sched.ScheduleOracle, "_yield_parked", keep_cursor)
+    else:
+        original = sched.ScheduleOracle._restore
+
+        def late(self):
+            if any(not r.offloaded for r in self.waiting.values()):
+                return []  # fresh prompts first
+            return original(self)
+        monkeypatch.setattr(sched.ScheduleOracle, "_restore", late)
+    mode, pool = PRESSURE_CASES[case]
+    failures = 0
+    for seed in range(4):
+        prompts, mnt, depths = workload(seed + 40, 10, 4)
+        cfg = dict(PRESSURED, refill=True, use_async_batching=True, kv_pressure_mode=mode)
+        if pool:
+            cfg["cpu_offload_space"] = _host_pool_gib(pool, **PRESSURED)
+        try:
+            assert_same_schedule(*run_pressured(cfg, prompts, mnt, depths))
+        except (AssertionError, sched.ScheduleOracleError):
+            failures += 1
+    assert failures > 0

@@ -183,3 +183,50 @@ def test_ouro_2p6b_512_sequence_single_kv_schedule_replay() -> None:
           f"refills {engine.last_stats.scheduler_refills}", flush=True)
     del engine, model
     torch.cuda.empty_cache()
+
+
+def test_ouro_2p6b_shape_per_step_kv_under_pressure_schedule_replay() -> None:
+    """The per-step workload under KV pressure: Ouro-2.6B shape (48 layers), last_exited KV with
+    exit copies, 64 sequences of the headline distributions on a pool of a third of the blocks
+    they need with no admission margin, offload to a pinned host pool (a soft reset would replace exit-step KV). Every launch,
+    every swap-out and restore, the exit-copy count and the free blocks at the end equal the
+    schedule oracle's run with the same host pool."""
+
+    from continuous_depth_batching_amd.config import ContinuousDepthBatchingConfig
+    from continuous_depth_batching_amd.engine import ContinuousDepthBatchingEngine
+    from continuous_depth_batching_amd.ouro import build_ouro, ouro_1p4b_config
+    from continuous_depth_batching_amd.workloads import ouro_decode_workload
+
+    cfg = ouro_1p4b_config(num_hidden_layers=48)
+    model = build_ouro(cfg, seed=1, dtype=torch.bfloat16, device="cuda")
+    prompts, mnt, depths = ouro_decode_workload(64, cfg.vocab_size)
+    prompts = [p[:600] for p in prompts]
+    mnt = [min(m, 96) for m in mnt]
+    depths = [d[: m - 1] for d, m in zip(depths, mnt)]
+    need = sum(-(-(len(p) + o + 1) // 16) for p, o in zip(prompts, mnt))
+    common = dict(max_recurrent_steps=4, num_blocks=need // 3, block_size=16, max_model_len=4096, max_num_seqs=64,
+                  kv_policy="last_exited", refill=True, synthetic_exit_replay=True, delay_gate_consumption=False,
+                  kv_pressure_mode="offload", safety_margin=0.0)
+    engine = ContinuousDepthBatchingEngine.from_model(model, ContinuousDepthBatchingConfig(
+        cpu_offload_space=64.0, **common))
+    engine.record_launches = True
+    engine.consume_all_results = True
+    outs = engine.generate_batch(prompts, max_new_tokens=mnt, eos_token_id=None, exit_depths=depths)
+    torch.cuda.synchronize()
+    om = engine.offloading_manager
+    want = ScheduleOracle(swap_blocks=om.num_cpu_blocks, **{k: v for k, v in common.items() if k != "kv_pressure_mode"},
+                          kv_pressure_mode="offload").run(prompts, mnt, exit_depths=depths)
+    for k, (g, w) in enumerate(zip(engine.launch_log, want["events"])):
+        assert g == w, f"launch {k} of {len(want['events'])} differs:\n engine {g}\n oracle {w}"
+    assert len(engine.launch_log) == len(want["events"])
+    assert [o.exit_depths for o in outs] == want["exit_depths"] == depths
+    s, ws = engine.last_stats, want["stats"]
+    assert s.exit_kv_copies == ws["exit_kv_copies"] > 0
+    assert om.num_offload_preemptions == ws["offload_preemptions"] > 0
+    assert om.num_restores == ws["restores"] == om.num_offload_preemptions
+    assert om.num_recompute_preemptions == ws["recompute_preemptions"] == 0
+    assert engine.cache.get_num_free_blocks() == engine.cache.num_blocks == want["free_blocks_at_end"]
+    print(f"\n[per-step pressure replay] {len(engine.launch_log)} launches, {om.num_offload_preemptions} swaps, "
+          f"{s.exit_kv_copies} exit copies", flush=True)
+    del engine, model
+    torch.cuda.empty_cache()

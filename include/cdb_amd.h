@@ -37,9 +37,9 @@ enum { CDB_DTYPE_F32 = 0, CDB_DTYPE_BF16 = 1 };
 
 /* Bytes of decode workspace for num_rows rows whose new-token positions are
  * all < max_seqlen with chunks of split_pages pages: an int32 header of
- * num_rows + 2 entries padded to 256 bytes and 1 KiB of work-queue counters
- * (kept at zero between calls by the kernels themselves), then per chunk a
- * 64-byte descriptor and an
+ * num_rows + 2 entries padded to 256 bytes, 1 KiB of work-queue counters and
+ * one int32 arrival counter per (row, head) padded to 256 bytes (all zeroed by
+ * the plan), then per chunk a 64-byte descriptor and an
  * fp32 partial of num_heads * (head_dim + 2) floats. A smaller workspace is
  * legal as long as it holds the header and one chunk per row: the plan then
  * lengthens the chunks until they fit. Returns -1 on bad input. */
@@ -117,12 +117,13 @@ int cdb_paged_decode_attention_staged(const void* q, const void* k_new, const vo
  * hipMalloc. Same arguments and results without the workspace: the split header and partials
  * live in a fixed device array of CDB_DECODE_SCRATCH_BYTES per GPU (resolved once per device,
  * held until the process ends). The call allocates nothing and frees nothing. Nothing in the
- * scratch must start at zero: each call writes its header and partials before reading them.
+ * scratch must start at zero: each call's plan writes its header and zeroes its counters before
+ * the decode kernel reads them.
  * Every call on one GPU shares that GPU's array, so calls that overlap on one GPU (two streams,
  * or two threads) race; serialize them. Returns CDB_ERR_CAPACITY when the header plus one
  * chunk per row (a 64-byte descriptor and num_heads * (head_dim + 2) floats) exceeds the
- * scratch (at 16 heads x 128: more than 2000 rows); a smaller surplus only lengthens the
- * chunks. */
+ * scratch after the header, queue counters and arrival counters (at 16 heads x 128: more than
+ * 1984 rows); a smaller surplus only lengthens the chunks. */
 #define CDB_DECODE_SCRATCH_BYTES ((int64_t)16 << 20)
 int cdb_paged_decode_attention_noalloc(const void* q, const void* k_new, const void* v_new, void* k_pool,
                                        void* v_pool, int64_t layer_stride, int32_t num_cache_layers,

@@ -102,6 +102,27 @@ def _prelude_event(site: str, items: list[DepthWorkItem]) -> tuple:
     return ("prelude", site, tuple((i.state.request_id, i.token_position, i.hidden_slot) for i in items))
 
 
+@dataclass
+class _WaveCarry:
+    """What one no-refill iteration leaves for the next on the delayed horizon
+    (cdb/continuous_api.py:80-110 keeps the same three parts).
+
+    ``groups`` are successors built before their tokens are on the host, each group with the
+    staged result whose device tokens its rows index; the next wave's one prelude gathers them.
+    ``coda`` is the last wave's staged coda, read after the next wave's first launch.
+    ``prefills`` are prompt readbacks, applied at the top of the next iteration."""
+
+    groups: list[tuple[Any, list[DepthWorkItem], list[int]]] = field(default_factory=list)
+    coda: PendingCodaResult | None = None
+    prefills: list[PendingPrefillResult] = field(default_factory=list)
+
+    def num_items(self) -> int:
+        return sum(len(items) for _, items, _ in self.groups)
+
+    def empty(self) -> bool:
+        return not self.groups and self.coda is None and not self.prefills
+
+
 DEFAULT_MEM_FRACTION_STATIC = 0.8
 
 
@@ -653,11 +674,22 @@ class ContinuousDepthBatchingEngine:
         raise RuntimeError(f"request {head.request_id} cannot be scheduled: its {head.current_len()} KV tokens "
                            f"exceed the cache budget of {self.cache.num_pages} tokens")
 
-    # -- no-refill baseline (continuous_api.py:608-944, synchronous wave form) ----------------------------------
+    # -- no-refill baseline (continuous_api.py:608-944) ---------------------------------------------------------
     def _run_no_refill_loop(self) -> None:
+        """Sequence-level baseline: each iteration prefills while admission allows, then runs one
+        lockstep wave over every decoder whose token is sampled; rows that exit are not refilled.
+
+        On the delayed horizon nothing in the loop waits for a readback: a prefill's first tokens
+        and a wave's coda stay staged, their successors are built ahead of the tokens, and the next
+        wave's one prelude gathers those tokens on the device. The coda is read after that wave's
+        first launch, so a finish it reveals cancels the successor then."""
+
         sched = self.scheduler
-        max_steps = self.cdb_config.max_recurrent_steps or 0
+        carry = _WaveCarry()
         while sched.has_pending_work():
+            prefills, carry.prefills = carry.prefills, []
+            for pending in prefills:
+                self._apply_wave_prefill(pending)
             # Restored requests decode again, so they join this wave's cohort scan.
             self._restore_offloaded_requests()
             sched.record_resident_sample()
@@ -667,94 +699,179 @@ class ContinuousDepthBatchingEngine:
                                                          cache_budget=self.cache.num_pages)
                 if scheduled is None or not scheduled.requests:
                     break
-                self._run_no_refill_prefill(scheduled)
+                self._run_no_refill_prefill(scheduled, carry)
                 did_prefill = True
-            cohort = [s for s in sched.active_requests.values()
-                      if s.status == RequestStatus.DECODING and s.tokens_to_process and s.tokens_to_process[0] >= 0]
-            cohort = cohort[: self.cdb_config.max_num_seqs]
-            items = [item for s in cohort if (item := self.staging.stage(s)) is not None]
-            if not items:
-                if not did_prefill:
-                    if self.staging.parked:
-                        # No wave can run and no parked decoder can allocate: take one's KV away.
-                        self.staging.yield_one(len(sched.active_requests))
-                        continue
-                    if sched.has_pending_work():
-                        raise CacheFullError("no-refill wave dead end: no waiting prompt fits the KV cache "
-                                             "and no decode token is ready")
+            if self._run_wave(carry) or did_prefill:
                 continue
-            self._record_prelude("wave_cohort", len(items))
-            self.runner.compute_prelude_batch(items)
-            if self.record_launches:
-                self.launch_log.append(_prelude_event("wave_cohort", items))
-            survivors = items
-            exited: list[DepthWorkItem] = []
-            # On the delayed horizon a launch's decisions route the item after its next launch,
-            # exactly as in the refill loop.
-            delayed = self.exit_policy.delayed()
-            previous: dict[int, tuple[PendingFlags, int]] = {}
-            for step in range(max_steps):
-                for item in survivors:
-                    item.recurrent_step = step
-                rows = self._recurrent_rows(survivors) if self.record_launches else None
-                flags = self.runner.compute_recurrent_batch(survivors)
-                self.last_stats.recurrent_batches += 1
-                self.last_stats.recurrent_steps += len(survivors)
-                self.last_stats.recurrent_step_histogram[step] += len(survivors)
-                continuing = []
-                exits = []
-                for idx, item in enumerate(survivors):
-                    if delayed:
-                        prev = previous.pop(id(item), None)
-                        gate_exit = item.apply_exit_gate and prev is not None and prev[0].get(prev[1])
-                    else:
-                        gate_exit = item.apply_exit_gate and flags.get(idx)
-                    leave = step == max_steps - 1 or bool(gate_exit)
-                    exits.append(leave)
-                    if leave:
-                        self._record_exit(item, step)
-                        exited.append(item)
-                    else:
-                        continuing.append(item)
-                        if delayed:
-                            previous[id(item)] = (flags, idx)
-                self._flush_exit_kv_copies()
-                if self.record_launches:
-                    self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), self.scheduler.refill_events))
-                survivors = continuing
-                if not survivors:
-                    break
-            pending = self.runner.stage_coda_batch(exited, allow_async=False)
-            if self.record_launches:
-                self.launch_log.append(("coda", tuple((i.state.request_id, i.token_position, i.hidden_slot)
-                                                      for i in exited)))
-            tokens = self.runner.consume_coda_result(pending)
-            self.last_stats.coda_batches += 1
-            self.last_stats.coda_tokens += len(exited)
-            for item, token in zip(exited, tokens):
-                if item.state.status != RequestStatus.FINISHED:
-                    self._advance_after_coda(item, token)
+            if self.staging.parked:
+                # No wave can run and no parked decoder can allocate: take one's KV away.
+                self.staging.yield_one(len(sched.active_requests))
+                continue
+            if sched.has_pending_work():
+                raise CacheFullError("no-refill wave dead end: no waiting prompt fits the KV cache "
+                                     "and no decode token is ready")
+        if not carry.empty():
+            raise RuntimeError("no-refill loop ended with staged work still carried: its requests would "
+                               "have counted as pending")
         self._finish_stats()
 
-    def _run_no_refill_prefill(self, scheduled: ScheduledCDBBatch) -> None:
+    def _run_no_refill_prefill(self, scheduled: ScheduledCDBBatch, carry: _WaveCarry) -> None:
         requests = scheduled.requests or []
         stats = self.last_stats
         stats.prefill_batches += 1
         stats.prefill_requests += len(requests)
         stats.prefill_recurrent_steps += scheduled.num_q_tokens * (self.cdb_config.max_recurrent_steps or 0)
-        pending = self.runner.stage_prefill_batch(requests, allow_async=False)
+        delayed = self.exit_policy.delayed()
+        pending = self.runner.stage_prefill_batch(requests, allow_async=self.cdb_config.use_async_batching)
         if self.record_launches:
             self.launch_log.append(self._prefill_event(requests))
-        tokens = self.runner.consume_prefill_result(pending)
-        k = 0
+        # Successors that enter this iteration's wave ahead of their token, within the launch
+        # width the carried successors leave.
+        room = max(0, self.cdb_config.max_num_seqs - carry.num_items())
+        flags: list[bool] = []
+        ahead: list[DepthWorkItem] = []
+        rows: list[int] = []
         for future in requests:
-            self.scheduler.release_in_flight_request(future.state.request_id)
-            if not future.has_new_token:
+            state = future.state
+            if future.has_new_token:
+                stats.prefill_coda_tokens += 1
+                enter = (delayed and len(ahead) < room and not state.will_finish_on_pending_token()
+                         and self.staging.reserve_row(state))
+                if enter:
+                    rows.append(len(flags))
+                    ahead.append(self.staging.work_item(state, token_id=TMP_TOKEN_ID))
+                flags.append(enter)
+            self.scheduler.release_in_flight_request(state.request_id)
+        pending.eager_entries = flags
+        if not delayed:
+            self._apply_wave_prefill(pending)
+            return
+        if ahead:
+            carry.groups.append((pending, ahead, rows))
+        carry.prefills.append(pending)
+
+    def _apply_wave_prefill(self, pending: PendingPrefillResult) -> None:
+        """A prefill's first tokens. The wave's cohort scan stages the next token, so this only
+        records each token; a successor that already entered a wave is cancelled by a finish."""
+
+        tokens = self.runner.consume_prefill_result(pending)
+        entered = pending.eager_entries or [False] * len(tokens)
+        sampled = (f.state for f in pending.futures if f.has_new_token)
+        for state, token, _ in zip(sampled, tokens, entered, strict=True):
+            if state.status != RequestStatus.FINISHED and state.update_and_check_completion(token):
+                self._retire_request(state)
+
+    def _apply_wave_coda(self, pending: PendingCodaResult) -> None:
+        tokens = self.runner.consume_coda_result(pending)
+        self.last_stats.coda_batches += 1
+        self.last_stats.coda_tokens += len(pending.items)
+        ahead = pending.eager_reentries or [False] * len(tokens)
+        for item, token, entered in zip(pending.items, tokens, ahead, strict=True):
+            state = item.state
+            if state.status == RequestStatus.FINISHED:
                 continue
-            stats.prefill_coda_tokens += 1
-            token = tokens[k]
-            k += 1
-            self._advance_after_prefill(future.state, token)
+            if not entered:
+                self._advance_after_coda(item, token)
+            elif state.update_and_check_completion(token):
+                self._retire_request(state)
+
+    def _run_wave(self, carry: _WaveCarry) -> bool:
+        """One lockstep wave; returns whether it did any work (a launch, or reading a carried coda)."""
+
+        sched = self.scheduler
+        stats = self.last_stats
+        groups, coda = carry.groups, carry.coda
+        carry.groups, carry.coda = [], None
+        # A request retired since its successor was built (a first token read at the top of this
+        # iteration) loses that successor; it never took a hidden slot.
+        live_groups = []
+        for result, items, rows in groups:
+            keep = [(i, r) for i, r in zip(items, rows) if i.state.status != RequestStatus.FINISHED]
+            stats.cancelled_depth_items += len(items) - len(keep)
+            if keep:
+                live_groups.append((result, [i for i, _ in keep], [r for _, r in keep]))
+        carried = [item for _, items, _ in live_groups for item in items]
+        # Requests whose coda is still unread hold a token one wave behind: not scanned now.
+        behind = {i.state.request_id for i in coda.items} if coda is not None else set()
+        cohort = [s for s in sched.active_requests.values()
+                  if s.status == RequestStatus.DECODING and s.tokens_to_process and s.tokens_to_process[0] >= 0
+                  and s.request_id not in behind]
+        cohort = cohort[: max(0, self.cdb_config.max_num_seqs - len(carried))]
+        items = carried + [item for s in cohort if (item := self.staging.stage(s)) is not None]
+        if not items:
+            if coda is None:
+                return False
+            self._apply_wave_coda(coda)
+            return True
+        self._record_prelude("wave_cohort", len(items), gathered=len(carried))
+        self.runner.compute_prelude_batch(items, device_groups=[(result, rows) for result, _, rows in live_groups])
+        if self.record_launches:
+            self.launch_log.append(_prelude_event("wave_cohort", items))
+        max_steps = self.cdb_config.max_recurrent_steps or 0
+        # On the delayed horizon a launch's decisions route the item after its next launch,
+        # exactly as in the refill loop.
+        delayed = self.exit_policy.delayed()
+        previous: dict[int, tuple[PendingFlags, int]] = {}
+        survivors = items
+        exited: list[DepthWorkItem] = []
+        for step in range(max_steps):
+            for item in survivors:
+                item.recurrent_step = step
+            rows = self._recurrent_rows(survivors) if self.record_launches else None
+            flags = self.runner.compute_recurrent_batch(survivors)
+            stats.recurrent_batches += 1
+            stats.recurrent_steps += len(survivors)
+            stats.recurrent_step_histogram[step] += len(survivors)
+            if coda is not None:
+                # Read while the wave's first launch runs; a finish it reveals cancels below.
+                self._apply_wave_coda(coda)
+                coda = None
+            continuing, cancelled, exits = [], [], []
+            for idx, item in enumerate(survivors):
+                if item.state.status == RequestStatus.FINISHED:
+                    cancelled.append(item)
+                    previous.pop(id(item), None)
+                    exits.append(False)
+                    continue
+                if delayed:
+                    prev = previous.pop(id(item), None)
+                    gate_exit = item.apply_exit_gate and prev is not None and prev[0].get(prev[1])
+                else:
+                    gate_exit = item.apply_exit_gate and flags.get(idx)
+                leave = step == max_steps - 1 or bool(gate_exit)
+                exits.append(leave)
+                if leave:
+                    self._record_exit(item, step)
+                    exited.append(item)
+                else:
+                    continuing.append(item)
+                    if delayed:
+                        previous[id(item)] = (flags, idx)
+            if cancelled:
+                self.runner.release_hidden_slots(cancelled)
+                stats.cancelled_depth_items += len(cancelled)
+            self._flush_exit_kv_copies()
+            if self.record_launches:
+                self.launch_log.append(("recurrent", rows, tuple(map(bool, exits)), sched.refill_events))
+            survivors = continuing
+            if not survivors:
+                break
+        if not exited:
+            return True
+        pending = self.runner.stage_coda_batch(exited, allow_async=delayed)
+        if self.record_launches:
+            self.launch_log.append(("coda", tuple((i.state.request_id, i.token_position, i.hidden_slot)
+                                                  for i in exited)))
+        if not delayed:
+            self._apply_wave_coda(pending)
+            return True
+        # Successors of the exited rows enter the next wave ahead of their tokens.
+        ahead, rows, flags = self._select_eager_reentries(exited)
+        pending.eager_reentries = flags
+        if ahead:
+            carry.groups.append((pending, ahead, rows))
+        carry.coda = pending
+        return True
 
     # -- validation (continuous_api.py:1746-1833) ---------------------------------------------------------------
     @staticmethod

@@ -27,7 +27,10 @@ Scheduling follows, in the reference:
     continuous_batching/requests.py:183-237, input_outputs.py:316-350;
   * exit routing on the synchronous and delayed horizons -- continuous_api.py:1090-1245,
     1671-1724, exit_policy.py:87-169;
-  * the no-refill wave loop on the synchronous horizon -- continuous_api.py:608-944.
+  * the no-refill wave loop -- continuous_api.py:608-944, with its wave-boundary carry on the
+    delayed horizon (the coda read after the next wave's first launch, first tokens at the next
+    iteration's top, successors entering the next wave's one prelude) -- :636-642, 708-785,
+    864-932, 1350-1368.
 
 ``mixed_slot_recurrent_batches`` drops the slot-homogeneous launch rule (an option of this build's
 engine, not of the reference). ``replay_offset_one`` forces the replay horizon (the reference's tests force the delayed replay
@@ -52,8 +55,8 @@ equals) gives up its KV -- swapped to a host pool of ``swap_blocks`` blocks when
 finishes; swapped requests are restored first on later ticks (offload mode only), with blocks for
 their pending token.
 
-Not modelled (the restatement raises): reserve admission, open-loop arrivals, pre-loop exit
-distributions, and the no-refill loop on the delayed horizon.
+Not modelled (the restatement raises): reserve admission, open-loop arrivals and pre-loop exit
+distributions.
 """
 
 from __future__ import annotations
@@ -171,8 +174,6 @@ class ScheduleOracle:
         # adapter declares offset one or the overlap transport is on; replay follows the transport.
         self.delayed_live = exit_threshold is not None and (offset_one_signal or overlap)
         self.delayed_replay = synthetic_exit_replay and (overlap if replay_offset_one is None else replay_offset_one)
-        if not refill and (self.delayed_live or self.delayed_replay):
-            raise ScheduleOracleError("the no-refill loop is restated on the synchronous horizon only")
         if kv_pressure_mode not in ("none", "recompute", "offload"):
             raise ScheduleOracleError(f"kv_pressure_mode {kv_pressure_mode!r} is not restated")
         self.pressure = kv_pressure_mode
@@ -552,22 +553,29 @@ class ScheduleOracle:
         self._record("coda", len(items))
         staged = _Staged("coda", tokens, items=items, eager=[False] * len(items))
         if eager_ok:
-            succ = []
-            for idx, it in enumerate(items):
-                r = it.req
-                if self._will_finish_on_pending(r):
-                    continue
-                r.pos += 1
-                if not self._grow_one(r):
-                    r.pos -= 1
-                    continue
-                staged.eager[idx] = True
-                succ.append(self._new_item(r, float(tokens[idx])))
+            succ = self._successors(staged)
             if succ:
                 self._prelude(succ, "after_coda_eager")
                 self._push_front(succ)
                 self._record("prelude", len(succ), site="after_coda_eager")
         return staged
+
+    def _successors(self, staged: _Staged) -> list[_Item]:
+        """Next items built before the coda's tokens are read (continuous_api.py:1304-1327): every
+        row whose request does not finish on its pending token and gets room for one more token."""
+
+        succ = []
+        for idx, it in enumerate(staged.items):
+            r = it.req
+            if self._will_finish_on_pending(r):
+                continue
+            r.pos += 1
+            if not self._grow_one(r):
+                r.pos -= 1
+                continue
+            staged.eager[idx] = True
+            succ.append(self._new_item(r, float(staged.tokens[idx])))
+        return succ
 
     def _consume_coda(self, staged: _Staged, *, restage: bool) -> None:
         self.stats["coda_batches"] += 1
@@ -801,10 +809,24 @@ class ScheduleOracle:
                 batch.append(self.ready.popleft())
         return batch
 
-    # -- no-refill waves on the synchronous horizon (continuous_api.py:608-944) ----------------------------------
+    # -- no-refill waves (continuous_api.py:608-944) ----------------------------------------------------------------
     def _wave_loop(self) -> None:
+        """Prefill while admission allows, then one lockstep wave over the sampled decoders.
+
+        On the delayed horizon (continuous_api.py:636-642, 708-785, 864-932) a wave's coda is read
+        only after the next wave's first launch and a prefill's first tokens at the next iteration's
+        top; the successors built ahead of those tokens (``self.ahead``, coda successors first, then
+        prompt successors) open the next wave, whose prelude takes their hidden slots."""
+
+        delayed = self.delayed_live or self.delayed_replay
+        self.ahead: list[_Item] = []
+        self.unread_coda: _Staged | None = None
+        unread_prefills: list[_Staged] = []
         while self._pending_work():
             self.tick += 1
+            for staged in unread_prefills:
+                self._first_tokens(staged)
+            unread_prefills = []
             self._restore()  # restored decoders join this wave's cohort scan
             ran_prefill = False
             while self._admit_prefill():
@@ -813,21 +835,24 @@ class ScheduleOracle:
                     break
                 batch, num_q = packed
                 staged = self._stage_prefill(batch, num_q)
+                room = max(0, self.cap - len(self.ahead))
+                entered = []
                 for r, _, new in batch:
                     if new:
                         self.stats["prefill_coda_tokens"] += 1
-                        staged.eager.append(False)
+                        enter = (delayed and len(entered) < room and not self._will_finish_on_pending(r)
+                                 and self._grow_one(r))
+                        if enter:
+                            entered.append(self._new_item(r, float(staged.tokens[len(staged.eager)])))
+                        staged.eager.append(enter)
                     self.in_flight.discard(r.rid)
-                k = 0
-                for r, _, new in batch:
-                    if not new:
-                        continue
-                    tok = staged.tokens[k]
-                    k += 1
-                    if r.status != "finished" and self._take_token(r, tok):
-                        self._retire(r)
+                if delayed:
+                    self.ahead += entered
+                    unread_prefills.append(staged)
+                else:
+                    self._first_tokens(staged)
                 ran_prefill = True
-            ran_wave = self._wave()
+            ran_wave = self._wave(delayed)
             if not ran_prefill and not ran_wave:
                 if self.parked:
                     self._yield_parked()
@@ -835,13 +860,34 @@ class ScheduleOracle:
                 if not self._pending_work():
                     continue
                 raise ScheduleOracleError("no-refill loop stalled")
+        if unread_prefills or self.ahead or self.unread_coda is not None:
+            raise ScheduleOracleError("no-refill loop ended with unread results")
 
-    def _wave(self) -> bool:
+    def _first_tokens(self, staged: _Staged) -> None:
+        k = 0
+        for r, _, new in staged.items:
+            if not new:
+                continue
+            tok = staged.tokens[k]
+            k += 1
+            if r.status != "finished" and self._take_token(r, tok):
+                self._retire(r)
+
+    def _wave(self, delayed: bool) -> bool:
+        ahead = [it for it in self.ahead if it.req.status != "finished"]
+        self.stats["cancelled"] += len(self.ahead) - len(ahead)
+        self.ahead = []
+        coda, self.unread_coda = self.unread_coda, None
+        behind = {it.req.rid for it in coda.items} if coda is not None else set()
         cohort = [r for r in self.active.values()
-                  if r.status == "decoding" and r.to_process and r.to_process[0] >= 0][: self.cap]
-        items = [it for r in cohort if (it := self._stage_decode(r)) is not None]
+                  if r.status == "decoding" and r.to_process and r.to_process[0] >= 0 and r.rid not in behind]
+        cohort = cohort[: max(0, self.cap - len(ahead))]
+        items = ahead + [it for r in cohort if (it := self._stage_decode(r)) is not None]
         if not items:
-            return False
+            if coda is None:
+                return False
+            self._consume_coda(coda, restage=False)
+            return True
         self._prelude(items, "wave_cohort")
         self._record("prelude", len(items), site="wave_cohort", cohort=len(items))
         live = items
@@ -853,15 +899,36 @@ class ScheduleOracle:
             signals = self._step_rows(live)
             self.stats["recurrent_batches"] += 1
             self.stats["recurrent_steps"] += len(live)
-            keep, out, exits = [], [], []
+            if coda is not None:
+                self._consume_coda(coda, restage=False)
+                coda = None
+            keep, out, exits, dead = [], [], [], []
             for it, sig in zip(live, signals):
-                leave = self._decide_now(it, sig)
+                if it.req.status == "finished":
+                    dead.append(it)
+                    exits.append(False)
+                    continue
+                if self.delayed_live:
+                    prev, it.pending_signal = it.pending_signal, None
+                    leave = step == self.R - 1 or (prev is not None and self._policy(it, prev[0], prev[1]))
+                    if not leave:
+                        it.pending_signal = (step, sig)
+                elif self.delayed_replay:
+                    prev, it.pending_step = it.pending_step, None
+                    leave = step == self.R - 1 or (prev is not None and it.depth is not None and prev >= it.depth)
+                    if not leave:
+                        it.pending_step = step
+                else:
+                    leave = self._decide_now(it, sig)
                 exits.append(leave)
                 if leave:
                     self._mark_exit(it, step)
                     out.append(it)
                 else:
                     keep.append(it)
+            if dead:
+                self._free_slots(dead)
+                self.stats["cancelled"] += len(dead)
             self._flush_copies()
             self.events.append(("recurrent", tuple(rows), tuple(exits), self.stats["refills"]))
             self._record("recurrent", len(live), depths={step: len(live)}, exited=len(out), cohort=len(items))
@@ -869,8 +936,14 @@ class ScheduleOracle:
             live = keep
             if not live:
                 break
+        if not done:
+            return True
         staged = self._stage_coda(done, eager_ok=False)
-        self._consume_coda(staged, restage=False)
+        if delayed:
+            self.ahead = self._successors(staged)
+            self.unread_coda = staged
+        else:
+            self._consume_coda(staged, restage=False)
         return True
 
 

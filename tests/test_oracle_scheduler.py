@@ -133,12 +133,7 @@ def test_async_eager_reentry_matches_the_synchronous_streams() -> None:
 @pytest.mark.parametrize("refill", [True, False])
 @pytest.mark.parametrize("offset_one,use_async,delay,expected", [(False, False, False, 0), (True, True, True, 1)])
 def test_decision_horizon_sets_the_exit_depth(refill, offset_one, use_async, delay, expected) -> None:
-    # test_continuous_depth_batching.py:1117-1153 (the no-refill loop on the synchronous horizon only)
-    if not refill and expected == 1:
-        with pytest.raises(ScheduleOracleError):
-            oracle(exit_threshold=0.5, refill=False, use_async_batching=True, delay_gate_consumption=True,
-                   offset_one_signal=True)
-        return
+    # test_continuous_depth_batching.py:1117-1153
     r = oracle(exit_threshold=0.5, refill=refill, use_async_batching=use_async, delay_gate_consumption=delay,
                offset_one_signal=offset_one).run([[1]], 2)
     assert r["stats"]["exit_depth_histogram"] == {expected: 1}
@@ -368,3 +363,24 @@ def test_a_single_request_that_cannot_fit_is_an_error() -> None:
     with pytest.raises(ScheduleOracleError, match="single request"):
         ScheduleOracle(max_recurrent_steps=3, num_blocks=2, block_size=2, max_model_len=12, safety_margin=0.0,
                        kv_pressure_mode="recompute").run([[1, 2]], 8)
+
+
+def test_no_refill_delayed_wave_cancels_the_successor_of_a_late_eos() -> None:
+    # test_continuous_depth_batching.py:596-624: on the delayed horizon an EOS is read only with
+    # the boundary coda, one wave after its successor entered; request 2's first token is the EOS,
+    # read after its carried successor was built, which is then dropped at the next wave's entry.
+    prompts = [[1], [4], [5]]
+    depths = [[0] * 5, [1] * 5, [0] * 5]
+    kw = dict(synthetic_exit_replay=True, replay_offset_one=True)
+    refill = oracle(**kw).run(prompts, 6, eos_token_id=8, exit_depths=depths)
+    wave = oracle(**kw, refill=False).run(prompts, 6, eos_token_id=8, exit_depths=depths)
+    assert wave["tokens"] == refill["tokens"]
+    assert wave["tokens"][2] == [8]
+    assert any(t and t[-1] == 8 for t in wave["tokens"])
+    assert wave["stats"]["cancelled_depth_items"] > 0
+    # One recurrent step for the cancelled successor (cancelled at step 0, after the launch) and
+    # two for request 2's first decode token (depth 0 applied one step late) before its EOS is read.
+    assert wave["stats"]["recurrent_steps"] == refill["stats"]["recurrent_steps"] + 3
+    assert wave["stats"]["scheduler_refills"] == 0
+    assert set(wave["stats"]["prelude_tokens"]) == {"wave_cohort"}
+    assert wave["free_blocks_at_end"] == 16

@@ -60,7 +60,7 @@ def replay_and_compare(model, prompts, mnt, depths, **cfg):
 @pytest.mark.parametrize("policy,use_async,delay,refill", [
     ("single", True, False, True), ("single", False, False, True), ("single", True, True, True),
     ("last_exited", True, False, True), ("last_exited", True, True, True), ("single", False, False, False),
-    ("last_exited", False, False, False)])
+    ("last_exited", False, False, False), ("single", True, True, False), ("last_exited", True, True, False)])
 def test_tiny_ouro_schedule_replay(policy, use_async, delay, refill) -> None:
     from tests.test_engine_gpu import build_model
 

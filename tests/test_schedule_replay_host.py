@@ -84,10 +84,14 @@ def test_replay_schedule_matches_on_the_synchronous_horizon(seed, use_async, ref
 
 
 @pytest.mark.parametrize("seed", range(4))
-def test_replay_schedule_matches_on_the_delayed_horizon(seed) -> None:
+@pytest.mark.parametrize("refill", [True, False])
+def test_replay_schedule_matches_on_the_delayed_horizon(seed, refill) -> None:
+    """On the delayed horizon without refill, each wave carries its coda, the prompts' first
+    tokens and the successors built ahead of them into the next wave (continuous_api.py:808-944)."""
+
     prompts, mnt, depths = workload(seed + 10, 10, 4)
     cfg = dict(BIG, max_num_seqs=6, kv_policy="last_exited", use_async_batching=True,
-               delay_gate_consumption=True, synthetic_exit_replay=True)
+               delay_gate_consumption=True, synthetic_exit_replay=True, refill=refill)
     assert_same_schedule(*run_both(cfg, prompts, mnt, depths=depths))
 
 
@@ -104,8 +108,6 @@ def test_chunked_prefill_eos_and_min_coda_batches(seed, use_async) -> None:
 @pytest.mark.parametrize("use_async,delay", [(False, False), (True, False), (True, True)])
 @pytest.mark.parametrize("refill", [True, False])
 def test_live_gate_schedule_matches(rule, threshold, use_async, delay, refill) -> None:
-    if not refill and delay:
-        pytest.skip("the oracle restates the no-refill loop on the synchronous horizon")
     prompts, mnt, _ = workload(31, 8, 3)
     cfg = dict(BIG, max_recurrent_steps=3, max_num_seqs=4, refill=refill, use_async_batching=use_async,
                delay_gate_consumption=delay, exit_threshold=threshold)
@@ -245,6 +247,56 @@ def test_pressure_replays_exercise_every_preemption_path() -> None:
     assert seen["recompute"][1] > 0 and seen["recompute"][0] == 0
     assert seen["offload"][0] > 0 and seen["offload"][1] == 0 and seen["offload"][2] == seen["offload"][0]
     assert seen["offload-small-pool"][0] > 0 and seen["offload-small-pool"][1] > 0
+
+
+DELAYED_WAVE = dict(BIG, max_num_seqs=6, kv_policy="last_exited", use_async_batching=True,
+                    delay_gate_consumption=True, synthetic_exit_replay=True, refill=False)
+
+
+def test_delayed_waves_exercise_every_carry_path() -> None:
+    """The delayed no-refill replays must reach successors gathered from a carried coda or
+    prompt, and successors cancelled by a finish read one wave late."""
+
+    gathered = cancelled = 0
+    for seed in range(4):
+        prompts, mnt, depths = workload(seed + 10, 10, 4)
+        engine, outs, want = run_both(DELAYED_WAVE, prompts, mnt, depths=depths, eos=5)
+        assert_same_schedule(engine, outs, want)
+        gathered += engine.last_stats.prelude_gathered_tokens["wave_cohort"]
+        cancelled += engine.last_stats.cancelled_depth_items
+    assert gathered > 0 and cancelled > 0
+
+
+@pytest.mark.parametrize("mistake", ["coda_read_before_the_wave", "successors_reversed", "no_coda_successors"])
+def test_the_delayed_wave_comparison_catches_a_planted_mistake(monkeypatch, mistake) -> None:
+    """A plausible mistake in the wave-boundary carry, planted in the oracle, must make the
+    comparison fail: the last wave's coda read before the next wave's prelude (as on the
+    synchronous horizon), the carried successors entering in reverse order, or no successors
+    built for a wave's coda rows."""
+
+    import oracle.scheduler as sched
+
+    if mistake == "no_coda_successors":
+        monkeypatch.setattr(sched.ScheduleOracle, "_successors", lambda self, staged: [])
+    else:
+        original = sched.ScheduleOracle._wave
+
+        def planted(self, delayed):
+            if mistake == "successors_reversed":
+                self.ahead = self.ahead[::-1]
+            elif self.unread_coda is not None:
+                coda, self.unread_coda = self.unread_coda, None
+                self._consume_coda(coda, restage=False)
+            return original(self, delayed)
+        monkeypatch.setattr(sched.ScheduleOracle, "_wave", planted)
+    failures = 0
+    for seed in range(4):
+        prompts, mnt, depths = workload(seed + 10, 10, 4)
+        try:
+            assert_same_schedule(*run_both(DELAYED_WAVE, prompts, mnt, depths=depths, eos=5))
+        except (AssertionError, sched.ScheduleOracleError):
+            failures += 1
+    assert failures > 0
 
 
 @pytest.mark.parametrize("mistake", ["first_parked_victim", "soft_reset_keeps_cursor", "restore_after_prompts"])

@@ -64,6 +64,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-microbench", action="store_true")
     p.add_argument("--cpu-sample-tokens", type=int, default=160)
     p.add_argument("--attention-iters", type=int, default=20)
+    p.add_argument("--attention-rows", type=int, default=256,
+                   help="decode-attention: time the first N rows of the 256-row shape (at most 120 rows run "
+                        "the deep form, which merges in the decode kernel); the bench line keeps 256")
     return p.parse_args()
 
 
@@ -166,15 +169,16 @@ def time_decode_attention(case, split_pages: int, iters: int) -> dict:
             "mean_context": float(case.contexts.mean())}
 
 
-def decode_attention_c2_case(prompts, outputs, device):
-    """The 256-row recurrent shape of the workload: each sequence mid-way through its output."""
+def decode_attention_c2_case(prompts, outputs, device, rows: int | None = None):
+    """The 256-row recurrent shape of the workload: each sequence mid-way through its output
+    (its first ``rows`` rows when given)."""
 
     import torch
 
     from continuous_depth_batching_amd.workloads import DecodeAttentionCase, rope_tables_torch
 
     rng = np.random.default_rng(5)
-    contexts = np.asarray([len(p) + max(1, o // 2) for p, o in zip(prompts, outputs)], dtype=np.int64)
+    contexts = np.asarray([len(p) + max(1, o // 2) for p, o in zip(prompts, outputs)], dtype=np.int64)[:rows]
     rows = len(contexts)
     bs = 16
     pages = (contexts + bs - 1) // bs
@@ -438,6 +442,15 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, prefill_tokens:
     if rope_batch is not None:
         out["rope_kv_write_first_prefill_batch"] = dict(row(*rope_batch), tokens=prefill_tokens)
     return out
+
+
+def decode_kernels(rows: int) -> str:
+    """The kernels one attend call runs at ``rows`` rows of 16-token pages (the decode library's
+    form choice: the deep form, which merges in the decode kernel, up to 120 rows)."""
+
+    if rows <= 120:
+        return "cdb::paged_decode_deep_kernel<bf16,128> (merge in the kernel)"
+    return "cdb::paged_decode_fast_kernel<bf16,128> + decode_merge_kernel"
 
 
 TRAFFIC_RECORD = "profiles/decode_attention_c2_256rows_traffic.json"
@@ -935,14 +948,17 @@ def main() -> int:
         print(json.dumps(line))
         return 0
 
-    attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device),
+    rows = args.attention_rows if args.workload == "decode-attention" else None
+    if rows is not None and not 1 <= rows <= len(prompts):
+        raise SystemExit(f"--attention-rows must be in [1, {len(prompts)}]")
+    attention = time_decode_attention(decode_attention_c2_case(prompts, outputs, device, rows),
                                       split_pages=0, iters=args.attention_iters)
     torch.cuda.empty_cache()
     roofline = {"bound": "hbm", "achieved": round(attention["gbps"], 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(attention["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(attention["bytes"]),
                 "traffic_source": f"{TRAFFIC_RECORD}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE on this shape, "
                                   "scaled by a 1 GiB copy",
-                "kernel": "cdb::paged_decode_fast_kernel<bf16,128> + decode_merge_kernel (one layer's attend)",
+                "kernel": decode_kernels(attention["rows"]) + " (one layer's attend)",
                 "launch_ms": round(attention["ms"], 4), "algorithmic_bytes": attention["bytes"],
                 "plan_ms": round(attention["plan_ms"], 4),
                 "plan_note": "cdb::decode_plan_kernel runs once per recurrent launch for all 24 layers",

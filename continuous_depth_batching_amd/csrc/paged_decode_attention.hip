@@ -1120,21 +1120,59 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
 // new-token and slot merge), so a row's result does not depend on the form.
 constexpr int kDeepRows = 120;  // the deep form measured faster than the fast form up to 120 rows
 constexpr int kDeepSteps = 4;
-// Deep-form launches of at most this many rows merge in the decode kernel. Against the merge
-// launch (same box, per layer): 0.7-1.4 us faster from 1 to 32 rows, even at 48, 1.3-1.6 us slower
-// at 96-120 rows, where the last arrivers' count and coherent reads outlast a separate launch.
-constexpr int kSelfMergeRows = 48;
 
 template <typename T, int D, bool kCoherent = false>
 CDB_DEVICE void merge_chunks(const float* part, int64_t stride, int nsplit, int lane, T* out_row);
 
-// Agent-coherent float accesses: the eight XCDs' L2s do not share dirty lines, and these go to
-// the point where all of them agree (sc1), without writing back or invalidating a whole L2.
-CDB_DEVICE void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Agent-coherent float loads: the eight XCDs' L2s do not share dirty lines, and these read at the
+// point where all of them agree (sc1), without invalidating a whole L2.
 CDB_DEVICE float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One item's partial (D accumulator floats, then the max and the sum): slot 0's values, the ones
+// the merge and the single-chunk output use (the other slots' sums can differ in the last bit,
+// since each lane may fuse its own product into its add). Lane (slot s, chunk q) fetches slot 0's
+// pair 2s of chunk q and writes it as one 8-byte store (elements 8q + 2s and 8q + 2s + 1 at
+// D = 128; the first C/2 slots in general), so a wave's store covers the accumulator contiguously.
+// These are the in-kernel merge's agent-coherent stores: a 4-byte coherent store per float, each
+// written through alone, moved eight times the partial's bytes. For the merge launch, slot 0
+// stores its own values with plain stores, which the L2 combines.
+template <int D>
+CDB_DEVICE void store_partial(const DecodeParams& P, float* part, const float* acc, float m_all, float l, int slot,
+                              int chunk) {
+  constexpr int C = D / 16;
+  static_assert(C % 2 == 0, "pairs of accumulator floats");
+  if (!P.self_merge) {
+    // For the merge launch: plain stores, which the L2 combines, from slot 0 itself.
+    if (slot == 0) {
+#pragma unroll
+      for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
+      if (chunk == 0) {
+        part[D] = m_all;
+        part[D + 1] = l;
+      }
+    }
+    return;
+  }
+  float lo = 0.f, hi = 0.f;
+#pragma unroll
+  for (int k = 0; k < C / 2; ++k) {
+    const float a = __int_as_float(__builtin_amdgcn_ds_bpermute(chunk << 2, __float_as_int(acc[2 * k])));
+    const float b = __int_as_float(__builtin_amdgcn_ds_bpermute(chunk << 2, __float_as_int(acc[2 * k + 1])));
+    lo = slot == k ? a : lo;
+    hi = slot == k ? b : hi;
+  }
+  if (slot < C / 2) {
+    uint64_t* dst = reinterpret_cast<uint64_t*>(part + chunk * C + 2 * slot);
+    const uint64_t pair = (uint64_t)__float_as_uint(lo) | ((uint64_t)__float_as_uint(hi) << 32);
+    __hip_atomic_store(dst, pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (slot == 0 && chunk == 0) {
+    uint64_t* dst = reinterpret_cast<uint64_t*>(part + D);
+    const uint64_t pair = (uint64_t)__float_as_uint(m_all) | ((uint64_t)__float_as_uint(l) << 32);
+    __hip_atomic_store(dst, pair, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // The deep form merges without a launch of its own. Every item of a multi-chunk row stores its
@@ -1288,25 +1326,10 @@ __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams 
 #pragma unroll
         for (int i = 0; i < C; i += 2) o.set_pair(i, acc[i] * inv, acc[i + 1] * inv);
         o.store(out_row + chunk * C);
-      } else if (c.live) {
-        float* part = P.partial + ((int64_t)c.partial * H + c.h) * (D + 2);
-        if (P.self_merge) {
-#pragma unroll
-          for (int i = 0; i < C; ++i) store_coherent(part + chunk * C + i, acc[i]);
-          if (chunk == 0) {
-            store_coherent(part + D, m_all);
-            store_coherent(part + D + 1, l);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
-          if (chunk == 0) {
-            part[D] = m_all;
-            part[D + 1] = l;
-          }
-        }
       }
     }
+    if (!c.single && c.live) store_partial<D>(P, P.partial + ((int64_t)c.partial * H + c.h) * (D + 2), acc, m_all, l,
+                                              slot, chunk);
     if (P.self_merge && !c.single && c.nsplit > 1) finish_row_head<T, D>(P, c, lane);
   }
   if (P.self_merge) fill_chunkless_rows<T, D>(P, wave_id, nwaves, lane);
@@ -1660,7 +1683,10 @@ int decode_attention(const void* q, const void* k_new, const void* v_new, void* 
   P.rope_style = rope_style; P.max_positions = max_positions;
   P.num_cache_layers = num_cache_layers; P.pool_blocks = pool_blocks;
   P.scale_log2 = scale * 1.4426950408889634f;
-  P.self_merge = num_rows <= kSelfMergeRows;
+  // Every deep-form launch merges in the decode kernel. Against the merge launch (same box, per
+  // layer, with the partials' 8-byte coherent stores): 0.1-0.5 us faster from 1 to 16 rows,
+  // 1-2 us from 24 to 120 rows.
+  P.self_merge = num_rows <= kDeepRows;
 
   if (g_num_cus == 0) {
     int dev = 0;

@@ -250,21 +250,24 @@ FAST_FORM_SHAPES = {
 }
 
 
+@pytest.mark.parametrize("rows", [96, 136])
 @pytest.mark.parametrize("shape", sorted(FAST_FORM_SHAPES))
-def test_fast_form_above_120_rows_against_the_oracle(shape: str) -> None:
-    """136 rows (more than the deep form's 120, so the persistent fast form with its XCD tail
-    queues, cross-item prefetch and LDS stash runs) against the float64 oracle, with padding
-    rows, one row past its block table and one row at a cache layer outside the pool: those
-    two get NaN and write nothing, every other row is within the bar and its appended K/V row
-    is bit-identical to the oracle's."""
+def test_wide_launches_against_the_oracle(shape: str, rows: int) -> None:
+    """Against the float64 oracle: 136 rows (more than the deep form's 120, so the persistent fast
+    form with its XCD tail queues, cross-item prefetch, LDS stash and merge launch runs) and 96 rows
+    (the deep form, whose last-arriving waves merge each row's chunks in the decode kernel). Both
+    with padding rows, multi-chunk rows, one row past its block table and one row at a cache layer
+    outside the pool: those two get NaN and write nothing, every other row is within the bar and
+    its appended K/V row is bit-identical to the oracle's. Two calls run on one workspace, so the
+    arrival counters and tail queues the first call leaves must serve the second."""
 
     dtype, heads, kv_heads, dim, rope_style, bias = FAST_FORM_SHAPES[shape]
-    case = make_case(seed=35 + dim, num_rows=136, num_heads=heads, num_kv_heads=kv_heads, head_dim=dim,
+    case = make_case(seed=35 + dim + rows, num_rows=rows, num_heads=heads, num_kv_heads=kv_heads, head_dim=dim,
                      max_context=420, rope_style=rope_style, dtype=dtype, padding_rows=5, qk_bias=bias)
     width = case.block_table.shape[1]
     case.seqlens[7] = width * case.block_size  # one past its table
     case.cache_layer[11] = case.kv_pool.shape[0]  # one past the pool's cache layers
-    got, got_pool = run_hip(case, 0)
+    got, got_pool = run_hip(case, 0, repeats=2)
     assert np.isnan(got[7]).all() and np.isnan(got[11]).all()
     case.seqlens[7] = case.seqlens[11] = -1  # as padding for the oracle: no write, no output
     want, want_pool = run_oracle(case)

@@ -12,7 +12,7 @@
 // with RoPE (ouro/modeling_ouro.py:179-204, huginn/modeling_huginn.py:155-196)
 // folded in.
 //
-// Three kernels on one stream:
+// Kernels on one stream:
 //   * decode_plan_kernel (one workgroup) cuts every row's context into chunks
 //     of a fixed number of pages and lists the chunks longest first: all full
 //     chunks, then the rows' last chunks by decreasing length. Each chunk gets
@@ -20,30 +20,37 @@
 //     the rows' positions, table rows and cache-layer offsets, so a caller that
 //     runs the same rows through several layers plans once and attends per
 //     layer (cdb_paged_decode_attention_staged).
-//   * paged_decode_fast_kernel (16-token pages, 8-page chunks: the engine's
-//     shape) or paged_decode_kernel (any page size and chunk length): a work
-//     item is (chunk, query head) and belongs to one wave; wave w of the
-//     persistent grid takes items w, w + W, w + 2W, ... in the plan's order, so
-//     the longest items go first and every wave ends on short ones. While a
-//     wave streams one item it already holds the next item's descriptor and
-//     loads its query and new token, and the next item's first K/V step is
-//     issued into the buffer the current item's last step frees: after the
-//     first item, little time is spent outside the K/V stream.
-//   * decode_merge_kernel combines the partials of rows with several chunks, in
-//     chunk order, and fills the output of rows without work.
+//   * one decode kernel. A work item is (chunk, query head) and belongs to one
+//     wave of a persistent grid, which takes items in the plan's order, so the
+//     longest items go first and every wave ends on short ones.
+//     - paged_decode_fast_kernel (16-token pages, 8-page chunks: the engine's
+//       shape; more than kDeepRows rows): while a wave streams one item it
+//       already holds the next item's descriptor and loads its query and new
+//       token, and the next item's first K/V step is issued into the buffer the
+//       current item's last step frees; the launch's tail goes to whichever
+//       wave asks first, from its XCD's queue.
+//     - paged_decode_deep_kernel (the same shape, at most kDeepRows rows): each
+//       wave keeps three K/V steps in flight, and the wave that stores a row's
+//       last chunk merges the row (arrival counters, agent-coherent partials).
+//     - paged_decode_kernel: any page size and chunk length.
+//   * decode_merge_kernel (after the fast and general forms) combines the
+//     partials of rows with several chunks, in chunk order, and fills the
+//     output of rows without work.
 // A chunk's tokens, and therefore its partial, do not depend on which other
-// rows share the launch, and the merge order is fixed: a row's output is
-// bit-identical in any batch composition (unless the workspace is too small
-// for the launch's chunks, when the plan lengthens them).
+// rows share the launch, every form computes a chunk the same way, and the
+// merge order is fixed: a row's output is bit-identical in any batch
+// composition (unless the workspace is too small for the launch's chunks, when
+// the plan lengthens them).
 // Inside a wave, lane = 16 * slot + chunk: the 16 lanes of a DPP row split the
 // head dimension into 16-byte chunks and the 4 slots take interleaved tokens,
 // each with its own online-softmax state, merged across slots at the end. A
-// wave step is 16 tokens (4 per slot); two register buffers keep one step in
-// flight while the other is reduced.
+// wave step is 16 tokens (4 per slot).
 //
-// Workspace: int32 header [chunk_tokens, chunk_prefix[0..B]] padded to 256
-// bytes, then int32 descriptors [capacity][8], then fp32 partials
-// [capacity, H, D + 2] (unnormalized accumulator, running max, running sum).
+// Workspace, each part 256-byte aligned: int32 header [chunk_tokens,
+// chunk_prefix[0..B]], the tail queue counters (kQueues lines of 128 bytes),
+// one int32 arrival counter per (row, head); then int32 descriptors
+// [capacity][16], then fp32 partials [capacity, H, D + 2] (unnormalized
+// accumulator, running max, running sum).
 
 #include <algorithm>
 #include <mutex>

@@ -460,9 +460,16 @@ DECODE_SOURCE = "continuous_depth_batching_amd/csrc/paged_decode_attention.hip"
 
 
 def decode_source_sha256() -> str:
-    import hashlib
+    """SHA-256 of the decode source's code: comments, blank lines and trailing spaces removed, so
+    that a record counted on the kernels stays valid across comment edits and no longer."""
 
-    return hashlib.sha256((REPO / DECODE_SOURCE).read_bytes()).hexdigest()
+    import hashlib
+    import re
+
+    text = (REPO / DECODE_SOURCE).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    lines = (re.sub(r"//.*$", "", line).rstrip() for line in text.splitlines())
+    return hashlib.sha256("\n".join(line for line in lines if line).encode()).hexdigest()
 
 
 def measured_traffic(algorithmic_bytes: int) -> int | None:

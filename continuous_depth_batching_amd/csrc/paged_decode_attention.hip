@@ -104,7 +104,6 @@ struct DecodeParams {
   int32_t num_cache_layers;     // valid cache layers are [0, num_cache_layers)
   int64_t pool_blocks;          // valid block ids are [0, pool_blocks)
   int64_t capacity;             // chunks the workspace holds (descriptors and partials)
-  int32_t self_merge;           // deep form: merge and fill in the decode kernel (no merge launch)
   float scale_log2;             // softmax scale * log2(e)
 };
 
@@ -1142,26 +1141,13 @@ CDB_DEVICE float load_coherent(const float* p) {
 // since each lane may fuse its own product into its add). Lane (slot s, chunk q) fetches slot 0's
 // pair 2s of chunk q and writes it as one 8-byte store (elements 8q + 2s and 8q + 2s + 1 at
 // D = 128; the first C/2 slots in general), so a wave's store covers the accumulator contiguously.
-// These are the in-kernel merge's agent-coherent stores: a 4-byte coherent store per float, each
-// written through alone, moved eight times the partial's bytes. For the merge launch, slot 0
-// stores its own values with plain stores, which the L2 combines.
+// The stores are agent-coherent, for the in-kernel merge. They go out as pairs because each
+// coherent store is written through on its own: one 4-byte store per float moved eight times the
+// partial's bytes.
 template <int D>
-CDB_DEVICE void store_partial(const DecodeParams& P, float* part, const float* acc, float m_all, float l, int slot,
-                              int chunk) {
+CDB_DEVICE void store_partial(float* part, const float* acc, float m_all, float l, int slot, int chunk) {
   constexpr int C = D / 16;
   static_assert(C % 2 == 0, "pairs of accumulator floats");
-  if (!P.self_merge) {
-    // For the merge launch: plain stores, which the L2 combines, from slot 0 itself.
-    if (slot == 0) {
-#pragma unroll
-      for (int i = 0; i < C; ++i) part[chunk * C + i] = acc[i];
-      if (chunk == 0) {
-        part[D] = m_all;
-        part[D + 1] = l;
-      }
-    }
-    return;
-  }
   float lo = 0.f, hi = 0.f;
 #pragma unroll
   for (int k = 0; k < C / 2; ++k) {
@@ -1335,11 +1321,11 @@ __global__ void __launch_bounds__(256, 2) paged_decode_deep_kernel(DecodeParams 
         o.store(out_row + chunk * C);
       }
     }
-    if (!c.single && c.live) store_partial<D>(P, P.partial + ((int64_t)c.partial * H + c.h) * (D + 2), acc, m_all, l,
-                                              slot, chunk);
-    if (P.self_merge && !c.single && c.nsplit > 1) finish_row_head<T, D>(P, c, lane);
+    if (!c.single && c.live)
+      store_partial<D>(P.partial + ((int64_t)c.partial * H + c.h) * (D + 2), acc, m_all, l, slot, chunk);
+    if (!c.single && c.nsplit > 1) finish_row_head<T, D>(P, c, lane);
   }
-  if (P.self_merge) fill_chunkless_rows<T, D>(P, wave_id, nwaves, lane);
+  fill_chunkless_rows<T, D>(P, wave_id, nwaves, lane);
 }
 
 // The merge of one (row, head): chunk c's partial (unnormalized accumulator of
@@ -1507,8 +1493,10 @@ int launch_decode(const DecodeParams& P, int stages, int num_cus, hipStream_t st
                  : deep        ? launch_persistent(paged_decode_deep_kernel<T, D, R>, P, num_cus, stream)
                                : launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream);
   if (rc != CDB_OK) return rc;
-  // A self-merging deep launch has merged and filled every row; the others end with the merge launch.
-  if (deep && P.self_merge) return CDB_OK;
+  // A deep launch has merged and filled every row itself (against the merge launch, same box, per
+  // layer, with the partials' 8-byte coherent stores: 0.1-0.5 us faster from 1 to 16 rows, 1-2 us
+  // from 24 to 120 rows); the others end with the merge launch.
+  if (deep) return CDB_OK;
   const int64_t waves = (int64_t)P.num_rows * P.num_heads;
   hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, P);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
@@ -1690,10 +1678,6 @@ int decode_attention(const void* q, const void* k_new, const void* v_new, void* 
   P.rope_style = rope_style; P.max_positions = max_positions;
   P.num_cache_layers = num_cache_layers; P.pool_blocks = pool_blocks;
   P.scale_log2 = scale * 1.4426950408889634f;
-  // Every deep-form launch merges in the decode kernel. Against the merge launch (same box, per
-  // layer, with the partials' 8-byte coherent stores): 0.1-0.5 us faster from 1 to 16 rows,
-  // 1-2 us from 24 to 120 rows.
-  P.self_merge = num_rows <= kDeepRows;
 
   if (g_num_cus == 0) {
     int dev = 0;

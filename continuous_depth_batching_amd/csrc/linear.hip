@@ -225,7 +225,12 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
 //   * x chunks go through LDS, double-buffered, in operand order (16-byte
 //     unit (r, g) of block (row tile, step) holds x[16 t + r][32 s + 8 g ..]);
 //   * workgroups of one column range (different row ranges) sit on one XCD,
-//     so the weights cross HBM once.
+//     so the weights cross HBM once;
+//   * PIPE: x chunks are triple-buffered and stored two chunks ahead, and each
+//     step's x operands are read from LDS while the previous step's MFMAs run
+//     (without it a step's reads wait for the previous step's last MFMA, and
+//     its MFMAs for the reads). Every output still adds its K steps in order
+//     in one accumulator, so the results are bit-identical either way.
 // ---------------------------------------------------------------------------
 // Slot of x unit (row r of a 16-row tile, step t of the chunk, k group g) within
 // its 64-unit block: the MFMA lane that reads it is r + 16 g, with r swizzled by
@@ -245,15 +250,17 @@ CDB_DEVICE int x_slot(int r, int t, int g) {
 // adds them in split order and rounds once (the residual RMSNorm).
 // NTAIL: N is a multiple of 16 but not of 64 * NTW, so the last column range is
 // narrower; without it N must be a multiple of 64 * NTW.
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false>
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false,
+          bool PIPE = false>
 __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   constexpr int NT = GATED ? 2 * NTW : NTW;
   constexpr int ROWS = 16 * MT;
   constexpr int KC = 32 * SC;
   constexpr int UNITS = ROWS * KC / 8;
   static_assert(UNITS % 256 == 0, "x chunk must split evenly over the workgroup");
+  static_assert(!PIPE || STAGES >= 3, "the pipelined form stores x two chunks ahead of its use");
   constexpr int UPT = UNITS / 256;
-  __shared__ bf16x8_t xs[2][MT][SC][kWave];
+  __shared__ bf16x8_t xs[PIPE ? 3 : 2][MT][SC][kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -330,7 +337,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Chunk j's weights live in ring[j % STAGES] and its x in xring[j % STAGES] from STAGES
-  // chunks before it is used; x moves to LDS one chunk ahead of its MFMAs.
+  // chunks before it is used; x moves to LDS one chunk ahead of its MFMAs (two with PIPE).
   bf16x8_t ring[STAGES][NT][SC];
   bf16x8_t xring[STAGES][UPT];
 #pragma unroll
@@ -339,34 +346,87 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
     load_x(st, xring[st]);
   }
   store_x(0, xring[0]);
+  if constexpr (PIPE) {
+    if (nchunks > 1) store_x(1, xring[1]);
+  }
   __syncthreads();
 
+  if constexpr (PIPE) {
+    // Chunk c's x sits in xs[c % 3]. Step (c, t)'s operands are read during step
+    // (c, t - 1) -- or, for t = 0, during chunk c - 1's last step, after the barrier
+    // that ended chunk c - 2 published xs[c % 3]. Chunk c stores chunk c + 2's x into
+    // xs[(c + 2) % 3], whose last reads (chunk c - 1's) all completed before the
+    // barrier that ended chunk c - 1 (the barrier waits for this wave's LDS reads).
+    auto read_b = [&](int c, int t, bf16x8_t (&b)[MT]) {
+      const bool valid = c * SC + t < total;
 #pragma unroll
-  for (int c0 = 0; c0 < nchunks; c0 += STAGES) {
+      for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[c % 3][mt][t][xrd[t]] : bf16x8_t{};
+    };
+    bf16x8_t b[MT];
+    read_b(0, 0, b);
 #pragma unroll
-    for (int st = 0; st < STAGES; ++st) {
-      const int c = c0 + st;
-      if (c < nchunks) {
-        const int cur = c & 1;
-        const bool more = c + 1 < nchunks;
+    for (int c0 = 0; c0 < nchunks; c0 += STAGES) {
 #pragma unroll
-        for (int t = 0; t < SC; ++t) {
-          const bool valid = c * SC + t < total;
-          bf16x8_t b[MT];
+      for (int st = 0; st < STAGES; ++st) {
+        const int c = c0 + st;
+        if (c < nchunks) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[cur][mt][t][xrd[t]] : bf16x8_t{};
+          for (int t = 0; t < SC; ++t) {
+            const bool valid = c * SC + t < total;
+            const bool next = t + 1 < SC || c + 1 < nchunks;
+            bf16x8_t bn[MT];
+            if (t + 1 < SC) read_b(c, t + 1, bn);
+            else if (c + 1 < nchunks) read_b(c + 1, 0, bn);
+            // Keeps the reads above this step's MFMAs: left to itself the scheduler
+            // sinks each read below the last MFMA that uses the register it refills.
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            const bf16x8_t a = valid ? ring[st][nt][t] : bf16x8_t{};
+            for (int nt = 0; nt < NT; ++nt) {
+              const bf16x8_t a = valid ? ring[st][nt][t] : bf16x8_t{};
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-              acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+              for (int mt = 0; mt < MT; ++mt)
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+            }
+            if (next) {
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) b[mt] = bn[mt];
+            }
           }
+          if (c + STAGES < nchunks) load_w(c + STAGES, ring[st]);
+          if (c + 2 < nchunks) store_x((c + 2) % 3, xring[(st + 2) % STAGES]);
+          if (c + STAGES < nchunks) load_x(c + STAGES, xring[st]);
+          lds_barrier();
         }
-        if (c + STAGES < nchunks) load_w(c + STAGES, ring[st]);
-        if (more) store_x(cur ^ 1, xring[(st + 1) % STAGES]);
-        if (c + STAGES < nchunks) load_x(c + STAGES, xring[st]);
-        lds_barrier();
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c0 = 0; c0 < nchunks; c0 += STAGES) {
+#pragma unroll
+      for (int st = 0; st < STAGES; ++st) {
+        const int c = c0 + st;
+        if (c < nchunks) {
+          const int cur = c & 1;
+          const bool more = c + 1 < nchunks;
+#pragma unroll
+          for (int t = 0; t < SC; ++t) {
+            const bool valid = c * SC + t < total;
+            bf16x8_t b[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) b[mt] = valid ? xs[cur][mt][t][xrd[t]] : bf16x8_t{};
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+              const bf16x8_t a = valid ? ring[st][nt][t] : bf16x8_t{};
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[mt], acc[nt][mt], 0, 0, 0);
+            }
+          }
+          if (c + STAGES < nchunks) load_w(c + STAGES, ring[st]);
+          if (more) store_x(cur ^ 1, xring[(st + 1) % STAGES]);
+          if (c + STAGES < nchunks) load_x(c + STAGES, xring[st]);
+          lds_barrier();
+        }
       }
     }
   }
@@ -403,13 +463,14 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
   }
 }
 
-template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false>
+template <int MT, int NTW, int SC, int STAGES, bool GATED, int KSTEPS, int KSPLIT = 1, bool NTAIL = false,
+          bool PIPE = false>
 int launch_linear_wide(LinearParams prm, hipStream_t stream) {
   if ((NTAIL ? prm.N % 16 : prm.N % (64 * NTW)) || prm.K != 32 * KSTEPS * KSPLIT) return CDB_ERR_SHAPE;
   const int n_tiles = NTAIL ? (prm.N / 16 + 4 * NTW - 1) / (4 * NTW) : prm.N / (64 * NTW);  // as the kernel counts
   const int m_tiles = (prm.M + 16 * MT - 1) / (16 * MT);
   const int pairs = n_tiles * KSPLIT;
-  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT, NTAIL>),
+  hipLaunchKernelGGL((linear_wide_kernel<MT, NTW, SC, STAGES, GATED, KSTEPS, KSPLIT, NTAIL, PIPE>),
                      dim3((pairs + 7) / 8 * 8 * m_tiles), dim3(256), 0, stream, prm);
   return hipGetLastError() == hipSuccess ? CDB_OK : CDB_ERR_HIP;
 }
@@ -566,7 +627,9 @@ int dispatch_rows(const LinearParams& prm, bool gated, int max_waves, hipStream_
 
 // Wide-tile path: batches of 33 to 256 rows over 2048-wide inputs with outputs
 // of 4096+ columns (the Ouro-1.4B QKV and gate/up projections). Tiles from a
-// sweep over (row tiles, column tiles, chunk, stages) with cold weights.
+// sweep over (row tiles, column tiles, chunk, stages, pipelined x reads) with
+// cold weights; the pipelined form wins only where a wave has 16 or more MFMAs
+// per step to hide its reads behind (the gated projection above 64 rows).
 bool wide_path(const LinearParams& prm) {
   // 5280-wide inputs (the Huginn QKV and gate/up projections) between 65 and 128 rows.
   if (prm.K == 5280) return prm.M > 64 && prm.M <= 128 && prm.N >= 4096 && prm.N % 16 == 0;
@@ -583,10 +646,10 @@ int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
                  : launch_linear_wide<2, 1, 4, 4, false, 64>(prm, stream);
   }
   if (prm.M <= 128) {
-    return gated ? launch_linear_wide<4, 1, 2, 4, true, 64>(prm, stream)
+    return gated ? launch_linear_wide<4, 1, 2, 4, true, 64, 1, false, true>(prm, stream)
                  : launch_linear_wide<4, 1, 2, 4, false, 64>(prm, stream);
   }
-  return gated ? launch_linear_wide<8, 1, 2, 4, true, 64>(prm, stream)
+  return gated ? launch_linear_wide<8, 1, 2, 4, true, 64, 1, false, true>(prm, stream)
                : launch_linear_wide<4, 2, 2, 4, false, 64>(prm, stream);
 }
 
@@ -621,7 +684,8 @@ int dispatch_parts(const LinearParams& prm, hipStream_t stream) {
   if (prm.K == 5632) {
     if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 44, 4>(prm, stream);
     if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 44, 4>(prm, stream);
-    return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
+    if (prm.M <= 128) return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);
+    return launch_linear_wide<8, 1, 2, 4, false, 44, 4, false, true>(prm, stream);  // two row ranges, pipelined
   }
   if (prm.K == 5280) {
     if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 55, 3, true>(prm, stream);

@@ -191,6 +191,35 @@ def test_split_k_partials_sum_to_the_fp32_product(rows: int, k: int, n: int) -> 
     _check_rounded(total.bfloat16(), x.float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x, w))
 
 
+def test_wide_tile_forms_give_a_row_the_same_bits_in_any_batch() -> None:
+    """Every wide-tile form adds an output's K steps in order in one accumulator, so a
+    row's result does not depend on its batch: 48 rows (two-tile row ranges), 100 rows
+    (four-tile; the gated one reads x ahead of its MFMAs) and 256 rows (eight-tile gated
+    and down forms, both reading x ahead) agree bit for bit, for the gated projection and
+    for the split-K partials. A dropped, repeated or reordered K step in one form fails."""
+
+    from continuous_depth_batching_amd import ops
+
+    x, w = _inputs(256, 2048, 2 * 5632, seed=31)
+    packed = ops.pack_linear_weight(w)
+    xd, wd = _inputs(256, 5632, 2048, seed=37)
+    packed_d = ops.pack_linear_weight(wd)
+    gated, parts = {}, {}
+    for rows in (48, 100, 256):
+        gated[rows] = torch.empty((rows, 5632), dtype=torch.bfloat16, device="cuda")
+        ops.linear_raw(x[:rows], packed, gated[rows], gated=True)
+        parts[rows] = torch.full((ops.linear_parts_splits(rows, 2048, 5632), rows, 2048), float("nan"), device="cuda")
+        ops.linear_parts_raw(xd[:rows], packed_d, parts[rows])
+    torch.cuda.synchronize()
+    assert torch.equal(gated[256][:100], gated[100]) and torch.equal(gated[100][:48], gated[48])
+    assert parts[48].shape[0] == parts[256].shape[0] == 4
+    assert torch.equal(parts[256][:, :100], parts[100]) and torch.equal(parts[100][:, :48], parts[48])
+    gu = (x[:256].float() @ w.float().t()).bfloat16().float()
+    g, u = gu[:, :5632], gu[:, 5632:]
+    ref = (g * torch.sigmoid(g)).bfloat16().float() * u
+    assert ((gated[256].float() - ref).abs() <= 2 * _bf16_ulp(ref) + 1e-3).float().mean().item() >= 0.99
+
+
 @pytest.mark.parametrize("rows,k,n", [(1, 2048, 2048), (16, 5632, 2048), (33, 2048, 2048), (96, 5632, 2048),
                                       (128, 2048, 2048), (256, 5632, 2048), (7, 5280, 5280), (128, 17920, 5280)])
 def test_norm_from_partials_is_the_two_step_result(rows: int, k: int, n: int) -> None:

@@ -35,6 +35,13 @@ CDB_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
 // Round an fp32 value to the nearest bf16 and return it as fp32.
 CDB_DEVICE float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// SiLU of a bf16 value x, rounded to bf16: R(x / (1 + e^-x)) with e^-x from the
+// hardware exponential and the IEEE division. For every one of the 65536 bf16
+// inputs this gives the same bits as the libm expf form and as torch's bf16 SiLU
+// (NaN inputs give NaN), which a GPU test checks input by input; so it is only
+// for x that is itself a bf16 value.
+CDB_DEVICE float silu_bf16(float x) { return round_bf16(x / (1.0f + __expf(-x))); }
+
 // Element traits: load/store one scalar of the storage type as fp32.
 template <typename T> struct Elem;
 template <> struct Elem<float> {

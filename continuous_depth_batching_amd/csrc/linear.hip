@@ -64,6 +64,24 @@ CDB_DEVICE bf16x8_t load_w(const bf16_t* p) {
 }
 CDB_DEVICE bf16x8_t load_x(const bf16_t* p) { return *reinterpret_cast<const bf16x8_t*>(p); }
 
+// Sum of partial tile `tile` over the first `slots` LDS slots, added in slot order.
+// Every slot is read up front so the reads overlap instead of each waiting for the
+// previous add; slots past `slots` are read and not used (a select, not an add of
+// zero, so a -0 sum keeps its sign).
+template <int SLOTS, int NT, int MT>
+CDB_DEVICE f32x4_t sum_slots(const f32x4_t (&red)[SLOTS][NT][MT][kWave], int tile, int mt, int l, int slots) {
+  f32x4_t part[SLOTS];
+#pragma unroll
+  for (int sl = 0; sl < SLOTS; ++sl) part[sl] = red[sl][tile][mt][l];
+  f32x4_t v = part[0];
+#pragma unroll
+  for (int sl = 1; sl < SLOTS; ++sl) {
+    const f32x4_t w = v + part[sl];
+    v = sl < slots ? w : v;
+  }
+  return v;
+}
+
 // MT: 16-row tiles of x (1, 2 or 4). NB: 16-column tiles of y per workgroup; every
 // wave computes all of them, so each x vector it loads feeds NB (gated: 2*NB)
 // MFMAs. S: contraction steps loaded per batch. SLOTS: LDS partial tiles (waves
@@ -161,8 +179,7 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
       const int mt = (idx / kWave) % MT;
       const int l = idx & (kWave - 1);
       const int m = mt * 16 + (l & 15);
-      f32x4_t v = red[0][j][mt][l];
-      for (int sl = 1; sl < slots; ++sl) v += red[sl][j][mt][l];
+      const f32x4_t v = sum_slots(red, j, mt, l, slots);
       const int c0 = n0 + 16 * j + 4 * (l >> 4);
       float best = -INFINITY;
       int bi = 0x7fffffff;
@@ -193,18 +210,15 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
     const int l = idx & (kWave - 1);
     const int m = mt * 16 + (l & 15);
     if (m < p.M) {
-      f32x4_t v = red[0][j][mt][l], u = {};
-      for (int sl = 1; sl < slots; ++sl) v += red[sl][j][mt][l];
-      if constexpr (GATED) {
-        u = red[0][NB + j][mt][l];
-        for (int sl = 1; sl < slots; ++sl) u += red[sl][NB + j][mt][l];
-      }
+      const f32x4_t v = sum_slots(red, j, mt, l, slots);
+      f32x4_t u = {};
+      if constexpr (GATED) u = sum_slots(red, NB + j, mt, l, slots);
       Vec<bf16_t, 4> o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if constexpr (GATED) {
           const float gate = round_bf16(v[i]);
-          const float act = round_bf16(gate / (1.0f + expf(-gate)));
+          const float act = silu_bf16(gate);
           o.set(i, act * round_bf16(u[i]));
         } else {
           o.set(i, v[i]);
@@ -452,7 +466,7 @@ __global__ void __launch_bounds__(256) linear_wide_kernel(LinearParams p) {
       for (int i = 0; i < 4; ++i) {
         if constexpr (GATED) {
           const float gate = round_bf16(acc[j][mt][i]);
-          const float act = round_bf16(gate / (1.0f + expf(-gate)));
+          const float act = silu_bf16(gate);
           o.set(i, act * round_bf16(acc[NTW + j][mt][i]));
         } else {
           o.set(i, acc[j][mt][i]);

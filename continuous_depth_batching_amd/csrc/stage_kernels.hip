@@ -211,7 +211,9 @@ __global__ void __launch_bounds__(kThreads) silu_mul_kernel(const T* gu, T* out,
 #pragma unroll
     for (int i = 0; i < V; ++i) {
       const float x = g.get(i);
-      const float s = Elem<T>::round(x / (1.0f + expf(-x)));
+      float s;
+      if constexpr (sizeof(T) == 2) s = silu_bf16(x);  // x is a bf16 value
+      else s = x / (1.0f + expf(-x));
       o.set(i, Elem<T>::round(mul_rn(s, u.get(i))));
     }
     o.store(out + row * width + col);

@@ -9,6 +9,7 @@ product rounded.
 
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -105,6 +106,38 @@ def test_gated_linear_follows_bf16_silu_chain(rows: int, k: int, f: int) -> None
     ops.silu_mul_raw(torch.mm(x, w.t()), unfused)
     torch.cuda.synchronize()
     assert ((y.float() - unfused.float()).abs() <= 2 * _bf16_ulp(ref) + 1e-6).float().mean().item() >= 0.98
+
+
+@pytest.mark.parametrize("rows", [16, 100, 256])
+def test_fused_silu_gives_torch_bits_for_every_normal_bf16_gate(rows: int) -> None:
+    """One-hot x rows pick single weights, so every gate accumulator is exactly one bf16
+    weight and every up value exactly 1, and each output is the SiLU of that bf16 value
+    alone. Across the batch every finite normal bf16 value (and +0) is a gate once; each
+    output must equal torch's bf16 SiLU bit for bit (the row kernel at 16 rows, the
+    pipelined wide-tile forms at 100 and 256)."""
+
+    from continuous_depth_batching_amd import ops
+
+    f, k = 5632, 2048
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    exponent = (bits >> 7) & 0xFF
+    values = bits[(exponent != 0) & (exponent != 0xFF)]   # finite normal values of both signs
+    values = np.concatenate([[np.uint16(0)], values])      # and +0
+    assert len(values) <= rows * f
+    gates = np.zeros(rows * f, dtype=np.uint16)
+    gates[:len(values)] = values
+    gate = torch.from_numpy(gates.view(np.int16)).view(torch.bfloat16).reshape(rows, f).cuda()
+    w = torch.zeros((2 * f, k), dtype=torch.bfloat16, device="cuda")
+    w[:f, :rows] = gate.t()                                # w_gate[n, r] = gate[r, n]
+    w[f:, :rows] = 1.0                                     # w_up[n, r] = 1
+    x = torch.zeros((rows, k), dtype=torch.bfloat16, device="cuda")
+    x[torch.arange(rows), torch.arange(rows)] = 1.0        # x[r] = e_r
+    y = torch.empty((rows, f), dtype=torch.bfloat16, device="cuda")
+    ops.linear_raw(x, ops.pack_linear_weight(w), y, gated=True)
+    want = torch.nn.functional.silu(gate)
+    torch.cuda.synchronize()
+    differ = y.view(torch.int16) != want.view(torch.int16)
+    assert not bool(differ.any()), f"{int(differ.sum())} gates differ, e.g. {gate[differ][:4].tolist()}"
 
 
 def test_linear_strided_operands_and_determinism() -> None:

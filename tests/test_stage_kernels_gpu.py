@@ -74,6 +74,23 @@ def test_silu_mul(dtype: str) -> None:
         assert np.mean(got == want) >= 0.99
 
 
+def test_silu_mul_bf16_is_torch_silu_on_every_input() -> None:
+    """The bf16 SiLU (hardware exponential, IEEE division) on all 65536 bf16 bit
+    patterns, each times an up value of 1: the same bits as torch's own bf16 SiLU for
+    every input, NaN where torch gives NaN (the NaN inputs, and -inf: -inf / inf)."""
+
+    g = torch.from_numpy(np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.int16))
+    g = g.view(torch.bfloat16).reshape(64, 1024).cuda()
+    out = torch.ops.cdb.silu_mul(torch.cat([g, torch.ones_like(g)], dim=1))
+    want = torch.nn.functional.silu(g)
+    torch.cuda.synchronize()
+    same = out.view(torch.int16) == want.view(torch.int16)
+    nan = torch.isnan(out) & torch.isnan(want)
+    assert bool((same | nan).all()), f"{int((~(same | nan)).sum())} inputs differ"
+    assert bool((torch.isnan(out) == torch.isnan(want)).all())
+    assert int(torch.isnan(out).sum()) == 254 + 1
+
+
 def test_copy_rows_gather_scatter_and_token_gather() -> None:
     from continuous_depth_batching_amd import ops
 

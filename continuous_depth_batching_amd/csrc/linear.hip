@@ -124,18 +124,20 @@ __global__ void __launch_bounds__(MAXT) linear_kernel(LinearParams p) {
   for (int s = s_begin; s < s_end; s += S) {
     // Straight-line batch of S steps: steps past the wave's range (only in the last
     // wave's last batch) reload its last step in bounds and contribute a zero W tile.
+    // x first: loads complete in issue order, so the first MFMA then waits only for
+    // the batch's x (an L2 hit) and its own weight block, not for every weight block.
     bf16x8_t wv[NT][S], xv[MT][S];
-#pragma unroll
-    for (int t = 0; t < S; ++t) {
-      const int64_t blk = (int64_t)min(s + t, s_end - 1) * 512;
-#pragma unroll
-      for (int nt = 0; nt < NT; ++nt) wv[nt][t] = load_w(wrow[nt] + blk);
-    }
 #pragma unroll
     for (int t = 0; t < S; ++t) {
       const int64_t k = (int64_t)min(s + t, s_end - 1) * 32;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) xv[mt][t] = load_x(xrow[mt] + k);
+    }
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      const int64_t blk = (int64_t)min(s + t, s_end - 1) * 512;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) wv[nt][t] = load_w(wrow[nt] + blk);
     }
     // Keep the whole batch of loads in flight before the first MFMA waits on one.
     __builtin_amdgcn_sched_barrier(0);

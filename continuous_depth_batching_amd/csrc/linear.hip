@@ -674,13 +674,15 @@ int dispatch_wide(const LinearParams& prm, bool gated, hipStream_t stream) {
 // counts and tiles from a sweep with cold weights, timed together with the
 // residual RMSNorm that adds the partials: four ranges up to 64 rows; above,
 // two for the 2048-wide input (whose partials would cost more than the
-// parallelism buys) up to 128 rows, four for the 5632-wide one up to 256.
+// parallelism buys) up to 128 rows, four for the 5632-wide one up to 256. The
+// 5632-wide input takes eight ranges up to 16 rows: 2048 outputs are 32 column
+// ranges, so eight ranges fill 256 CUs where four leave half of them idle.
 // Returns 0 for shapes without a split form.
 int parts_splits(int64_t rows, int32_t out_features, int32_t in_features) {
   if (rows < 1 || rows > kLinearWideMaxRows || out_features < 64 || out_features % 16) return 0;
   if (out_features % 64 == 0) {
     if (in_features == 2048) return rows <= 64 ? 4 : rows <= 128 ? 2 : 0;
-    if (in_features == 5632) return 4;
+    if (in_features == 5632) return rows <= 16 ? 8 : 4;
   }
   // The Huginn O (5280 -> 5280) and down (17920 -> 5280) projections: 5280 columns are
   // 82.5 column ranges of 64, so the last range is half full. Split counts from the same
@@ -698,6 +700,7 @@ int dispatch_parts(const LinearParams& prm, hipStream_t stream) {
     return launch_linear_wide<2, 1, 4, 4, false, 32, 2>(prm, stream);
   }
   if (prm.K == 5632) {
+    if (prm.M <= 16) return launch_linear_wide<1, 1, 4, 4, false, 22, 8>(prm, stream);
     if (prm.M <= 32) return launch_linear_wide<1, 1, 4, 4, false, 44, 4>(prm, stream);
     if (prm.M <= 64) return launch_linear_wide<2, 1, 4, 4, false, 44, 4>(prm, stream);
     if (prm.M <= 128) return launch_linear_wide<4, 1, 2, 4, false, 44, 4>(prm, stream);

@@ -227,7 +227,7 @@ def test_split_k_table_without_gpu() -> None:
     bf16 = _lib.CDB_DTYPE_BF16
     cases = {
         (16, 2048, 2048): 4, (64, 2048, 2048): 4, (128, 2048, 2048): 2, (129, 2048, 2048): 0,
-        (1, 2048, 5632): 4, (256, 2048, 5632): 4, (257, 2048, 5632): 0,
+        (1, 2048, 5632): 8, (16, 2048, 5632): 8, (17, 2048, 5632): 4, (256, 2048, 5632): 4, (257, 2048, 5632): 0,
         (16, 5280, 5280): 3, (128, 5280, 5280): 3, (256, 5280, 5280): 3,
         (16, 5280, 17920): 8, (64, 5280, 17920): 8, (65, 5280, 17920): 4, (128, 5280, 17920): 4,
         (64, 2040, 2048): 0,   # out_features not a multiple of 16

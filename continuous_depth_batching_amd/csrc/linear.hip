@@ -66,13 +66,13 @@ CDB_DEVICE bf16x8_t load_x(const bf16_t* p) { return *reinterpret_cast<const bf1
 
 // Sum of partial tile `tile` over the first `slots` LDS slots, added in slot order.
 // Every slot is read up front so the reads overlap instead of each waiting for the
-// previous add; slots past `slots` are read and not used (a select, not an add of
-// zero, so a -0 sum keeps its sign).
+// previous add. Past `slots` the last written slot is read again and not used (a
+// select, not an add of zero, so a -0 sum keeps its sign).
 template <int SLOTS, int NT, int MT>
 CDB_DEVICE f32x4_t sum_slots(const f32x4_t (&red)[SLOTS][NT][MT][kWave], int tile, int mt, int l, int slots) {
   f32x4_t part[SLOTS];
 #pragma unroll
-  for (int sl = 0; sl < SLOTS; ++sl) part[sl] = red[sl][tile][mt][l];
+  for (int sl = 0; sl < SLOTS; ++sl) part[sl] = red[min(sl, slots - 1)][tile][mt][l];
   f32x4_t v = part[0];
 #pragma unroll
   for (int sl = 1; sl < SLOTS; ++sl) {

@@ -79,7 +79,7 @@ def test_wide_tile_path_matches_rounded_fp32_product(rows: int, k: int, n: int) 
     _check_rounded(y, x.float() @ w.float().t(), max_mismatch=0.01, extra=_sum_error(x, w))
 
 
-@pytest.mark.parametrize("rows", [1, 16, 20, 48, 64, 65, 100, 128, 256])
+@pytest.mark.parametrize("rows", [1, 16, 20, 48, 64, 65, 100, 128, 129, 200, 256])
 @pytest.mark.parametrize("k,f", [(2048, 5632), (5280, 17920), (64, 16)])
 def test_gated_linear_follows_bf16_silu_chain(rows: int, k: int, f: int) -> None:
     from continuous_depth_batching_amd import ops

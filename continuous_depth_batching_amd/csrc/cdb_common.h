@@ -82,6 +82,29 @@ template <typename T, int N> struct Vec {
       for (int i = 0; i < kWords; ++i) w[i] = src[i];
     }
   }
+  // The same loads with the nontemporal hint: for data read once and streamed, so it
+  // displaces less of what the caches hold.
+  CDB_DEVICE void load_nt(const T* p) {
+    typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2_nt __attribute__((ext_vector_type(2)));
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p);
+    if constexpr (kWords % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 4) {
+        const u32x4_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_nt*>(src + i));
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+      }
+    } else if constexpr (kWords % 2 == 0) {
+#pragma unroll
+      for (int i = 0; i < kWords; i += 2) {
+        const u32x2_nt v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_nt*>(src + i));
+        w[i] = v.x; w[i + 1] = v.y;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWords; ++i) w[i] = __builtin_nontemporal_load(src + i);
+    }
+  }
   CDB_DEVICE void store(T* p) const {
     uint32_t* dst = reinterpret_cast<uint32_t*>(p);
     if constexpr (kWords % 4 == 0) {

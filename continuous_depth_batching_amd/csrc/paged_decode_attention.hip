@@ -891,7 +891,9 @@ CDB_DEVICE FastItem make_fast_item(const DecodeParams& P, const RawFastDesc& r, 
 // Wave step s (16 tokens of page s of the chunk) of K and V. The lane's byte
 // offsets inside a page, one per token u, are loop-invariant; a masked page
 // reads page 0 of the layer (any valid address) and every token of a masked
-// page or at/after t_end gets zero weight.
+// page or at/after t_end gets zero weight. The pages are read once per layer,
+// so the loads carry the nontemporal hint (launches of up to 120 rows measured
+// 4-7% faster with it, larger ones unchanged).
 template <typename T, int D>
 CDB_DEVICE void load_fast_step(const DecodeParams& P, const FastItem& f, int s, const uint32_t (&lane_off)[4],
                                int slot, Vec<T, D / 16> (&kv)[4], Vec<T, D / 16> (&vv)[4], bool (&valid)[4]) {
@@ -903,8 +905,8 @@ CDB_DEVICE void load_fast_step(const DecodeParams& P, const FastItem& f, int s, 
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     valid[u] = blk >= 0 && t0 + 4 * u + slot < f.it.t_end;
-    kv[u].load(reinterpret_cast<const T*>(kp + lane_off[u]));
-    vv[u].load(reinterpret_cast<const T*>(vp + lane_off[u]));
+    kv[u].load_nt(reinterpret_cast<const T*>(kp + lane_off[u]));
+    vv[u].load_nt(reinterpret_cast<const T*>(vp + lane_off[u]));
   }
 }
 

@@ -65,8 +65,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-sample-tokens", type=int, default=160)
     p.add_argument("--attention-iters", type=int, default=20)
     p.add_argument("--attention-rows", type=int, default=256,
-                   help="decode-attention: time the first N rows of the 256-row shape (at most 120 rows run "
-                        "the deep form, which merges in the decode kernel); the bench line keeps 256")
+                   help="decode-attention: time the first N rows of the 256-row shape (up to 256 rows of "
+                        "128-wide heads run the deep form, which merges in the decode kernel); the bench "
+                        "line keeps 256")
     return p.parse_args()
 
 
@@ -446,9 +447,9 @@ def time_companion_kernels(rows: int = 1024, hidden: int = 2048, prefill_tokens:
 
 def decode_kernels(rows: int) -> str:
     """The kernels one attend call runs at ``rows`` rows of 16-token pages (the decode library's
-    form choice: the deep form, which merges in the decode kernel, up to 120 rows)."""
+    form choice at 128-wide heads: the deep form, which merges in the decode kernel, up to 256 rows)."""
 
-    if rows <= 120:
+    if rows <= 256:
         return "cdb::paged_decode_deep_kernel<bf16,128> (merge in the kernel)"
     return "cdb::paged_decode_fast_kernel<bf16,128> + decode_merge_kernel"
 

@@ -24,12 +24,12 @@
 //     wave of a persistent grid, which takes items in the plan's order, so the
 //     longest items go first and every wave ends on short ones.
 //     - paged_decode_fast_kernel (16-token pages, 8-page chunks: the engine's
-//       shape; more than kDeepRows rows): while a wave streams one item it
+//       shape; more than kDeepRowsOf<D> rows): while a wave streams one item it
 //       already holds the next item's descriptor and loads its query and new
 //       token, and the next item's first K/V step is issued into the buffer the
 //       current item's last step frees; the launch's tail goes to whichever
 //       wave asks first, from its XCD's queue.
-//     - paged_decode_deep_kernel (the same shape, at most kDeepRows rows): each
+//     - paged_decode_deep_kernel (the same shape, at most kDeepRowsOf<D> rows): each
 //       wave keeps three K/V steps in flight, and the wave that stores a row's
 //       last chunk merges the row (arrival counters, agent-coherent partials).
 //     - paged_decode_kernel: any page size and chunk length.
@@ -892,8 +892,8 @@ CDB_DEVICE FastItem make_fast_item(const DecodeParams& P, const RawFastDesc& r, 
 // offsets inside a page, one per token u, are loop-invariant; a masked page
 // reads page 0 of the layer (any valid address) and every token of a masked
 // page or at/after t_end gets zero weight. The pages are read once per layer,
-// so the loads carry the nontemporal hint (launches of up to 120 rows measured
-// 4-7% faster with it, larger ones unchanged).
+// so the loads carry the nontemporal hint (the deep form measured 4-7% faster
+// with it, the persistent form 1-2%, and the headline decode run 3%).
 template <typename T, int D>
 CDB_DEVICE void load_fast_step(const DecodeParams& P, const FastItem& f, int s, const uint32_t (&lane_off)[4],
                                int slot, Vec<T, D / 16> (&kv)[4], Vec<T, D / 16> (&vv)[4], bool (&valid)[4]) {
@@ -1120,13 +1120,17 @@ __global__ void __launch_bounds__(256, 3) paged_decode_fast_kernel(DecodeParams 
   }
 }
 
-// The fast form for small launches (at most kDeepRows rows): such a launch
-// gives a wave one to four items, so latency matters more than occupancy. Each wave keeps kDeepSteps - 1 steps of K/V in
+// The fast form for launches of up to kDeepRowsOf<D> rows: such a launch gives a
+// wave a few items, so latency matters more than occupancy. Each wave keeps kDeepSteps - 1 steps of K/V in
 // flight (four register buffers, 2 waves per SIMD) instead of one, and takes
 // its items without cross-item prefetch. A chunk is computed exactly as in
 // paged_decode_fast_kernel (same steps in the same order, same masking, same
 // new-token and slot merge), so a row's result does not depend on the form.
-constexpr int kDeepRows = 120;  // the deep form measured faster than the fast form up to 120 rows
+// The limit is where the deep form stops measuring faster than the persistent
+// one: 256 rows for 128-wide heads (with the nontemporal K/V loads, 4-8% faster
+// from 128 to 256 rows, no merge launch; 120 rows before them), 120 rows for the
+// other head sizes, where it was measured with cached loads.
+template <int D> constexpr int kDeepRowsOf = D == 128 ? 256 : 120;
 constexpr int kDeepSteps = 4;
 
 template <typename T, int D, bool kCoherent = false>
@@ -1490,7 +1494,7 @@ int launch_decode(const DecodeParams& P, int stages, int num_cus, hipStream_t st
     if (hipGetLastError() != hipSuccess) return CDB_ERR_HIP;
   }
   if (!(stages & CDB_DECODE_STAGE_ATTEND)) return CDB_OK;
-  const bool deep = fast_form(P) && P.num_rows <= kDeepRows;
+  const bool deep = fast_form(P) && P.num_rows <= kDeepRowsOf<D>;
   const int rc = !fast_form(P) ? launch_persistent(paged_decode_kernel<T, D, R>, P, num_cus, stream)
                  : deep        ? launch_persistent(paged_decode_deep_kernel<T, D, R>, P, num_cus, stream)
                                : launch_persistent(paged_decode_fast_kernel<T, D, R>, P, num_cus, stream);

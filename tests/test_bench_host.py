@@ -27,8 +27,8 @@ def test_traffic_record_applies_to_the_current_decode_code_only(monkeypatch, tmp
     src.write_text("// a note\n" + code.replace("\n", "  \n\n") + "\n/* another\n note */\n")
     assert bench.measured_traffic(alg) == record["traffic_bytes_per_call"]
     # Any change of code does.
-    src.write_text(code.replace("constexpr int kDeepRows = 120;", "constexpr int kDeepRows = 121;"))
-    assert "kDeepRows = 121" in src.read_text()
+    src.write_text(code.replace("kDeepRowsOf = D == 128 ? 256 : 120;", "kDeepRowsOf = D == 128 ? 255 : 120;"))
+    assert "? 255 : 120;" in src.read_text()
     assert bench.measured_traffic(alg) is None
 
 

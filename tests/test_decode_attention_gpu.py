@@ -207,14 +207,15 @@ def _attend(case, d, ws, rows, cache_layer0=0, stages=None):
 def test_row_output_is_bit_identical_in_any_batch_composition() -> None:
     # A row's chunks and their merge order depend only on the row: alone, inside the
     # full batch, or inside a shuffled half of it, its output is the same to the bit.
-    # 160 rows run the persistent fast form and the merge launch; 80 rows the deep form and
-    # the merge launch; 30 rows and single rows the deep form merging in the decode kernel.
-    case = make_case(seed=31, num_rows=160, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1500,
+    # 272 rows run the persistent fast form and the merge launch (more than the deep form's
+    # 256 rows at 128-wide heads); 136 rows, 30 rows and single rows the deep form, which
+    # merges in the decode kernel.
+    case = make_case(seed=31, num_rows=272, num_heads=16, num_kv_heads=16, head_dim=128, max_context=1500,
                      rope_style=1, dtype="bf16", padding_rows=3)
     d, ws = _device_case(case)
-    full = _attend(case, d, ws, list(range(160)))
+    full = _attend(case, d, ws, list(range(272)))
     rng = np.random.default_rng(3)
-    half = rng.permutation(160)[:80].tolist()
+    half = rng.permutation(272)[:136].tolist()
     sub = _attend(case, d, ws, half)
     few = _attend(case, d, ws, half[:30])
     torch.cuda.synchronize()
@@ -250,12 +251,13 @@ FAST_FORM_SHAPES = {
 }
 
 
-@pytest.mark.parametrize("rows", [96, 136])
+@pytest.mark.parametrize("rows", [96, 272])
 @pytest.mark.parametrize("shape", sorted(FAST_FORM_SHAPES))
 def test_wide_launches_against_the_oracle(shape: str, rows: int) -> None:
-    """Against the float64 oracle: 136 rows (more than the deep form's 120, so the persistent fast
-    form with its XCD tail queues, cross-item prefetch, LDS stash and merge launch runs) and 96 rows
-    (the deep form, whose last-arriving waves merge each row's chunks in the decode kernel). Both
+    """Against the float64 oracle: 272 rows (more than the deep form's limit, 256 rows at 128-wide
+    heads and 120 at the others, so the persistent fast form with its XCD tail queues, cross-item
+    prefetch, LDS stash and merge launch runs) and 96 rows (the deep form, whose last-arriving waves
+    merge each row's chunks in the decode kernel). Both
     with padding rows, multi-chunk rows, one row past its block table and one row at a cache layer
     outside the pool: those two get NaN and write nothing, every other row is within the bar and
     its appended K/V row is bit-identical to the oracle's. Two calls run on one workspace, so the

@@ -90,7 +90,7 @@ def run_probed(model, prompts, mnt, depths, tracked: list[int], refill: bool):
     torch.cuda.synchronize()
     del engine
     torch.cuda.empty_cache()
-    assert max(widths) > 120, "tracked rows must run in launches of the persistent decode form"
+    assert max(widths) > 120, "tracked rows must also run in wide launches (more than 120 rows)"
     return [o.generated_tokens for o in outs], probe
 
 
